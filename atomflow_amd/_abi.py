@@ -1,0 +1,110 @@
+"""ctypes prototypes of libatomflow_kv.so (include/af_kv.h, include/af_runtime.h)."""
+import ctypes
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+F = ctypes.c_float
+SZ = ctypes.c_size_t
+PI32 = ctypes.POINTER(ctypes.c_int32)
+PI64 = ctypes.POINTER(ctypes.c_int64)
+
+
+class KvPool(ctypes.Structure):
+    """af_kv_pool (include/af_kv.h)."""
+
+    _fields_ = [
+        ("base", P),
+        ("scales", P),
+        ("dtype", I32),
+        ("block_size", I32),
+        ("n_layers", I32),
+        ("n_kv_heads", I32),
+        ("head_dim", I32),
+        ("reserved", I32),
+        ("total_blocks", I64),
+    ]
+
+
+PPOOL = ctypes.POINTER(KvPool)
+
+PROTOTYPES = {
+    # af_kv.h
+    "af_status_string": (ctypes.c_char_p, [I]),
+    "af_version": (I, []),
+    "af_rope_table_build": (I, [P, P, I, I, F, P]),
+    "af_rope_table_host": (I, [P, P, I, I, F]),
+    "af_rope": (I, [P, P, P, P, I, I, I, I, P]),
+    "af_write_kv_cache": (I, [P, P, P, I, I, I, I, P]),
+    "af_rope_append": (I, [P, P, P, P, P, I, P, I, I, I, I, P, P]),
+    "af_cached_attention": (I, [P, P, P, P, I, I, I, I, P]),
+    "af_attention_reserve": (I, [I, I, I, I]),
+    "af_attention_workspace_size": (SZ, [I, I, I, I, I]),
+    "af_attention_workspace_init": (I, [P, SZ, P]),
+    "af_attention_default_splits": (I, [I, I, I]),
+    "af_cached_attention_ex": (I, [P, P, P, P, I, P, I, I, I, I, I, P, SZ, P]),
+    "af_kv_pool_bytes": (SZ, [PPOOL]),
+    "af_paged_rope_append": (I, [P, I, PPOOL, I, P, P, P, P, I, I, P]),
+    "af_paged_attention": (I, [P, I, PPOOL, I, P, I, P, I, I, P, I, I, I, P, SZ, P]),
+    "af_paged_gather": (I, [PPOOL, I, P, I, P, P, P]),
+    "af_kv_copy_blocks": (I, [PPOOL, P, P, I, P]),
+    "af_fp8_quantize": (I, [P, P, SZ, F, P]),
+    "af_bm_create": (I, [I, I, I, I, I, I, I, ctypes.POINTER(P)]),
+    "af_bm_destroy": (I, [P]),
+    "af_bm_attach_pool": (I, [P, P, P]),
+    "af_bm_pool": (I, [P, PPOOL]),
+    "af_bm_allocate_block": (I, [P]),
+    "af_bm_free_block": (I, [P, I]),
+    "af_bm_num_free_blocks": (I, [P]),
+    "af_bm_ref_count": (I, [P, I]),
+    "af_bm_seq_create": (I, [P]),
+    "af_bm_seq_fork": (I, [P, I]),
+    "af_bm_seq_free": (I, [P, I]),
+    "af_bm_seq_len": (I, [P, I]),
+    "af_bm_seq_table": (I, [P, I, PI32, I, PI32]),
+    "af_bm_seq_append": (I, [P, I, PI64, PI32, PI32, PI32]),
+    "af_bm_seq_extend": (I, [P, I, I, PI32, PI32, PI32]),
+    "af_bm_seq_slot": (I64, [P, I, I]),
+    "af_bm_plan_decode": (I, [P, P, I, P, P, P, I, PI32]),
+    "af_bm_export_tables": (I, [P, P, I, P, I, P]),
+    # af_runtime.h
+    "af_rt_device_count": (I, [ctypes.POINTER(I)]),
+    "af_rt_set_device": (I, [I]),
+    "af_rt_device_info": (I, [ctypes.c_char_p, I, ctypes.POINTER(I), ctypes.c_char_p, I]),
+    "af_rt_device_sync": (I, []),
+    "af_rt_last_error": (I, []),
+    "af_rt_malloc": (I, [ctypes.POINTER(P), SZ]),
+    "af_rt_free": (I, [P]),
+    "af_rt_host_malloc": (I, [ctypes.POINTER(P), SZ]),
+    "af_rt_host_free": (I, [P]),
+    "af_rt_mem_info": (I, [ctypes.POINTER(SZ), ctypes.POINTER(SZ)]),
+    "af_rt_memcpy_h2d": (I, [P, P, SZ, P]),
+    "af_rt_memcpy_d2h": (I, [P, P, SZ, P]),
+    "af_rt_memcpy_d2d": (I, [P, P, SZ, P]),
+    "af_rt_fill_u32": (I, [P, U32, SZ, P]),
+    "af_rt_fill_randn_f16": (I, [P, SZ, U64, F, P]),
+    "af_rt_fill_randn_fp8": (I, [P, SZ, U64, F, P]),
+    "af_rt_stream_create": (I, [ctypes.POINTER(P)]),
+    "af_rt_stream_destroy": (I, [P]),
+    "af_rt_stream_sync": (I, [P]),
+    "af_rt_event_create": (I, [ctypes.POINTER(P)]),
+    "af_rt_event_destroy": (I, [P]),
+    "af_rt_event_record": (I, [P, P]),
+    "af_rt_event_sync": (I, [P]),
+    "af_rt_event_elapsed_ms": (I, [ctypes.POINTER(F), P, P]),
+    "af_rt_capture_begin": (I, [P]),
+    "af_rt_capture_end": (I, [P, ctypes.POINTER(P)]),
+    "af_rt_graph_launch": (I, [P, P]),
+    "af_rt_graph_destroy": (I, [P]),
+}
+
+
+def bind(lib):
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib

@@ -1,0 +1,81 @@
+// af_common.h — shared definitions for the gfx950 KV-cache kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "af_kv.h"
+
+#define AF_TRY_HIP(expr)                              \
+    do {                                              \
+        hipError_t af_e_ = (expr);                    \
+        if (af_e_ != hipSuccess) return int(af_e_);   \
+    } while (0)
+
+// Launch-configuration errors surface here; execution faults surface at the
+// next synchronising call, as with any HIP launch.
+#define AF_TRY_LAUNCH()                               \
+    do {                                              \
+        hipError_t af_e_ = hipGetLastError();         \
+        if (af_e_ != hipSuccess) return int(af_e_);   \
+    } while (0)
+
+namespace af {
+
+constexpr int kWave = 64;
+// Longest split grid; bounds the per-(sequence, head) partial buffers.
+constexpr int kMaxSplits = 256;
+// Fewest tokens a split may own: below this the partial (m, l, o[]) traffic and
+// the combine cost more than the split saves.
+constexpr int kMinSpan = 64;
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Split-K buffers of the decode-attention kernels. Layout of a workspace:
+//   [0, kCounterBytes)           arrival counters, one per (sequence, KV head),
+//                                zero between launches (each launch re-zeroes
+//                                the counters it used)
+//   [kCounterBytes, ...)         part_ml [batch][n_q_heads][splits][2] (max, sum)
+//   then                         part_o  [batch][n_q_heads][splits][head_dim]
+// The counter region has a fixed size and position, so one workspace serves
+// launches of any batch / split count without re-initialisation.
+constexpr size_t kCounterBytes = 64 * 1024;
+constexpr int kMaxCounters = int(kCounterBytes / sizeof(uint32_t));
+
+struct AttnWorkspace {
+    uint32_t* counters;
+    float* part_ml;
+    float* part_o;
+};
+
+inline size_t attn_workspace_bytes(int batch, int n_q_heads, int head_dim, int num_splits) {
+    const size_t pm = size_t(batch) * n_q_heads * num_splits * 2 * sizeof(float);
+    const size_t po = size_t(batch) * n_q_heads * num_splits * head_dim * sizeof(float);
+    return kCounterBytes + align_up(pm, 256) + align_up(po, 256);
+}
+
+inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, int num_splits) {
+    char* p = static_cast<char*>(base);
+    AttnWorkspace w;
+    w.counters = reinterpret_cast<uint32_t*>(p);
+    p += kCounterBytes;
+    w.part_ml = reinterpret_cast<float*>(p);
+    p += align_up(size_t(batch) * n_q_heads * num_splits * 2 * sizeof(float), 256);
+    w.part_o = reinterpret_cast<float*>(p);
+    return w;
+}
+
+// Number of compute units of the current device (cached per device).
+int device_compute_units();
+
+// Default split count: enough workgroups for ~2 per CU, each split at least
+// kMinSpan tokens, at most kMaxSplits.
+int default_splits(int max_seq_len, int batch, int n_kv_heads);
+
+// Fill kernel launcher shared by the runtime ABI and workspace init.
+int fill_u32(void* dst, uint32_t value, size_t n_words, hipStream_t stream);
+
+}  // namespace af

@@ -1,0 +1,43 @@
+// af_device.h — device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace af {
+
+typedef _Float16 f16;
+
+__device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(f16, h)); }
+// fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default mode).
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, f16(f)); }
+
+// OCP E4M3FN encode (bias 7, max 448 = 0x7E, 0x7F NaN, no infinities), round to
+// nearest even. The input must already be clamped to +-448.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x43e00000u) return sign | 0x7eu;  // 448
+    if (a < 0x3c800000u) {                      // below 2^-6: quantum 2^-9
+        const float v = __builtin_bit_cast(float, a) * 512.0f;
+        return sign | uint32_t(__builtin_rintf(v));  // 8 lands on 2^-6 (e=1, m=0)
+    }
+    const int e = int(a >> 23) - 127;
+    const uint32_t mant = a & 0x7fffffu;
+    uint32_t m3 = mant >> 20;
+    const uint32_t rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3 += 1;  // carry bumps the exponent
+    return sign | ((uint32_t(e + 7) << 3) + m3);
+}
+
+// Quantiser convention of tools/quantize_weights.py:249-260: divide by the
+// scale (IEEE), clamp to +-448, cast to e4m3fn (round to nearest even).
+__device__ __forceinline__ uint32_t quantize_fp8(uint16_t h, float scale) {
+    float v = h2f(h) / scale;
+    v = fminf(fmaxf(v, -448.0f), 448.0f);
+    return e4m3_encode(v);
+}
+
+}  // namespace af

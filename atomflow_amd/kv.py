@@ -1,0 +1,273 @@
+"""Python mirror of the KV-cache operator interface.
+
+Names, argument order and meaning follow the reference's launchers
+(include/ops/kernel.h:32-42, 93-103, 167-174, 195-197) and its paged contract
+(src/experimental/server_arch/paged_kv_manager.h:90-121). Tensors are device
+pointers (``int``) or ``device.DeviceBuffer`` objects; ``stream`` is a
+``device.Stream``, a raw handle, or None (default stream). Every call goes to
+libatomflow_kv.so and raises ``AfError`` on a non-zero status.
+"""
+import ctypes
+
+import numpy as np
+
+from . import AF_KV_FP16, AF_KV_FP8_E4M3, AfError, _abi, check, lib
+from .device import DeviceBuffer, _s
+
+
+def _p(x):
+    if x is None:
+        return None
+    return x.ptr if isinstance(x, DeviceBuffer) else int(x)
+
+
+# ---- a1 / a2 / a3 ---------------------------------------------------------
+def build_rope_cache(d_cos, d_sin, max_seq, head_dim, base, stream=None):
+    check(lib().af_rope_table_build(_p(d_cos), _p(d_sin), max_seq, head_dim, base, _s(stream)),
+          "build_rope_cache")
+
+
+def rope_table_host(max_seq, head_dim, base=500000.0):
+    cos = np.empty((max_seq, head_dim // 2), np.float32)
+    sin = np.empty((max_seq, head_dim // 2), np.float32)
+    check(lib().af_rope_table_host(cos.ctypes.data, sin.ctypes.data, max_seq, head_dim, base),
+          "af_rope_table_host")
+    return cos, sin
+
+
+def launch_rope(q, k, cos_cache, sin_cache, seq_len, kv_head_num, q_head_num, head_dim,
+                stream=None):
+    check(lib().af_rope(_p(q), _p(k), _p(cos_cache), _p(sin_cache), seq_len, kv_head_num,
+                        q_head_num, head_dim, _s(stream)), "launch_rope")
+
+
+def launch_write_kv_cache(qkv_out, k_cache, v_cache, current_pos, q_dim, kv_dim, max_seq,
+                          stream=None):
+    check(lib().af_write_kv_cache(_p(qkv_out), _p(k_cache), _p(v_cache), current_pos, max_seq,
+                                  q_dim, kv_dim, _s(stream)), "launch_write_kv_cache")
+
+
+def launch_rope_append(qkv_out, k_cache, v_cache, cos_table, sin_table, pos, max_seq, n_q_heads,
+                       n_kv_heads, head_dim, d_pos=None, d_status=None, stream=None):
+    check(lib().af_rope_append(_p(qkv_out), _p(k_cache), _p(v_cache), _p(cos_table),
+                               _p(sin_table), pos, _p(d_pos), max_seq, n_q_heads, n_kv_heads,
+                               head_dim, _p(d_status), _s(stream)), "launch_rope_append")
+
+
+# ---- a5 ---------------------------------------------------------------------
+def launch_cached_attention(q, k_cache, v_cache, out, seq_len, head_dim, n_q_heads, n_kv_heads,
+                            stream=None):
+    check(lib().af_cached_attention(_p(q), _p(k_cache), _p(v_cache), _p(out), seq_len, head_dim,
+                                    n_q_heads, n_kv_heads, _s(stream)), "launch_cached_attention")
+
+
+def default_splits(max_seq_len, batch, n_kv_heads):
+    return lib().af_attention_default_splits(max_seq_len, batch, n_kv_heads)
+
+
+class AttentionWorkspace:
+    """Split-K workspace (partials + arrival counters), zeroed once at creation."""
+
+    def __init__(self, batch, n_q_heads, n_kv_heads, head_dim, num_splits=0, stream=None):
+        self.nbytes = lib().af_attention_workspace_size(batch, n_q_heads, n_kv_heads, head_dim,
+                                                        num_splits)
+        if self.nbytes == 0:
+            raise AfError(-2, "af_attention_workspace_size")
+        self.buf = DeviceBuffer(self.nbytes)
+        check(lib().af_attention_workspace_init(self.buf.ptr, self.nbytes, _s(stream)),
+              "af_attention_workspace_init")
+
+    @property
+    def ptr(self):
+        return self.buf.ptr
+
+
+def launch_cached_attention_ex(q, k_cache, v_cache, out, seq_len, max_seq_len, head_dim,
+                               n_q_heads, n_kv_heads, workspace, num_splits=0, d_seq_len=None,
+                               stream=None):
+    check(lib().af_cached_attention_ex(_p(q), _p(k_cache), _p(v_cache), _p(out), seq_len,
+                                       _p(d_seq_len), max_seq_len, head_dim, n_q_heads,
+                                       n_kv_heads, num_splits, workspace.ptr, workspace.nbytes,
+                                       _s(stream)), "launch_cached_attention_ex")
+
+
+# ---- a6-a8: paged pool -----------------------------------------------------
+def make_pool(base, dtype, block_size, n_layers, n_kv_heads, head_dim, total_blocks, scales=None):
+    p = _abi.KvPool()
+    p.base = _p(base)
+    p.scales = _p(scales)
+    p.dtype = dtype
+    p.block_size = block_size
+    p.n_layers = n_layers
+    p.n_kv_heads = n_kv_heads
+    p.head_dim = head_dim
+    p.reserved = 0
+    p.total_blocks = total_blocks
+    return p
+
+
+def pool_bytes(pool):
+    return lib().af_kv_pool_bytes(ctypes.byref(pool))
+
+
+def launch_paged_rope_append(qkv_out, batch, pool, layer, d_slots, d_positions, cos_table,
+                             sin_table, max_pos, n_q_heads, stream=None):
+    check(lib().af_paged_rope_append(_p(qkv_out), batch, ctypes.byref(pool), layer, _p(d_slots),
+                                     _p(d_positions), _p(cos_table), _p(sin_table), max_pos,
+                                     n_q_heads, _s(stream)), "launch_paged_rope_append")
+
+
+def launch_paged_attention(q, q_stride, pool, layer, d_block_tables, max_blocks_per_seq,
+                           d_seq_lens, batch, max_seq_len, out, out_stride, n_q_heads, workspace,
+                           num_splits=0, stream=None):
+    check(lib().af_paged_attention(_p(q), q_stride, ctypes.byref(pool), layer, _p(d_block_tables),
+                                   max_blocks_per_seq, _p(d_seq_lens), batch, max_seq_len, _p(out),
+                                   out_stride, n_q_heads, num_splits, workspace.ptr,
+                                   workspace.nbytes, _s(stream)), "launch_paged_attention")
+
+
+def paged_gather(pool, layer, d_block_table, seq_len, k_dst, v_dst, stream=None):
+    check(lib().af_paged_gather(ctypes.byref(pool), layer, _p(d_block_table), seq_len, _p(k_dst),
+                                _p(v_dst), _s(stream)), "paged_gather")
+
+
+def kv_copy_blocks(pool, d_copies, d_count, max_copies, stream=None):
+    check(lib().af_kv_copy_blocks(ctypes.byref(pool), _p(d_copies), _p(d_count), max_copies,
+                                  _s(stream)), "kv_copy_blocks")
+
+
+def fp8_quantize(src_f16, dst, n, scale, stream=None):
+    check(lib().af_fp8_quantize(_p(src_f16), _p(dst), n, scale, _s(stream)), "fp8_quantize")
+
+
+class BlockManager:
+    """atomflow::server::BlockManager through the C ABI.
+
+    ``allocate_block`` returns an id or -1 (pool exhausted) like the reference
+    (paged_kv_manager.h:105-107); the other methods raise ``AfError``.
+    """
+
+    def __init__(self, total_blocks, block_size=16, n_layers=1, n_kv_heads=8, head_dim=128,
+                 dtype=AF_KV_FP16, allocate_pool=False):
+        h = ctypes.c_void_p()
+        check(lib().af_bm_create(total_blocks, block_size, n_layers, n_kv_heads, head_dim, dtype,
+                                 1 if allocate_pool else 0, ctypes.byref(h)), "af_bm_create")
+        self.h = h.value
+        self.block_size = block_size
+
+    def close(self):
+        if self.h:
+            lib().af_bm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # reference contract
+    def allocate_block(self):
+        return lib().af_bm_allocate_block(self.h)
+
+    def free_block(self, block_id):
+        return check(lib().af_bm_free_block(self.h, block_id), "free_block")
+
+    def num_free_blocks(self):
+        return lib().af_bm_num_free_blocks(self.h)
+
+    # extensions
+    def try_free_block(self, block_id):
+        return lib().af_bm_free_block(self.h, block_id)
+
+    def ref_count(self, block_id):
+        return lib().af_bm_ref_count(self.h, block_id)
+
+    def attach_pool(self, base, scales=None):
+        check(lib().af_bm_attach_pool(self.h, _p(base), _p(scales)), "attach_pool")
+
+    def pool(self):
+        p = _abi.KvPool()
+        check(lib().af_bm_pool(self.h, ctypes.byref(p)), "af_bm_pool")
+        return p
+
+    def seq_create(self):
+        return _nonneg(lib().af_bm_seq_create(self.h), "seq_create")
+
+    def seq_fork(self, src):
+        return lib().af_bm_seq_fork(self.h, src)
+
+    def seq_free(self, seq):
+        return lib().af_bm_seq_free(self.h, seq)
+
+    def seq_len(self, seq):
+        return lib().af_bm_seq_len(self.h, seq)
+
+    def seq_table(self, seq):
+        n = lib().af_bm_seq_table(self.h, seq, None, 0, None)
+        if n < 0:
+            return n
+        ids = (ctypes.c_int32 * max(n, 1))()
+        fill = ctypes.c_int32(0)
+        lib().af_bm_seq_table(self.h, seq, ids, n, ctypes.byref(fill))
+        return list(ids[:n]), fill.value
+
+    def seq_append(self, seq):
+        """(pos, slot, (cow_src, cow_dst, cow_rows)) or a negative status."""
+        slot = ctypes.c_int64(0)
+        a, b, c = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_int32(0)
+        r = lib().af_bm_seq_append(self.h, seq, ctypes.byref(slot), ctypes.byref(a),
+                                   ctypes.byref(b), ctypes.byref(c))
+        if r < 0:
+            return r
+        return r, slot.value, (a.value, b.value, c.value)
+
+    def seq_extend(self, seq, n):
+        a, b, c = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_int32(0)
+        r = lib().af_bm_seq_extend(self.h, seq, n, ctypes.byref(a), ctypes.byref(b),
+                                   ctypes.byref(c))
+        if r < 0:
+            return r
+        return r, (a.value, b.value, c.value)
+
+    def seq_slot(self, seq, pos):
+        return lib().af_bm_seq_slot(self.h, seq, pos)
+
+    def plan_decode(self, seqs, max_copies=None):
+        """(slots[int64], positions[int32], copies[n,3] int32) or a negative status."""
+        seqs = np.ascontiguousarray(seqs, np.int32)
+        n = len(seqs)
+        if max_copies is None:
+            max_copies = max(n, 1)
+        slots = np.zeros(n, np.int64)
+        pos = np.zeros(n, np.int32)
+        copies = np.zeros((max_copies, 3), np.int32)
+        nc = ctypes.c_int32(0)
+        r = lib().af_bm_plan_decode(self.h, seqs.ctypes.data, n, slots.ctypes.data, pos.ctypes.data,
+                                    copies.ctypes.data, max_copies, ctypes.byref(nc))
+        if r < 0:
+            return r
+        return slots, pos, copies[: nc.value].copy()
+
+    def export_tables(self, seqs, max_blocks):
+        seqs = np.ascontiguousarray(seqs, np.int32)
+        tables = np.zeros((len(seqs), max_blocks), np.int32)
+        lens = np.zeros(len(seqs), np.int32)
+        check(lib().af_bm_export_tables(self.h, seqs.ctypes.data, len(seqs), tables.ctypes.data,
+                                        max_blocks, lens.ctypes.data), "export_tables")
+        return tables, lens
+
+
+def _nonneg(r, what):
+    if r < 0:
+        raise AfError(r, what)
+    return r
+
+
+__all__ = [
+    "AF_KV_FP16", "AF_KV_FP8_E4M3", "AttentionWorkspace", "BlockManager", "build_rope_cache",
+    "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
+    "launch_cached_attention_ex", "launch_paged_attention", "launch_paged_rope_append",
+    "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
+    "pool_bytes", "rope_table_host",
+]

@@ -1,0 +1,255 @@
+/*
+ * af_kv.h — C ABI of the MI355X KV-cache hot path (libatomflow_kv.so).
+ *
+ * Plain C: raw device pointers, integer sizes, a stream handle. No C++ or torch
+ * types. Every function returns an int status:
+ *     0            success (AF_OK)
+ *     > 0          a hipError_t value from the HIP runtime
+ *     < 0          an AF_ERR_* code below
+ * The ABI never throws and never aborts. Kernel launches are asynchronous and
+ * stream-ordered, do no host synchronisation and allocate nothing, so they may
+ * be recorded into a hipGraph (stream capture). Device buffers are owned by the
+ * caller unless a function says otherwise.
+ *
+ * Conventions shared with the reference (Altersieg/AtomFlow):
+ *   qkv_out row    = [Q: n_q_heads*head_dim | K: kv_dim | V: kv_dim] fp16
+ *                    (src/core/engine.cu:326-331, include/core/model_state.h:48)
+ *   KV cache row t = [kv_head 0 dims 0..hd-1 | kv_head 1 ... ], kv_dim = n_kv_heads*head_dim
+ *                    (include/core/model_state.h:56-64, README.md:57)
+ *   GQA mapping    = kv_head(h) = h * n_kv_heads / n_q_heads (src/kernel/tiled_attention.cu:208)
+ *   RoPE pairs     = (d, d + head_dim/2), table row `pos` = pos * head_dim/2 floats
+ *                    (src/kernel/rope.cu:22-45, src/kernel/helpers.cu:94-113)
+ */
+#ifndef AF_KV_H_
+#define AF_KV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define AF_OK 0
+/* -1 is the value the reference's BlockManager::allocate_block() returns when
+ * the pool is exhausted (src/experimental/server_arch/paged_kv_manager.h:105-107). */
+#define AF_ERR_POOL_EXHAUSTED (-1)
+#define AF_ERR_INVALID_ARG (-2)     /* null pointer, bad size, inconsistent shapes   */
+#define AF_ERR_UNSUPPORTED (-3)     /* head_dim / GQA ratio / dtype not compiled in  */
+#define AF_ERR_OUT_OF_RANGE (-4)    /* position >= capacity, table too short          */
+#define AF_ERR_BAD_BLOCK (-5)       /* block id out of range or already free          */
+#define AF_ERR_WORKSPACE (-6)       /* workspace missing or too small                 */
+#define AF_ERR_BAD_SEQUENCE (-7)    /* unknown sequence id                            */
+#define AF_ERR_NOT_BUILT (-8)       /* library built without a device code object     */
+
+typedef void* af_stream_t; /* hipStream_t; NULL = the default stream */
+
+/* KV element types; values equal the reference's DataType enumerators
+ * (include/core/view.h:15-20). */
+#define AF_KV_FP16 1
+#define AF_KV_FP8_E4M3 3
+
+const char* af_status_string(int status);
+/* (major << 16) | (minor << 8) | patch */
+int af_version(void);
+
+/* ======================================================================== */
+/* a1. RoPE cos/sin table                                                    */
+/* ======================================================================== */
+/* Replaces build_rope_cache (include/ops/kernel.h:195-197, src/kernel/helpers.cu:94-113).
+ * Table layout [max_seq, head_dim/2] fp32; computed on the host in float
+ * (theta = s / powf(base, 2*i/head_dim); cosf/sinf) and copied to the device.
+ * The copy is synchronous with respect to the host (the host staging buffer is
+ * released on return). */
+int af_rope_table_build(float* d_cos, float* d_sin, int max_seq, int head_dim, float base,
+                        af_stream_t stream);
+/* Same table into host memory (no device needed). */
+int af_rope_table_host(float* h_cos, float* h_sin, int max_seq, int head_dim, float base);
+
+/* ======================================================================== */
+/* a2 / a3. Reference-shaped RoPE and KV write                              */
+/* ======================================================================== */
+/* Replaces launch_rope (include/ops/kernel.h:32-42, src/kernel/rope.cu:48-84).
+ * q: [seq_len, q_head_num*head_dim] fp16, k: [seq_len, kv_head_num*head_dim]
+ * fp16, both rotated in place; cos/sin: table rows starting at the position of
+ * token 0 (the engine passes d_cos + pos*head_dim/2, src/core/engine.cu:340-344). */
+int af_rope(void* q, void* k, const float* cos_cache, const float* sin_cache, int seq_len,
+            int kv_head_num, int q_head_num, int head_dim, af_stream_t stream);
+
+/* Replaces launch_write_kv_cache (include/ops/kernel.h:167-174, src/kernel/helpers.cu:141-156).
+ * k_cache[current_pos, :] = qkv_out[q_dim : q_dim+kv_dim],
+ * v_cache[current_pos, :] = qkv_out[q_dim+kv_dim : q_dim+2*kv_dim].
+ * max_seq (the cache's row count) is checked: current_pos >= max_seq -> AF_ERR_OUT_OF_RANGE. */
+int af_write_kv_cache(const void* qkv_out, void* k_cache, void* v_cache, int current_pos,
+                      int max_seq, int q_dim, int kv_dim, af_stream_t stream);
+
+/* ======================================================================== */
+/* a2+a3 fused. RoPE + append into the contiguous cache (one launch)         */
+/* ======================================================================== */
+/* Equivalent to launch_rope(pos) followed by launch_write_kv_cache(pos)
+ * (src/core/engine.cu:326-355): Q and K inside qkv_out are rotated in place,
+ * then K (rotated) and V are written to row pos of k_cache / v_cache.
+ * Position: *d_pos when d_pos != NULL (device-resident, for graph replay),
+ * otherwise `pos`. A device-resident pos >= max_seq writes nothing and stores
+ * AF_ERR_OUT_OF_RANGE into *d_status when d_status != NULL. */
+int af_rope_append(void* qkv_out, void* k_cache, void* v_cache, const float* cos_table,
+                   const float* sin_table, int pos, const int32_t* d_pos, int max_seq,
+                   int n_q_heads, int n_kv_heads, int head_dim, int32_t* d_status,
+                   af_stream_t stream);
+
+/* ======================================================================== */
+/* a5. GQA decode attention over the contiguous cache                       */
+/* ======================================================================== */
+/* Replaces launch_cached_attention (include/ops/kernel.h:93-103,
+ * src/kernel/tiled_attention.cu:275-296), same arguments. Split-K over the
+ * sequence with a library-owned workspace (allocated on the first call per
+ * device; call af_attention_reserve() first when the call will be captured). */
+int af_cached_attention(const void* q, const void* k_cache, const void* v_cache, void* out,
+                        int seq_len, int head_dim, int n_q_heads, int n_kv_heads,
+                        af_stream_t stream);
+
+/* Pre-allocates the library-owned workspace for batch x n_q_heads heads. */
+int af_attention_reserve(int batch, int n_q_heads, int n_kv_heads, int head_dim);
+
+/* Workspace bytes for the explicit-workspace entry points. */
+size_t af_attention_workspace_size(int batch, int n_q_heads, int n_kv_heads, int head_dim,
+                                   int num_splits);
+/* Zero-fills a workspace (a fill kernel, not a memset node). Needed once after
+ * allocation; every attention launch leaves its counters at zero again. */
+int af_attention_workspace_init(void* workspace, size_t workspace_bytes, af_stream_t stream);
+/* Split count the library picks for a given longest sequence and batch. */
+int af_attention_default_splits(int max_seq_len, int batch, int n_kv_heads);
+
+/* Explicit-workspace form. seq_len: used when d_seq_len == NULL; otherwise the
+ * length is read on the device (graph replay). num_splits <= 0 picks the
+ * default for max_seq_len. k/v row stride is n_kv_heads*head_dim. */
+int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache, void* out,
+                           int seq_len, const int32_t* d_seq_len, int max_seq_len, int head_dim,
+                           int n_q_heads, int n_kv_heads, int num_splits, void* workspace,
+                           size_t workspace_bytes, af_stream_t stream);
+
+/* ======================================================================== */
+/* a6-a8. Paged KV pool                                                      */
+/* ======================================================================== */
+/* One device allocation holds every layer (one block id spans all layers):
+ *   base = [layer 0 K | layer 0 V | layer 1 K | ... ], each slab
+ *          total_blocks * block_size * kv_dim elements,
+ *   block b of layer l, K row r at
+ *          base + ((2*l) * total_blocks + b) * block_size * kv_dim + r * kv_dim.
+ * FP8 pools carry fp32 scales [n_layers][2 (K,V)][n_kv_heads]; element value =
+ * e4m3fn(code) * scale (convention of tools/quantize_weights.py:249-260). */
+typedef struct af_kv_pool {
+    void* base;
+    const float* scales; /* FP8 only, else NULL */
+    int32_t dtype;       /* AF_KV_FP16 or AF_KV_FP8_E4M3 */
+    int32_t block_size;  /* tokens per block, power of two, >= 8 */
+    int32_t n_layers;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t reserved;
+    int64_t total_blocks;
+} af_kv_pool;
+
+size_t af_kv_pool_bytes(const af_kv_pool* pool);
+
+/* Paged RoPE + append for a batch (the paged form of af_rope_append).
+ * qkv_out: [batch, q_dim + 2*kv_dim] fp16 (rows contiguous).
+ * d_positions[b]: the logical position of the new token (RoPE row).
+ * d_slots[b]: physical row = block_id * block_size + offset (from the BlockManager).
+ * FP8 pools quantise K/V with the layer's scales (RNE, clamped to +-448). */
+int af_paged_rope_append(void* qkv_out, int batch, const af_kv_pool* pool, int layer,
+                         const int64_t* d_slots, const int32_t* d_positions,
+                         const float* cos_table, const float* sin_table, int max_pos,
+                         int n_q_heads, af_stream_t stream);
+
+/* Paged GQA decode attention for a batch.
+ * q: [batch, q_stride] fp16 (head h at q + b*q_stride + h*head_dim),
+ * d_block_tables: [batch, max_blocks_per_seq] int32, d_seq_lens: [batch] int32,
+ * out: [batch, out_stride] fp16. max_seq_len bounds every d_seq_lens[b] and sizes
+ * the split grid. Workspace from af_attention_workspace_size(batch, ...). */
+int af_paged_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                       const int32_t* d_block_tables, int max_blocks_per_seq,
+                       const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
+                       int out_stride, int n_q_heads, int num_splits, void* workspace,
+                       size_t workspace_bytes, af_stream_t stream);
+
+/* Gathers one sequence's first seq_len logical rows of `layer` into
+ * contiguous [seq_len, kv_dim] buffers (K and V; elements copied bit for bit). */
+int af_paged_gather(const af_kv_pool* pool, int layer, const int32_t* d_block_table,
+                    int seq_len, void* k_dst, void* v_dst, af_stream_t stream);
+
+/* Copy-on-write block copies for every layer: for i < *d_count (device int),
+ * rows [0, d_copies[3i+2]) of block d_copies[3i] are copied to block
+ * d_copies[3i+1], K and V, all layers. max_copies bounds *d_count. */
+int af_kv_copy_blocks(const af_kv_pool* pool, const int32_t* d_copies, const int32_t* d_count,
+                      int max_copies, af_stream_t stream);
+
+/* FP8 E4M3 quantisation of fp16 values with one fp32 scale (device). */
+int af_fp8_quantize(const void* src_f16, uint8_t* dst, size_t n, float scale, af_stream_t stream);
+
+/* ======================================================================== */
+/* a6. BlockManager (host bookkeeping, optional device pool)                */
+/* ======================================================================== */
+/* Contract of atomflow::server::BlockManager
+ * (src/experimental/server_arch/paged_kv_manager.h:90-121), extended with
+ * refcounts, sequences (PageTables), fork and copy-on-write. Not thread-safe. */
+typedef struct af_block_manager af_block_manager;
+
+/* allocate_pool = 1: one hipMalloc for the pool, like BlockManager::initialize
+ * (paged_kv_manager.h:103); 0: host bookkeeping only (the pool may be given
+ * later with af_bm_attach_pool). */
+int af_bm_create(int total_blocks, int block_size, int n_layers, int n_kv_heads, int head_dim,
+                 int dtype, int allocate_pool, af_block_manager** out);
+int af_bm_destroy(af_block_manager* bm);
+int af_bm_attach_pool(af_block_manager* bm, void* base, const float* scales);
+int af_bm_pool(const af_block_manager* bm, af_kv_pool* out);
+
+/* allocate_block(): block id, or AF_ERR_POOL_EXHAUSTED (-1) (paged_kv_manager.h:105-107).
+ * The new block has ref_count 1. */
+int af_bm_allocate_block(af_block_manager* bm);
+/* free_block(id) (paged_kv_manager.h:111): drops one reference; at zero the id
+ * returns to the top of the free stack. */
+int af_bm_free_block(af_block_manager* bm, int block_id);
+int af_bm_num_free_blocks(const af_block_manager* bm);
+/* ref_count of a block (0 when free), or AF_ERR_BAD_BLOCK. */
+int af_bm_ref_count(const af_block_manager* bm, int block_id);
+
+/* Sequences (PageTable = ordered block ids + last_block_fill). */
+int af_bm_seq_create(af_block_manager* bm);              /* -> seq id */
+int af_bm_seq_fork(af_block_manager* bm, int src_seq);   /* -> new seq id, every block ref+1 */
+int af_bm_seq_free(af_block_manager* bm, int seq);       /* free_block on each block */
+int af_bm_seq_len(const af_block_manager* bm, int seq);  /* tokens */
+/* Writes up to max_ids block ids; returns the number of blocks. */
+int af_bm_seq_table(const af_block_manager* bm, int seq, int32_t* ids, int max_ids,
+                    int32_t* last_block_fill);
+/* Plans one token append: a new block when the tail is full (or the table is
+ * empty); copy-on-write when the tail is partial and shared (ref > 1): a new
+ * block takes the tail's role, the caller copies rows [0, *cow_rows) from
+ * *cow_src to *cow_dst for every layer (af_kv_copy_blocks), the old tail drops
+ * one reference. Returns the new token's logical position; *slot = physical
+ * row (block * block_size + offset). cow_* = -1 / 0 when no copy is needed.
+ * On AF_ERR_POOL_EXHAUSTED nothing changes. */
+int af_bm_seq_append(af_block_manager* bm, int seq, int64_t* slot, int32_t* cow_src,
+                     int32_t* cow_dst, int32_t* cow_rows);
+/* Appends n_tokens at once (prefill-style reservation, same rules per token).
+ * Returns the first new position; copy-on-write of a shared tail is reported
+ * as for af_bm_seq_append (at most one copy per call). */
+int af_bm_seq_extend(af_block_manager* bm, int seq, int n_tokens, int32_t* cow_src,
+                     int32_t* cow_dst, int32_t* cow_rows);
+/* Physical row of logical token `pos` of `seq`, or a negative status. */
+int64_t af_bm_seq_slot(const af_block_manager* bm, int seq, int pos);
+
+/* Batched step planning for n sequences: one append each. Fills host arrays
+ * slots[n], positions[n], copies[3*max_copies] (src, dst, rows) and *n_copies.
+ * On failure no sequence is changed. */
+int af_bm_plan_decode(af_block_manager* bm, const int32_t* seqs, int n, int64_t* slots,
+                      int32_t* positions, int32_t* copies, int max_copies, int32_t* n_copies);
+/* Block tables [n][max_blocks] (unused entries = 0) and lengths for n sequences. */
+int af_bm_export_tables(const af_block_manager* bm, const int32_t* seqs, int n, int32_t* tables,
+                        int max_blocks, int32_t* seq_lens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AF_KV_H_ */

@@ -1,0 +1,64 @@
+#pragma once
+// C++ operator boundary of the KV-cache hot path: the reference's launcher
+// names and argument orders (include/ops/kernel.h:32-42, 93-103, 167-174,
+// 195-197) with hipStream_t, plus the fused and paged launchers this build adds.
+// Failures throw std::runtime_error carrying the af_kv.h status text (the
+// reference aborts in Debug and ignores errors in Release, utils.h:41-118).
+// All launchers are asynchronous and safe inside stream capture (except
+// build_rope_cache, which copies synchronously, as it runs once at init).
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "af_kv.h"
+#include "core/view.h"
+
+// kernel.h:32-42 — q [seq_len, q_head_num*head_dim], k [seq_len, kv_head_num*head_dim]
+// rotated in place; cos/sin point at the first token's table row.
+void launch_rope(const View& q_input, const View& k_input, const float* cos_cache,
+                 const float* sin_cache, int seq_len, int kv_head_num, int q_head_num,
+                 int head_dim, hipStream_t stream);
+
+// kernel.h:93-103 — seq_len = current_pos + 1 tokens of the [MAX_SEQ_LEN, kv_dim] caches.
+void launch_cached_attention(const __half* q, const __half* k_cache, const __half* v_cache,
+                             __half* out, int seq_len, int head_dim, int n_q_heads,
+                             int n_kv_heads, hipStream_t stream);
+
+// kernel.h:167-174 — row current_pos of the caches from qkv_out [Q | K | V].
+// k_cache.dims[0] (MAX_SEQ_LEN) bounds current_pos.
+void launch_write_kv_cache(const View& qkv_out, View& k_cache, View& v_cache, int current_pos,
+                           int q_dim, int kv_dim, hipStream_t stream);
+
+// kernel.h:195-197 — [max_seq, head_dim/2] fp32 tables, host-computed, copied.
+void build_rope_cache(float* d_cos, float* d_sin, int max_seq, int head_dim, float base,
+                      hipStream_t stream);
+
+// ---- added by this build ---------------------------------------------------
+// launch_rope(pos) + launch_write_kv_cache(pos) in one kernel. d_pos (device,
+// nullable) overrides pos so a captured graph can advance the position.
+void launch_rope_append(View& qkv_out, View& k_cache, View& v_cache, const float* cos_table,
+                        const float* sin_table, int pos, const int32_t* d_pos, int n_q_heads,
+                        int n_kv_heads, int head_dim, hipStream_t stream);
+
+// Split-K attention with a caller workspace (af_attention_workspace_size) and a
+// device-resident length (nullable).
+void launch_cached_attention_ws(const __half* q, const __half* k_cache, const __half* v_cache,
+                                __half* out, int seq_len, const int32_t* d_seq_len,
+                                int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,
+                                int num_splits, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
+void launch_paged_rope_append(__half* qkv_out, int batch, const af_kv_pool& pool, int layer,
+                              const int64_t* d_slots, const int32_t* d_positions,
+                              const float* cos_table, const float* sin_table, int max_pos,
+                              int n_q_heads, hipStream_t stream);
+
+void launch_paged_attention(const __half* q, int q_stride, const af_kv_pool& pool, int layer,
+                            const int32_t* d_block_tables, int max_blocks_per_seq,
+                            const int32_t* d_seq_lens, int batch, int max_seq_len, __half* out,
+                            int out_stride, int n_q_heads, int num_splits, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+void launch_kv_copy_blocks(const af_kv_pool& pool, const int32_t* d_copies, const int32_t* d_count,
+                           int max_copies, hipStream_t stream);

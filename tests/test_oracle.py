@@ -1,0 +1,317 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Each check is independent of the oracle's own code: IEEE conversions in numpy,
+closed forms of RoPE and softmax attention, torch's SDPA and float8_e4m3fn
+(through the committed fixtures in tests/golden/), and brute-force numpy
+restatements with independent indexing.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import HD, KV_DIM, NKV, NQ, Q_DIM, THETA, contiguous_case, randn_f16
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---- fp16 conversions ------------------------------------------------------
+def test_f16_to_f32_all_patterns():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    ours = oracle.f16_to_f32(h)
+    ref = h.astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_round_trip_all_halves():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    keep = ~np.isnan(h)
+    back = oracle.f32_to_f16(h.astype(np.float32)[keep])
+    assert np.array_equal(back.view(np.uint16), h[keep].view(np.uint16))
+
+
+def test_f32_to_f16_ties_and_random_vs_numpy():
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32)  # exact in fp32: ties to even
+    r = np.random.Generator(np.random.PCG64(3))
+    rand = np.concatenate([
+        (r.standard_normal(200000) * 10.0 ** r.uniform(-9, 5, 200000)).astype(np.float32),
+        np.array([65504, 65519.99, 65520, 1e9, 2.0 ** -25, 2.0 ** -24, 3 * 2.0 ** -26, 0.0, -0.0,
+                  np.inf, -np.inf], np.float32)])
+    for x in (mids, -mids, rand):
+        ours = oracle.f32_to_f16(x).view(np.uint16)
+        with np.errstate(over="ignore"):
+            ref = x.astype(np.float16).view(np.uint16)
+        assert np.array_equal(ours, ref)
+
+
+# ---- a1: RoPE table --------------------------------------------------------
+def test_rope_table_closed_forms():
+    cos, sin = oracle.rope_table(4096, HD, THETA)
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    s = np.arange(64, dtype=np.float64)[:, None]
+    i = np.arange(HD // 2, dtype=np.float64)[None, :]
+    theta = s / THETA ** (2 * i / HD)
+    assert np.max(np.abs(cos[:64] - np.cos(theta))) < 1e-5
+    assert np.max(np.abs(sin[:64] - np.sin(theta))) < 1e-5
+    norm = cos.astype(np.float64) ** 2 + sin.astype(np.float64) ** 2
+    assert np.max(np.abs(norm - 1.0)) < 1e-6
+
+
+# ---- a2 / a3 ---------------------------------------------------------------
+def _numpy_rope(q, k, c, s, nq, nkv, hd):
+    """Independent restatement: fp32 products and sum, each IEEE-rounded by numpy."""
+    def rot(x, nh):
+        x = x.astype(np.float32).reshape(nh, 2, hd // 2)
+        a, b = x[:, 0, :], x[:, 1, :]
+        return np.concatenate([a * c - b * s, a * s + b * c], axis=1).astype(np.float16).ravel()
+    return rot(q, nq), rot(k, nkv)
+
+
+def test_rope_matches_numpy_bit_exact():
+    cos, sin = oracle.rope_table(2048, HD, THETA)
+    for pos in (0, 1, 7, 512, 2047):
+        qkv = randn_f16(Q_DIM + 2 * KV_DIM, 11 + pos)
+        q, k = qkv[:Q_DIM], qkv[Q_DIM:Q_DIM + KV_DIM]
+        oq, okk = oracle.rope(q, k, cos[pos], sin[pos], NQ, NKV, HD)
+        nq_, nk_ = _numpy_rope(q, k, cos[pos], sin[pos], NQ, NKV, HD)
+        assert np.array_equal(oq.view(np.uint16), nq_.view(np.uint16))
+        assert np.array_equal(okk.view(np.uint16), nk_.view(np.uint16))
+
+
+def test_rope_identity_norm_and_composition():
+    cos, sin = oracle.rope_table(256, HD, THETA)
+    q = randn_f16(Q_DIM, 5)
+    k = randn_f16(KV_DIM, 6)
+    oq, okk = oracle.rope(q, k, cos[0], sin[0], NQ, NKV, HD)
+    assert np.array_equal(oq, q) and np.array_equal(okk, k)  # pos 0 = identity
+    oq, _ = oracle.rope(q, k, cos[100], sin[100], NQ, NKV, HD)
+    x = q.astype(np.float64).reshape(NQ, 2, HD // 2)
+    y = oq.astype(np.float64).reshape(NQ, 2, HD // 2)
+    n0 = np.hypot(x[:, 0], x[:, 1])
+    n1 = np.hypot(y[:, 0], y[:, 1])
+    assert np.max(np.abs(n1 - n0) / np.maximum(n0, 1e-3)) < 2e-3  # rotation keeps pair norms
+    # rotating by pos a then pos b ~ pos a+b (fp16 rounding twice)
+    a, b = 37, 61
+    qa, _ = oracle.rope(q, k, cos[a], sin[a], NQ, NKV, HD)
+    qab, _ = oracle.rope(qa, k, cos[b], sin[b], NQ, NKV, HD)
+    qs, _ = oracle.rope(q, k, cos[a + b], sin[a + b], NQ, NKV, HD)
+    assert np.max(np.abs(qab.astype(np.float32) - qs.astype(np.float32))) < 1e-2
+
+
+def test_rope_multi_token_rows():
+    cos, sin = oracle.rope_table(64, HD, THETA)
+    q = randn_f16((5, Q_DIM), 21)
+    k = randn_f16((5, KV_DIM), 22)
+    oq, ok_ = oracle.rope(q, k, cos[3:8], sin[3:8], NQ, NKV, HD)
+    for t in range(5):
+        a, b = _numpy_rope(q[t], k[t], cos[3 + t], sin[3 + t], NQ, NKV, HD)
+        assert np.array_equal(oq[t].view(np.uint16), a.view(np.uint16))
+        assert np.array_equal(ok_[t].view(np.uint16), b.view(np.uint16))
+
+
+def test_write_kv_cache_and_canaries():
+    qkv, k, v = contiguous_case(64, 10, 31)
+    k0, v0 = k.copy(), v.copy()
+    oracle.write_kv_cache(qkv, k, v, 10, Q_DIM, KV_DIM)
+    assert np.array_equal(k[10], qkv[Q_DIM:Q_DIM + KV_DIM])
+    assert np.array_equal(v[10], qkv[Q_DIM + KV_DIM:])
+    rows = np.arange(64) != 10
+    assert np.array_equal(k[rows], k0[rows]) and np.array_equal(v[rows], v0[rows])
+
+
+def test_rope_append_is_rope_then_write():
+    cos, sin = oracle.rope_table(600, HD, THETA)
+    qkv, k, v = contiguous_case(600, 512, 41)
+    k2, v2 = k.copy(), v.copy()
+    out = oracle.rope_append(qkv, k, v, cos, sin, 512, NQ, NKV, HD)
+    rq, rk = _numpy_rope(qkv[:Q_DIM], qkv[Q_DIM:Q_DIM + KV_DIM], cos[512], sin[512], NQ, NKV, HD)
+    assert np.array_equal(out[:Q_DIM].view(np.uint16), rq.view(np.uint16))
+    assert np.array_equal(out[Q_DIM:Q_DIM + KV_DIM].view(np.uint16), rk.view(np.uint16))
+    assert np.array_equal(out[Q_DIM + KV_DIM:], qkv[Q_DIM + KV_DIM:])
+    assert np.array_equal(k[512].view(np.uint16), rk.view(np.uint16))
+    assert np.array_equal(v[512], qkv[Q_DIM + KV_DIM:])
+    assert np.array_equal(k[:512], k2[:512]) and np.array_equal(k[513:], k2[513:])
+
+
+# ---- a5: attention ---------------------------------------------------------
+def _numpy_attention(q, k, v, L, nq, nkv, hd):
+    qf = q.astype(np.float64).reshape(nq, hd)
+    kf = k[:L].astype(np.float64).reshape(L, nkv, hd)
+    vf = v[:L].astype(np.float64).reshape(L, nkv, hd)
+    out = np.empty((nq, hd))
+    for h in range(nq):
+        kv = h * nkv // nq
+        s = kf[:, kv, :] @ qf[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ vf[:, kv, :]
+    return out.ravel()
+
+
+def test_attention_L1_is_v_row():
+    q = randn_f16(Q_DIM, 51)
+    k = randn_f16((1, KV_DIM), 52)
+    v = randn_f16((1, KV_DIM), 53)
+    out = oracle.cached_attention(q, k, v, 1, NQ, NKV, HD)
+    exp = np.concatenate([v[0, (h // 3) * HD:(h // 3 + 1) * HD] for h in range(NQ)])
+    assert np.array_equal(out.view(np.uint16), exp.view(np.uint16))
+
+
+def test_attention_equal_keys_mean_and_dominant_key():
+    L = 40
+    q = randn_f16(Q_DIM, 61)
+    k = np.tile(randn_f16((1, KV_DIM), 62), (L, 1))
+    v = randn_f16((L, KV_DIM), 63)
+    out = oracle.cached_attention(q, k, v, L, NQ, NKV, HD).astype(np.float64)
+    mean = v.astype(np.float64).mean(0)
+    exp = np.concatenate([mean[(h // 3) * HD:(h // 3 + 1) * HD] for h in range(NQ)])
+    assert np.max(np.abs(out - exp)) < 1e-3
+    # one key aligned with every query head of its group: softmax ~ one-hot
+    q = np.zeros(Q_DIM, np.float16)
+    q[:] = 1.0
+    k = np.zeros((L, KV_DIM), np.float16)
+    k[17] = 4.0  # score 4*128/sqrt(128) = 45 vs 0 elsewhere
+    out = oracle.cached_attention(q, k, v, L, NQ, NKV, HD).astype(np.float64)
+    exp = np.concatenate([v[17, (h // 3) * HD:(h // 3 + 1) * HD] for h in range(NQ)])
+    assert np.max(np.abs(out - exp)) < 2e-3
+
+
+def test_attention_permutation_invariance():
+    L = 300
+    q = randn_f16(Q_DIM, 71)
+    k = randn_f16((L, KV_DIM), 72)
+    v = randn_f16((L, KV_DIM), 73)
+    perm = np.random.Generator(np.random.PCG64(74)).permutation(L)
+    a = oracle.cached_attention(q, k, v, L, NQ, NKV, HD).astype(np.float32)
+    b = oracle.cached_attention(q, k[perm], v[perm], L, NQ, NKV, HD).astype(np.float32)
+    assert np.max(np.abs(a - b)) < 1e-3
+
+
+@pytest.mark.parametrize("case", range(7))
+def test_attention_vs_torch_sdpa_fixture(case):
+    from golden.make_golden import SDPA_CASES, digest, sdpa_inputs
+
+    z = np.load(os.path.join(GOLDEN, "sdpa_cases.npz"), allow_pickle=False)
+    nq, nkv, hd, L, seed = (int(x) for x in z["shapes"][case])
+    assert (nq, nkv, hd, L, seed) == SDPA_CASES[case]
+    q, k, v = sdpa_inputs(nq, nkv, hd, L, seed)
+    assert digest(q, k, v) == str(z["digests"][case]), "seeded inputs changed"
+    ref = z[f"out{case}"]
+    ours = oracle.cached_attention(q, k, v, L, nq, nkv, hd).astype(np.float64)
+    f64 = oracle.cached_attention_f64(q, k, v, L, nq, nkv, hd)
+    npy = _numpy_attention(q, k, v, L, nq, nkv, hd)
+    assert np.max(np.abs(f64 - ref)) < 1e-9      # fp64 oracle == SDPA
+    assert np.max(np.abs(npy - ref)) < 1e-9      # independent restatement == SDPA
+    assert np.max(np.abs(ours - ref)) < 2e-3     # fp32/fp16 oracle within the bar
+    assert np.max(np.abs(ours - ref) / (np.abs(ref) + 1e-2)) < 1e-1
+
+
+def test_attention_multithreaded_equals_scalar():
+    L = 700
+    q = randn_f16(Q_DIM, 81)
+    k = randn_f16((L, KV_DIM), 82)
+    v = randn_f16((L, KV_DIM), 83)
+    a = oracle.cached_attention(q, k, v, L, NQ, NKV, HD)
+    b = oracle.cached_attention(q, k, v, L, NQ, NKV, HD, threads=4)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+# ---- a8: FP8 E4M3 ------------------------------------------------------------
+def test_e4m3_decode_exhaustive_vs_torch():
+    z = np.load(os.path.join(GOLDEN, "fp8_e4m3fn.npz"), allow_pickle=False)
+    ours = oracle.e4m3_decode_table()
+    ref = z["decode"]
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(ours[fin], ref[fin])
+    assert np.sum(np.isnan(ref)) == 2 and np.nanmax(ours) == 448.0
+
+
+def test_e4m3_encode_vs_torch():
+    z = np.load(os.path.join(GOLDEN, "fp8_e4m3fn.npz"), allow_pickle=False)
+    x, enc = z["x"], z["encoded"]
+    ours = oracle.e4m3_encode(x)
+    assert np.array_equal(ours, enc)
+
+
+def test_fp8_quantize_reference_convention():
+    z = np.load(os.path.join(GOLDEN, "fp8_e4m3fn.npz"), allow_pickle=False)
+    ours = oracle.fp8_quantize(z["quant_src"], float(z["quant_scale"]))
+    assert np.array_equal(ours, z["quant_codes"])
+
+
+# ---- a7: paged -----------------------------------------------------------------
+def test_paged_gather_identity_and_permuted():
+    bs, nblk = 16, 40
+    slab = randn_f16((nblk * bs, KV_DIM), 91)
+    L = 300
+    ident = np.arange(nblk, dtype=np.int32)
+    g = oracle.paged_gather(slab, ident, L, bs, KV_DIM)
+    assert np.array_equal(g.view(np.uint16), slab[:L].view(np.uint16))
+    perm = np.random.Generator(np.random.PCG64(92)).permutation(nblk).astype(np.int32)
+    g = oracle.paged_gather(slab, perm, L, bs, KV_DIM)
+    exp = np.stack([slab[perm[t // bs] * bs + t % bs] for t in range(L)])
+    assert np.array_equal(g.view(np.uint16), exp.view(np.uint16))
+
+
+def test_paged_attention_equals_contiguous_on_gathered():
+    bs, nblk, L = 16, 64, 500
+    ks = randn_f16((nblk * bs, KV_DIM), 93)
+    vs = randn_f16((nblk * bs, KV_DIM), 94)
+    table = np.random.Generator(np.random.PCG64(95)).permutation(nblk).astype(np.int32)
+    q = randn_f16(Q_DIM, 96)
+    a = oracle.paged_attention_f16(q, ks, vs, table, L, bs, NQ, NKV, HD)
+    kg = oracle.paged_gather(ks, table, L, bs, KV_DIM)
+    vg = oracle.paged_gather(vs, table, L, bs, KV_DIM)
+    b = oracle.cached_attention(q, kg, vg, L, NQ, NKV, HD)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    ref = _numpy_attention(q, kg, vg, L, NQ, NKV, HD)
+    assert np.max(np.abs(a.astype(np.float64) - ref)) < 2e-3
+
+
+def test_paged_fp8_attention_vs_numpy_dequant():
+    bs, nblk, L = 32, 20, 555
+    rng = np.random.Generator(np.random.PCG64(97))
+    kc = rng.integers(0, 256, (nblk * bs, KV_DIM), dtype=np.uint8)
+    vc = rng.integers(0, 256, (nblk * bs, KV_DIM), dtype=np.uint8)
+    kc[(kc & 0x7F) == 0x7F] = 0  # no NaN codes
+    vc[(vc & 0x7F) == 0x7F] = 0
+    ksc = rng.uniform(0.001, 0.01, NKV).astype(np.float32)
+    vsc = rng.uniform(0.001, 0.01, NKV).astype(np.float32)
+    table = rng.permutation(nblk).astype(np.int32)
+    q = randn_f16(Q_DIM, 98)
+    ours = oracle.paged_attention_fp8(q, kc, vc, ksc, vsc, table, L, bs, NQ, NKV, HD)
+    lut = oracle.e4m3_decode_table().astype(np.float64)
+    kg = oracle.paged_gather(kc, table, L, bs, KV_DIM)
+    vg = oracle.paged_gather(vc, table, L, bs, KV_DIM)
+    kd = lut[kg] * np.repeat(ksc, HD)[None, :]
+    vd = lut[vg] * np.repeat(vsc, HD)[None, :]
+    ref = _numpy_attention(q, kd, vd, L, NQ, NKV, HD)
+    assert np.max(np.abs(ours.astype(np.float64) - ref)) < 2e-3
+
+
+def test_paged_write_fp8_matches_quantize():
+    rng = np.random.Generator(np.random.PCG64(99))
+    krow = randn_f16(KV_DIM, 100)
+    vrow = randn_f16(KV_DIM, 101)
+    ksc = rng.uniform(0.005, 0.02, NKV).astype(np.float32)
+    vsc = rng.uniform(0.005, 0.02, NKV).astype(np.float32)
+    ks = np.zeros((64, KV_DIM), np.uint8)
+    vs = np.zeros((64, KV_DIM), np.uint8)
+    oracle.paged_write_fp8(krow, vrow, ks, vs, 37, KV_DIM, HD, ksc, vsc)
+    for h in range(NKV):
+        sl = slice(h * HD, (h + 1) * HD)
+        assert np.array_equal(ks[37, sl], oracle.fp8_quantize(krow[sl], float(ksc[h])))
+        assert np.array_equal(vs[37, sl], oracle.fp8_quantize(vrow[sl], float(vsc[h])))
+    assert not ks[np.arange(64) != 37].any()
+
+
+def test_fixture_files_are_small():
+    for f in os.listdir(GOLDEN):
+        assert os.path.getsize(os.path.join(GOLDEN, f)) < 512 * 1024, f
+    h = hashlib.sha256(open(os.path.join(GOLDEN, "sdpa_cases.npz"), "rb").read()).hexdigest()
+    assert len(h) == 64
