@@ -59,6 +59,11 @@ __global__ void copy_blocks_kernel(uint8_t* __restrict__ base, size_t slab_bytes
     for (int v = threadIdx.x; v < vecs; v += blockDim.x) d[v] = s[v];
 }
 
+__global__ void add_i32_kernel(int32_t* __restrict__ p, int n, int32_t delta) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] += delta;
+}
+
 __global__ void fp8_quantize_kernel(const uint16_t* __restrict__ src, uint8_t* __restrict__ dst,
                                     size_t n, float scale) {
     const size_t stride = size_t(gridDim.x) * blockDim.x;
@@ -182,6 +187,15 @@ extern "C" int af_fp8_quantize(const void* src_f16, uint8_t* dst, size_t n, floa
 
 extern "C" int af_rt_fill_u32(void* dst, uint32_t value, size_t n_words, af_stream_t stream) {
     return fill_u32(dst, value, n_words, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_rt_add_i32(int32_t* d_values, int n, int32_t delta, af_stream_t stream) {
+    if (!d_values || n < 0) return AF_ERR_INVALID_ARG;
+    if (n == 0) return AF_OK;
+    hipLaunchKernelGGL(add_i32_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), d_values, n, delta);
+    AF_TRY_LAUNCH();
+    return AF_OK;
 }
 
 extern "C" int af_rt_fill_randn_f16(void* dst, size_t n, uint64_t seed, float stddev,

@@ -16,6 +16,14 @@ def device_count():
     return n.value if st == 0 else 0
 
 
+def set_device(index):
+    check(lib().af_rt_set_device(index), "af_rt_set_device")
+
+
+def add_i32(ptr, n, delta, stream=None):
+    check(lib().af_rt_add_i32(ptr, n, delta, _s(stream)), "af_rt_add_i32")
+
+
 def device_info():
     name = ctypes.create_string_buffer(256)
     arch = ctypes.create_string_buffer(64)

@@ -39,6 +39,9 @@ int af_rt_memcpy_d2h(void* dst, const void* src, size_t bytes, af_stream_t strea
 int af_rt_memcpy_d2d(void* dst, const void* src, size_t bytes, af_stream_t stream);
 /* Fill with a 32-bit pattern (a kernel, safe inside stream capture). */
 int af_rt_fill_u32(void* dst, uint32_t value, size_t n_words, af_stream_t stream);
+/* d_values[i] += delta for i < n (a kernel: a captured decode step uses it to
+ * advance its device-resident position and length). */
+int af_rt_add_i32(int32_t* d_values, int n, int32_t delta, af_stream_t stream);
 /* Synthetic N(0,1) fp16 data on the device: counter-based hash + Box-Muller.
  * Deterministic in (seed, index); for bench-scale inputs only. */
 int af_rt_fill_randn_f16(void* dst, size_t n, uint64_t seed, float stddev, af_stream_t stream);

@@ -29,3 +29,20 @@ def contiguous_case(max_seq, filled, seed, nq=NQ, nkv=NKV, hd=HD):
     k[:filled] = randn_f16((filled, kv_dim), seed + 1)
     v[:filled] = randn_f16((filled, kv_dim), seed + 2)
     return qkv, k, v
+
+
+# Attention tolerance: fp16 KV within max-abs 2e-3 /
+# rel 1e-2, FP8 KV within 5e-2, read elementwise as |got - ref| <= atol + rtol*|ref|.
+ATOL_F16, RTOL_F16 = 2e-3, 1e-2
+ATOL_FP8, RTOL_FP8 = 5e-2, 1e-2
+
+
+def assert_attn_close(got, ref, atol=ATOL_F16, rtol=RTOL_F16, what=""):
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(g)), f"{what}: non-finite output"
+    err = np.abs(g - r)
+    bad = err > atol + rtol * np.abs(r)
+    assert not bad.any(), (f"{what}: {bad.sum()} elements outside atol={atol} rtol={rtol}; "
+                           f"max abs err {err.max():.3e} at {int(err.argmax())}")
+    return float(err.max())

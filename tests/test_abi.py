@@ -1,0 +1,120 @@
+"""The C ABI library builds, loads without a GPU, and exports every symbol the
+public headers declare; the C++ headers compile and link in a host program."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import atomflow_amd
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = ["include/af_kv.h", "include/af_runtime.h"]
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = open(os.path.join(ROOT, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(af_\w+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", atomflow_amd.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_every_declared_function_is_exported():
+    decl = declared_functions()
+    assert len(decl) > 50
+    missing = decl - exported_symbols()
+    assert not missing, sorted(missing)
+
+
+def test_ctypes_prototypes_cover_the_headers():
+    from atomflow_amd import _abi
+
+    assert declared_functions() == set(_abi.PROTOTYPES), (
+        sorted(declared_functions() ^ set(_abi.PROTOTYPES)))
+
+
+def test_library_loads_and_reports_status_strings():
+    lib = atomflow_amd.lib()
+    assert lib.af_version() > 0
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+        assert lib.af_status_string(code)
+    assert lib.af_status_string(-1).decode() == "block pool exhausted"
+
+
+def test_host_only_entry_points_without_gpu():
+    from atomflow_amd import kv
+    import oracle
+
+    c, s = kv.rope_table_host(300, 128, 500000.0)
+    oc, os_ = oracle.rope_table(300, 128, 500000.0)
+    assert (c.view("u4") == oc.view("u4")).all() and (s.view("u4") == os_.view("u4")).all()
+    lib = atomflow_amd.lib()
+    assert lib.af_attention_workspace_size(1, 24, 8, 128, 64) > 64 * 1024
+    assert lib.af_attention_workspace_size(0, 24, 8, 128, 64) == 0
+    p = kv.make_pool(0, atomflow_amd.AF_KV_FP16, 16, 28, 8, 128, 1000)
+    assert kv.pool_bytes(p) == 28 * 2 * 1000 * 16 * 1024 * 2
+    # argument validation happens before any device call
+    assert lib.af_rope_append(None, None, None, None, None, 0, None, 16, 24, 8, 128, None,
+                              None) == atomflow_amd.AF_ERR_INVALID_ARG
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(atomflow_amd, "_lib", None)
+    monkeypatch.setattr(atomflow_amd, "LIB_PATH", "/nonexistent/libatomflow_kv.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        atomflow_amd.lib()
+
+
+def test_cpp_headers_compile_and_link(tmp_path):
+    src = tmp_path / "t.cpp"
+    src.write_text(r'''
+#include "core/view.h"
+#include "memory/block_manager.h"
+#include "memory/memory_planner.h"
+#include <cstdio>
+#include <vector>
+int main() {
+    using namespace atomflow::server;
+    BlockManager bm;
+    PoolConfig c; c.total_blocks = 8; c.block_size = 16; c.n_layers = 2; c.n_kv_heads = 8;
+    c.head_dim = 128;
+    bm.initialize(c, false, nullptr);
+    if (bm.allocate_block() != 0 || bm.num_free_blocks() != 7) return 1;
+    bm.free_block(0);
+    bool threw = false;
+    try { bm.free_block(0); } catch (const std::invalid_argument&) { threw = true; }
+    if (!threw) return 2;
+    int s = bm.create_sequence();
+    AppendSlot a;
+    if (bm.append_token(s, &a) != 0 || a.position != 0 || a.slot != 0) return 3;
+    std::vector<char> arena(1024);
+    MemoryPlanner mp(arena.data(), arena.size());
+    float* f = mp.allocate<float>(3);
+    if (mp.get_offset() != 16 || !f) return 4;
+    threw = false;
+    try { mp.allocate<char>(2000); } catch (const std::runtime_error&) { threw = true; }
+    if (!threw) return 5;
+    View v = create_contiguous_view(nullptr, DataType::FP16, {32769, 1024});
+    if (v.strides[0] != 1024 || v.offset(32768, 5) != size_t(32768) * 1024 + 5) return 6;
+    View big = create_contiguous_view(nullptr, DataType::FP8_E4M3, {28, 2, 50000 * 32, 1024});
+    if (big.numel() != int64_t(28) * 2 * 50000 * 32 * 1024) return 7;
+    std::puts("ok");
+    return 0;
+}
+''')
+    exe = tmp_path / "t"
+    libdir = os.path.dirname(atomflow_amd.LIB_PATH)
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"), str(src),
+                    "-L", libdir, "-latomflow_kv", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
