@@ -46,6 +46,8 @@ PROTOTYPES = {
     "af_attention_workspace_init": (I, [P, SZ, P]),
     "af_attention_default_splits": (I, [I, I, I]),
     "af_cached_attention_ex": (I, [P, P, P, P, I, P, I, I, I, I, I, P, SZ, P]),
+    "af_decode_attention_fused": (I, [P, P, P, P, P, I, P, I, P, I, I, I, I, P, SZ, P, P]),
+    "af_paged_decode_fused": (I, [P, I, PPOOL, I, P, P, P, P, I, P, I, I, P, I, I, I, P, SZ, P]),
     "af_kv_pool_bytes": (SZ, [PPOOL]),
     "af_paged_rope_append": (I, [P, I, PPOOL, I, P, P, P, P, I, I, P]),
     "af_paged_attention": (I, [P, I, PPOOL, I, P, I, P, I, I, P, I, I, I, P, SZ, P]),

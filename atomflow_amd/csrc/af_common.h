@@ -25,8 +25,9 @@
 namespace af {
 
 constexpr int kWave = 64;
-// Longest split grid; bounds the per-(sequence, head) partial buffers.
-constexpr int kMaxSplits = 256;
+// Longest split grid; bounds the per-(sequence, head) partial buffers and lets
+// the combine read every partial in one round of loads.
+constexpr int kMaxSplits = 64;
 // Fewest tokens a split may own: below this the partial (m, l, o[]) traffic and
 // the combine cost more than the split saves.
 constexpr int kMinSpan = 64;

@@ -85,19 +85,37 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ int ceil_div_d(int a, int b) { return (a + b - 1) / b; }
 
+// Agent-scope (all XCDs) relaxed atomic store / load of split-K partials.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct AttnArgs {
-    const uint16_t* q;
+    uint16_t* q;       // query rows; pre-RoPE qkv rows in the fused kernel
     int64_t q_stride;  // elements between sequences
-    const uint8_t* k;  // contiguous cache base, or the layer's K slab
-    const uint8_t* v;
+    uint8_t* k;        // contiguous cache base, or the layer's K slab
+    uint8_t* v;
     int64_t row_bytes;  // bytes between consecutive token rows (kv_dim * elem)
     const int32_t* tables;
     int32_t max_blocks;
     int32_t block_shift;
     int64_t total_blocks;
-    const int32_t* seq_lens;  // [batch] or NULL -> seq_len_host
+    const int32_t* seq_lens;  // unfused: [batch] lengths, or NULL -> seq_len_host
     int32_t seq_len_host;
-    int32_t max_seq_len;
+    int32_t max_seq_len;      // bound on every length (rows addressable)
+    // fused RoPE + append
+    const int32_t* positions;  // [batch] positions, or NULL -> pos_host
+    int32_t pos_host;
+    const int64_t* slots;      // paged: [batch] physical rows of the new token
+    int64_t max_rows;          // rows in the destination
+    const float* cos_t;
+    const float* sin_t;
+    int32_t max_pos;           // rows in the RoPE table
+    int32_t* d_status;
+    // output
     uint16_t* out;
     int64_t out_stride;
     int32_t n_kv_heads;
@@ -105,9 +123,9 @@ struct AttnArgs {
     int32_t min_span;
     float qk_scale;       // log2(e) / sqrt(head_dim)
     const float* scales;  // FP8: [2][n_kv_heads] (K, V) of this layer
-    float* part_o;
-    float* part_ml;
-    uint32_t* counters;
+    float* part_o;        // [batch][n_kv_heads][splits][GROUP * head_dim]
+    float* part_ml;       // [batch][n_kv_heads][splits][2 * GROUP]  (m..., l...)
+    uint32_t* counters;   // [batch][n_kv_heads]
 };
 
 template <int HD, bool FP8>
@@ -122,19 +140,62 @@ struct Layout {
     __device__ static int dim(int i, int j, int u) { return (i * 128 + j * 16) / kElem + u; }
 };
 
-template <int HD, int GROUP, bool FP8, bool PAGED>
+// One rotation of pair (x, y) by (c, s): separately rounded fp32 products and
+// sum, then fp16 round-to-nearest-even — the reference's rope_kernel numerics
+// (src/kernel/rope.cu:34-35); contraction into an FMA is disabled.
+__device__ __forceinline__ void rotate_pair(uint16_t x, uint16_t y, float c, float s,
+                                            uint16_t& xo, uint16_t& yo) {
+#pragma clang fp contract(off)
+    const float xf = float(__builtin_bit_cast(f16, x)), yf = float(__builtin_bit_cast(f16, y));
+    const float xc = xf * c;
+    const float ys = yf * s;
+    const float xs = xf * s;
+    const float yc = yf * c;
+    xo = __builtin_bit_cast(uint16_t, f16(xc - ys));
+    yo = __builtin_bit_cast(uint16_t, f16(xs + yc));
+}
+
+__device__ __forceinline__ uint32_t quantize_fp8_dev(uint16_t h, float scale) {
+    float v = float(__builtin_bit_cast(f16, h)) / scale;
+    v = fminf(fmaxf(v, -448.0f), 448.0f);
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x43e00000u) return sign | 0x7eu;
+    if (a < 0x3c800000u) return sign | uint32_t(__builtin_rintf(__builtin_bit_cast(float, a) * 512.0f));
+    const int e = int(a >> 23) - 127;
+    const uint32_t mant = a & 0x7fffffu;
+    uint32_t m3 = mant >> 20;
+    const uint32_t rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3 += 1;
+    return sign | ((uint32_t(e + 7) << 3) + m3);
+}
+
+__device__ __forceinline__ uint64_t load_agent_u64(const float* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup = (sequence b, KV head h, split). See the file comment.
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a) {
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
     constexpr int EPL = LY::kEpl;
-    constexpr int R = 2;                           // token rows per lane per chunk
-    constexpr int CHUNK = R * kRowsPerStep;        // tokens per wave chunk (16)
+    constexpr int R = 2;                     // token rows per lane per chunk
+    constexpr int CHUNK = R * kRowsPerStep;  // tokens per wave chunk (16)
+    constexpr int GHD = GROUP * HD;
+    constexpr int PER64 = (GHD / 2 + 63) / 64;             // 64-bit partial slots per lane
+    constexpr int SB = (24 / PER64) < 1 ? 1 : ((24 / PER64) > 8 ? 8 : (24 / PER64));
 
-    __shared__ float s_o[kWaves][GROUP][HD];
+    __shared__ float s_o[kWaves][GHD];
     __shared__ float s_m[kWaves][GROUP];
     __shared__ float s_l[kWaves][GROUP];
     __shared__ int32_t s_tab[PAGED ? kMaxTableLds : 1];
-    __shared__ float s_w[GROUP][kMaxSplits];
+    __shared__ float s_ml[2 * GROUP * kMaxSplits];  // (m, l) of every split, then weights
+    __shared__ float s_wt[GROUP][kMaxSplits];
+    __shared__ uint16_t s_q[FUSED ? GHD : 1];
+    __shared__ uint4 s_new[FUSED ? 2 * LY::kRowBytes / 16 : 1];  // new token's K then V row (head h)
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
@@ -145,14 +206,25 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     id /= a.n_kv_heads;
     const int split = id % a.num_splits;
     const int b = id / a.num_splits;
-    const int nq = a.n_kv_heads * GROUP;
+    const int nkv = a.n_kv_heads;
 
-    int L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
-    L = min(L, a.max_seq_len);
-    uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(h) * GROUP * HD;
+    int L, pos = 0;
+    if constexpr (FUSED) {
+        pos = a.positions ? a.positions[b] : a.pos_host;
+        const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
+        if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
+            if (tid == 0 && split == 0 && h == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
+            return;  // out-of-range append: nothing is written
+        }
+        L = pos + 1;
+    } else {
+        L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
+        L = min(L, a.max_seq_len);
+    }
+    uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(h) * GHD;
     if (L <= 0) {  // empty sequence: defined as a zero output
         if (split == 0)
-            for (int o = tid; o < GROUP * HD; o += kThreads) out_b[o] = 0;
+            for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
     int span = max(ceil_div_d(L, a.num_splits), a.min_span);
@@ -161,6 +233,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     if (split >= n_active) return;
     const int t_begin = split * span;
     const int t_end = min(L, t_begin + span);
+    const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
 
     // ---- stage this split's block-table entries (paged) --------------------
     int tab_base = 0;
@@ -177,46 +250,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         __syncthreads();
     }
 
-    // ---- query fragment: the lane's EPL dims of each of the GROUP heads ----
-    half2_t qv[GROUP][EPL / 2];
-    {
-        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GROUP * HD;
-#pragma unroll
-        for (int gh = 0; gh < GROUP; ++gh)
-#pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint16_t* src = qb + gh * HD + LY::dim(i, j, 0);
-#pragma unroll
-                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w) {
-                    const uint4 raw = *reinterpret_cast<const uint4*>(src + w * 8);
-                    const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
-                    qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
-                    qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
-                    qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
-                    qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
-                }
-            }
-    }
-
-    float qk_scale = a.qk_scale;
-    float v_scale = 1.0f;
-    if constexpr (FP8) {
-        qk_scale *= a.scales[h];
-        v_scale = a.scales[a.n_kv_heads + h];
-    }
-
-    float m_run[GROUP], l_run[GROUP], acc[GROUP][EPL];
-#pragma unroll
-    for (int gh = 0; gh < GROUP; ++gh) {
-        m_run[gh] = -INFINITY;
-        l_run[gh] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[gh][e] = 0.f;
-    }
-
     const int n_chunks = (t_end - t_begin + CHUNK - 1) / CHUNK;
     const uint8_t* kbase = a.k + size_t(h) * LY::kRowBytes + j * 16;
     const uint8_t* vbase = a.v + size_t(h) * LY::kRowBytes + j * 16;
+    // Rows that may be read from memory: [0, L) unfused; [0, L-1) fused (row
+    // L-1 is the token being appended and comes from LDS).
+    const int last_row = FUSED ? max(L - 2, 0) : L - 1;
 
     struct Chunk {
         uint4 k[R][LOADS];
@@ -224,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     };
 
     auto row_offset = [&](int t) -> int64_t {
-        const int tc = min(t, L - 1);  // rows past L are read from row L-1 and masked
+        const int tc = min(t, last_row);  // rows past the range are read in-bounds and masked
         if constexpr (PAGED) {
             const int mask = (1 << a.block_shift) - 1;
             const int64_t blk = s_tab[(tc >> a.block_shift) - tab_base];
@@ -247,8 +286,130 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         }
     };
 
-    auto process_chunk = [&](const Chunk& c, int chunk) {
+    // First chunk in flight before the query set-up.
+    Chunk ca, cb;
+    int c = wave;
+    if (c < n_chunks) load_chunk(ca, c);
+
+    // ---- query fragment -----------------------------------------------------
+    half2_t qv[GROUP][EPL / 2];
+    if constexpr (FUSED) {
+        // RoPE of the GROUP query heads into LDS (every split computes the same
+        // bits); the owner also rotates K head h, and stages the new K/V row.
+        const int half = HD / 2;
+        const uint16_t* qkv = a.q + size_t(b) * a.q_stride;
+        const float* crow = a.cos_t + size_t(pos) * half;
+        const float* srow = a.sin_t + size_t(pos) * half;
+        const int nq = nkv * GROUP;
+        for (int it = tid; it < (GROUP + 1) * half; it += kThreads) {
+            const int gh = it / half, d = it % half;
+            if (gh < GROUP) {
+                const uint16_t* src = qkv + size_t(h * GROUP + gh) * HD;
+                uint16_t xo, yo;
+                rotate_pair(src[d], src[d + half], crow[d], srow[d], xo, yo);
+                s_q[gh * HD + d] = xo;
+                s_q[gh * HD + d + half] = yo;
+            } else if (owner) {
+                uint16_t* kh = const_cast<uint16_t*>(qkv) + size_t(nq + h) * HD;
+                uint16_t xo, yo;
+                rotate_pair(kh[d], kh[d + half], crow[d], srow[d], xo, yo);
+                kh[d] = xo;  // K is rotated in place (only this workgroup reads K head h)
+                kh[d + half] = yo;
+                if constexpr (FP8) {
+                    uint8_t* kn = reinterpret_cast<uint8_t*>(s_new);
+                    kn[d] = uint8_t(quantize_fp8_dev(xo, a.scales[h]));
+                    kn[d + half] = uint8_t(quantize_fp8_dev(yo, a.scales[h]));
+                } else {
+                    uint16_t* kn = reinterpret_cast<uint16_t*>(s_new);
+                    kn[d] = xo;
+                    kn[d + half] = yo;
+                }
+            }
+        }
+        if (owner) {
+            const uint16_t* vh = qkv + size_t(nq + nkv + h) * HD;
+            for (int d = tid; d < HD; d += kThreads) {
+                if constexpr (FP8) {
+                    reinterpret_cast<uint8_t*>(s_new)[LY::kRowBytes + d] =
+                        uint8_t(quantize_fp8_dev(vh[d], a.scales[nkv + h]));
+                } else {
+                    reinterpret_cast<uint16_t*>(s_new)[HD + d] = vh[d];
+                }
+            }
+        }
+        __syncthreads();
+        if (owner) {  // append: K/V row of head h to the destination row
+            const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
+            constexpr int V16 = LY::kRowBytes / 16;
+            if (tid < 2 * V16) {
+                uint8_t* dst = (tid < V16 ? a.k : a.v) + row * a.row_bytes +
+                               size_t(h) * LY::kRowBytes + (tid % V16) * 16;
+                *reinterpret_cast<uint4*>(dst) = s_new[tid];
+            }
+        }
+#pragma unroll
+        for (int gh = 0; gh < GROUP; ++gh)
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i)
+#pragma unroll
+                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w) {
+                    const uint4 raw =
+                        *reinterpret_cast<const uint4*>(&s_q[gh * HD + LY::dim(i, j, 0) + w * 8]);
+                    const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
+                    qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
+                    qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
+                    qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
+                    qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
+                }
+    } else {
+        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
+#pragma unroll
+        for (int gh = 0; gh < GROUP; ++gh)
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const uint16_t* src = qb + gh * HD + LY::dim(i, j, 0);
+#pragma unroll
+                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w) {
+                    const uint4 raw = *reinterpret_cast<const uint4*>(src + w * 8);
+                    const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
+                    qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
+                    qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
+                    qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
+                    qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
+                }
+            }
+    }
+
+    float qk_scale = a.qk_scale;
+    float v_scale = 1.0f;
+    if constexpr (FP8) {
+        qk_scale *= a.scales[h];
+        v_scale = a.scales[nkv + h];
+    }
+
+    float m_run[GROUP], l_run[GROUP], acc[GROUP][EPL];
+#pragma unroll
+    for (int gh = 0; gh < GROUP; ++gh) {
+        m_run[gh] = -INFINITY;
+        l_run[gh] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[gh][e] = 0.f;
+    }
+
+    auto process_chunk = [&](Chunk& c, int chunk) {
         const int t0 = t_begin + chunk * CHUNK + g;
+        if constexpr (FUSED) {
+            // The new token (and padding past it) takes the appended row from LDS.
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (t0 + r * kRowsPerStep >= L - 1) {
+#pragma unroll
+                    for (int i = 0; i < LOADS; ++i) {
+                        c.k[r][i] = s_new[(i * 128 + j * 16) / 16];
+                        c.v[r][i] = s_new[LY::kRowBytes / 16 + (i * 128 + j * 16) / 16];
+                    }
+                }
+        }
         float s[R][GROUP];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -340,19 +501,20 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         }
     };
 
-    // ---- main loop: wave w takes chunks w, w+4, ...; one chunk prefetched ---
-    {
-        Chunk ca, cb;
-        int c = wave;
-        if (c < n_chunks) load_chunk(ca, c);
-        while (c < n_chunks) {
-            if (c + kWaves < n_chunks) load_chunk(cb, c + kWaves);
+    // ---- main loop: wave w takes chunks w, w+4, ... -------------------------
+    // The next chunk's loads are issued before the current chunk is consumed.
+    // The prefetch is unconditional (the last one re-reads the wave's final
+    // chunk, an L2 hit) so no control-flow join forces a full vmcnt wait.
+    if (c < n_chunks) {
+        for (;;) {
+            load_chunk(cb, min(c + kWaves, n_chunks - 1));
             process_chunk(ca, c);
             c += kWaves;
             if (c >= n_chunks) break;
-            if (c + kWaves < n_chunks) load_chunk(ca, c + kWaves);
+            load_chunk(ca, min(c + kWaves, n_chunks - 1));
             process_chunk(cb, c);
             c += kWaves;
+            if (c >= n_chunks) break;
         }
     }
 
@@ -380,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             for (int i = 0; i < LOADS; ++i)
 #pragma unroll
                 for (int u = 0; u < LY::kElemsPerLoad; ++u)
-                    s_o[wave][gh][LY::dim(i, j, u)] = acc[gh][i * LY::kElemsPerLoad + u];
+                    s_o[wave][gh * HD + LY::dim(i, j, u)] = acc[gh][i * LY::kElemsPerLoad + u];
             if (lane == 0) {
                 s_m[wave][gh] = m_run[gh];
                 s_l[wave][gh] = l_run[gh];
@@ -390,8 +552,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     __syncthreads();
 
     // ---- merge the 4 waves; write the output or this split's partial -------
-    for (int o = tid; o < GROUP * HD; o += kThreads) {
-        const int gh = o / HD, d = o % HD;
+    const size_t rec = (size_t(b) * nkv + h) * a.num_splits;  // first record of (b, h)
+    for (int o = tid; o < GHD; o += kThreads) {
+        const int gh = o / HD;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][gh]);
@@ -400,60 +563,114 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         for (int w = 0; w < kWaves; ++w) {
             const float f = fast_exp2(s_m[w][gh] - M);  // 0 for a wave that saw no token
             lsum += f * s_l[w][gh];
-            osum += f * s_o[w][gh][d];
+            osum += f * s_o[w][o];
         }
         if (n_active == 1) {
             out_b[o] = __builtin_bit_cast(uint16_t, f16(osum * v_scale / lsum));
         } else {
-            const size_t qh = size_t(b) * nq + size_t(h) * GROUP + gh;
-            const size_t slot = qh * a.num_splits + split;
-            a.part_o[slot * HD + d] = osum * v_scale;
-            if (d == 0) {
-                a.part_ml[slot * 2 + 0] = M;
-                a.part_ml[slot * 2 + 1] = lsum;
+            store_agent(a.part_o + (rec + split) * GHD + o, osum * v_scale);
+            if (o % HD == 0) {
+                store_agent(a.part_ml + (rec + split) * 2 * GROUP + gh, M);
+                store_agent(a.part_ml + (rec + split) * 2 * GROUP + GROUP + gh, lsum);
             }
         }
     }
-    if (n_active == 1) return;
+    if (n_active == 1) {
+        if constexpr (FUSED) {  // the only reader of Q heads h*GROUP.. : rotate in place now
+            uint16_t* qd = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
+            for (int o = tid; o < GHD; o += kThreads) qd[o] = s_q[o];
+        }
+        return;
+    }
 
     // ---- arrival: the last split of (b, h) to finish combines --------------
-    __threadfence();  // each wave publishes its partial stores device-wide
+    // Partials are agent-scope atomic stores (written through to the level
+    // where every XCD sees them); each wave waits until its stores are
+    // performed before the barrier, then one relaxed agent-scope increment
+    // publishes the split. The last arrival reads the partials with
+    // agent-scope atomic loads. This replaces a device-wide fence, whose L2
+    // write-back + invalidate per workgroup costs far more than the kernel.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        uint32_t* ctr = a.counters + size_t(b) * a.n_kv_heads + h;
-        const uint32_t prev = atomicAdd(ctr, 1u);
+        uint32_t* ctr = a.counters + size_t(b) * nkv + h;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         const int last = prev == uint32_t(n_active - 1);
-        if (last) *ctr = 0u;  // every other split has arrived: safe to re-arm
+        if (last)  // every other split has arrived: re-arm for the next launch
+            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = last;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();  // acquire the other splits' partials
 
-    for (int gh = wave; gh < GROUP; gh += kWaves) {
-        const size_t qh = size_t(b) * nq + size_t(h) * GROUP + gh;
-        const float* ml = a.part_ml + qh * a.num_splits * 2;
-        float mx = -INFINITY;
-        for (int s = lane; s < n_active; s += 64) mx = fmaxf(mx, ml[s * 2]);
-        mx = wave_max(mx);
-        float ls = 0.f;
-        for (int s = lane; s < n_active; s += 64) {
-            const float w = fast_exp2(ml[s * 2] - mx);
-            s_w[gh][s] = w;
-            ls += w * ml[s * 2 + 1];
+    // ---- combine: every partial load is issued before any is used ----------
+    // Wave w owns splits w*SB .. w*SB+SB-1 of each round of 4*SB splits; lane
+    // slot i holds floats 2*(lane + 64 i) and +1 of a record (GROUP*HD floats).
+    const float* ml = a.part_ml + rec * 2 * GROUP;
+    for (int e = tid; e < n_active * 2 * GROUP; e += kThreads) s_ml[e] = load_agent(ml + e);
+    float racc[PER64][2];
+#pragma unroll
+    for (int i = 0; i < PER64; ++i) racc[i][0] = racc[i][1] = 0.f;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    for (int base = 0; base < n_active; base += kWaves * SB) {
+        uint64_t val[SB][PER64];
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+            const int sp = base + wave_u * SB + k;  // wave-uniform: scalar base address
+            const float* rp = a.part_o + (rec + min(sp, n_active - 1)) * GHD;
+#pragma unroll
+            for (int i = 0; i < PER64; ++i) {
+                const int q2 = min(lane + 64 * i, GHD / 2 - 1);
+                val[k][i] = load_agent_u64(rp + 2 * q2);
+            }
         }
-        ls = wave_sum(ls);
-        const float inv = 1.0f / ls;
-        for (int s = lane; s < n_active; s += 64) s_w[gh][s] *= inv;
+        if (base == 0) {  // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s
+            __syncthreads();
+            for (int gh = wave; gh < GROUP; gh += kWaves) {
+                float mx = -INFINITY;
+                for (int sp = lane; sp < n_active; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
+                mx = wave_max(mx);
+                float ls = 0.f;
+                for (int sp = lane; sp < n_active; sp += 64)
+                    ls += fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * s_ml[sp * 2 * GROUP + GROUP + gh];
+                const float inv = 1.0f / wave_sum(ls);
+                for (int sp = lane; sp < n_active; sp += 64)
+                    s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * inv;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+            const int sp = base + wave_u * SB + k;
+            if (sp >= n_active) break;
+#pragma unroll
+            for (int i = 0; i < PER64; ++i) {
+                const int q2 = lane + 64 * i;
+                if (q2 < GHD / 2) {
+                    const float w = s_wt[(2 * q2) / HD][sp];
+                    racc[i][0] = fmaf(w, __builtin_bit_cast(float, uint32_t(val[k][i])), racc[i][0]);
+                    racc[i][1] = fmaf(w, __builtin_bit_cast(float, uint32_t(val[k][i] >> 32)), racc[i][1]);
+                }
+            }
+        }
+    }
+    // cross-wave sum, then the fp16 output (and, fused, the rotated Q in place)
+#pragma unroll
+    for (int i = 0; i < PER64; ++i) {
+        const int q2 = lane + 64 * i;
+        if (q2 < GHD / 2) {
+            s_o[wave][2 * q2] = racc[i][0];
+            s_o[wave][2 * q2 + 1] = racc[i][1];
+        }
     }
     __syncthreads();
-    for (int o = tid; o < GROUP * HD; o += kThreads) {
-        const int gh = o / HD, d = o % HD;
-        const size_t qh = size_t(b) * nq + size_t(h) * GROUP + gh;
-        const float* po = a.part_o + qh * a.num_splits * HD + d;
+    for (int o = tid; o < GHD; o += kThreads) {
         float x = 0.f;
-        for (int s = 0; s < n_active; ++s) x = fmaf(s_w[gh][s], po[size_t(s) * HD], x);
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) x += s_o[w][o];
         out_b[o] = __builtin_bit_cast(uint16_t, f16(x));
+        if constexpr (FUSED) a.q[size_t(b) * a.q_stride + size_t(h) * GHD + o] = s_q[o];
     }
 }
 
@@ -466,38 +683,45 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 namespace af {
 namespace {
 
-template <int HD, int GROUP, bool FP8, bool PAGED>
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED>
 hipError_t launch_attn(const AttnArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED>), dim3(grid), dim3(kThreads), 0,
-                       s, a);
+    hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED, FUSED>), dim3(grid),
+                       dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
-template <int HD, bool FP8, bool PAGED>
+template <int HD, bool FP8, bool PAGED, bool FUSED>
 int dispatch_group(const AttnArgs& a, int group, int grid, hipStream_t s) {
     switch (group) {
-        case 1: return int(launch_attn<HD, 1, FP8, PAGED>(a, grid, s));
-        case 2: return int(launch_attn<HD, 2, FP8, PAGED>(a, grid, s));
-        case 3: return int(launch_attn<HD, 3, FP8, PAGED>(a, grid, s));
-        case 4: return int(launch_attn<HD, 4, FP8, PAGED>(a, grid, s));
-        case 8: return int(launch_attn<HD, 8, FP8, PAGED>(a, grid, s));
+        case 1: return int(launch_attn<HD, 1, FP8, PAGED, FUSED>(a, grid, s));
+        case 2: return int(launch_attn<HD, 2, FP8, PAGED, FUSED>(a, grid, s));
+        case 3: return int(launch_attn<HD, 3, FP8, PAGED, FUSED>(a, grid, s));
+        case 4: return int(launch_attn<HD, 4, FP8, PAGED, FUSED>(a, grid, s));
+        case 8: return int(launch_attn<HD, 8, FP8, PAGED, FUSED>(a, grid, s));
         default: return AF_ERR_UNSUPPORTED;
     }
 }
 
-int dispatch(const AttnArgs& a, int head_dim, int group, bool fp8, bool paged, int grid,
-             hipStream_t s) {
+template <bool FUSED>
+int dispatch_fused(const AttnArgs& a, int head_dim, int group, bool fp8, bool paged, int grid,
+                   hipStream_t s) {
     if (fp8) {
         if (!paged || head_dim != 128) return AF_ERR_UNSUPPORTED;
-        return dispatch_group<128, true, true>(a, group, grid, s);
+        return dispatch_group<128, true, true, FUSED>(a, group, grid, s);
     }
     if (head_dim == 128)
-        return paged ? dispatch_group<128, false, true>(a, group, grid, s)
-                     : dispatch_group<128, false, false>(a, group, grid, s);
+        return paged ? dispatch_group<128, false, true, FUSED>(a, group, grid, s)
+                     : dispatch_group<128, false, false, FUSED>(a, group, grid, s);
     if (head_dim == 64)
-        return paged ? dispatch_group<64, false, true>(a, group, grid, s)
-                     : dispatch_group<64, false, false>(a, group, grid, s);
+        return paged ? dispatch_group<64, false, true, FUSED>(a, group, grid, s)
+                     : dispatch_group<64, false, false, FUSED>(a, group, grid, s);
     return AF_ERR_UNSUPPORTED;
+}
+
+int dispatch(const AttnArgs& a, int head_dim, int group, bool fp8, bool paged, bool fused,
+             int grid, hipStream_t s) {
+    return fused ? dispatch_fused<true>(a, head_dim, group, fp8, paged, grid, s)
+                 : dispatch_fused<false>(a, head_dim, group, fp8, paged, grid, s);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -608,15 +832,15 @@ static int check_heads(int head_dim, int n_q_heads, int n_kv_heads) {
     return AF_OK;
 }
 
-extern "C" int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache,
-                                      void* out, int seq_len, const int32_t* d_seq_len,
-                                      int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,
-                                      int num_splits, void* workspace, size_t workspace_bytes,
-                                      af_stream_t stream) {
+static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_cache, void* out,
+                                int seq_len, const int32_t* d_seq_len, int max_seq_len,
+                                int head_dim, int n_q_heads, int n_kv_heads, int num_splits,
+                                void* workspace, size_t workspace_bytes, bool fused,
+                                const float* cos_table, const float* sin_table, int pos,
+                                const int32_t* d_pos, int32_t* d_status, hipStream_t stream) {
     if (!q || !k_cache || !v_cache || !out || max_seq_len <= 0) return AF_ERR_INVALID_ARG;
     if (int st = check_heads(head_dim, n_q_heads, n_kv_heads)) return st;
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return AF_ERR_INVALID_ARG;
-    if (!d_seq_len && (seq_len < 0 || seq_len > max_seq_len)) return AF_ERR_OUT_OF_RANGE;
     if (num_splits <= 0) num_splits = default_splits(max_seq_len, 1, n_kv_heads);
     if (num_splits > kMaxSplits) return AF_ERR_INVALID_ARG;
     if (n_kv_heads > kMaxCounters) return AF_ERR_UNSUPPORTED;
@@ -624,14 +848,23 @@ extern "C" int af_cached_attention_ex(const void* q, const void* k_cache, const 
         return AF_ERR_WORKSPACE;
     const AttnWorkspace w = attn_workspace_carve(workspace, 1, n_q_heads, num_splits);
     AttnArgs a{};
-    a.q = static_cast<const uint16_t*>(q);
-    a.q_stride = int64_t(n_q_heads) * head_dim;
-    a.k = static_cast<const uint8_t*>(k_cache);
-    a.v = static_cast<const uint8_t*>(v_cache);
+    a.q = static_cast<uint16_t*>(q);
+    a.q_stride = q_stride;
+    a.k = static_cast<uint8_t*>(k_cache);
+    a.v = static_cast<uint8_t*>(v_cache);
     a.row_bytes = int64_t(n_kv_heads) * head_dim * 2;
     a.seq_lens = d_seq_len;
     a.seq_len_host = seq_len;
     a.max_seq_len = max_seq_len;
+    if (fused) {
+        a.positions = d_pos;
+        a.pos_host = pos;
+        a.max_rows = max_seq_len;
+        a.cos_t = cos_table;
+        a.sin_t = sin_table;
+        a.max_pos = max_seq_len;  // the table covers every cache row
+        a.d_status = d_status;
+    }
     a.out = static_cast<uint16_t*>(out);
     a.out_stride = int64_t(n_q_heads) * head_dim;
     a.n_kv_heads = n_kv_heads;
@@ -641,9 +874,36 @@ extern "C" int af_cached_attention_ex(const void* q, const void* k_cache, const 
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.counters = w.counters;
-    const int grid = num_splits * n_kv_heads;
-    return dispatch(a, head_dim, n_q_heads / n_kv_heads, false, false, grid,
-                    static_cast<hipStream_t>(stream));
+    return dispatch(a, head_dim, n_q_heads / n_kv_heads, false, false, fused,
+                    num_splits * n_kv_heads, stream);
+}
+
+extern "C" int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache,
+                                      void* out, int seq_len, const int32_t* d_seq_len,
+                                      int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,
+                                      int num_splits, void* workspace, size_t workspace_bytes,
+                                      af_stream_t stream) {
+    if (!d_seq_len && (seq_len < 0 || seq_len > max_seq_len)) return AF_ERR_OUT_OF_RANGE;
+    return contiguous_attention(const_cast<void*>(q), n_q_heads * head_dim,
+                                const_cast<void*>(k_cache), const_cast<void*>(v_cache), out,
+                                seq_len, d_seq_len, max_seq_len, head_dim, n_q_heads, n_kv_heads,
+                                num_splits, workspace, workspace_bytes, false, nullptr, nullptr, 0,
+                                nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_decode_attention_fused(void* qkv_out, void* k_cache, void* v_cache,
+                                         const float* cos_table, const float* sin_table, int pos,
+                                         const int32_t* d_pos, int max_seq, void* out,
+                                         int n_q_heads, int n_kv_heads, int head_dim,
+                                         int num_splits, void* workspace, size_t workspace_bytes,
+                                         int32_t* d_status, af_stream_t stream) {
+    if (!cos_table || !sin_table || !aligned16(cos_table) || !aligned16(sin_table))
+        return AF_ERR_INVALID_ARG;
+    if (!d_pos && (pos < 0 || pos >= max_seq)) return AF_ERR_OUT_OF_RANGE;
+    return contiguous_attention(qkv_out, (n_q_heads + 2 * n_kv_heads) * head_dim, k_cache,
+                                v_cache, out, 0, nullptr, max_seq, head_dim, n_q_heads, n_kv_heads,
+                                num_splits, workspace, workspace_bytes, true, cos_table, sin_table,
+                                pos, d_pos, d_status, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int af_attention_reserve(int batch, int n_q_heads, int n_kv_heads, int head_dim) {
@@ -670,13 +930,19 @@ extern "C" int af_cached_attention(const void* q, const void* k_cache, const voi
                                   bytes, stream);
 }
 
-extern "C" int af_paged_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
-                                  const int32_t* d_block_tables, int max_blocks_per_seq,
-                                  const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
-                                  int out_stride, int n_q_heads, int num_splits, void* workspace,
-                                  size_t workspace_bytes, af_stream_t stream) {
-    if (!q || !pool || !pool->base || !d_block_tables || !d_seq_lens || !out || batch < 0 ||
-        max_seq_len < 0 || max_blocks_per_seq <= 0)
+static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int layer,
+                           const int32_t* d_block_tables, int max_blocks_per_seq,
+                           const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
+                           int out_stride, int n_q_heads, int num_splits, void* workspace,
+                           size_t workspace_bytes, bool fused, const int64_t* d_slots,
+                           const int32_t* d_positions, const float* cos_table,
+                           const float* sin_table, int max_pos, hipStream_t stream) {
+    if (!q || !pool || !pool->base || !d_block_tables || !out || batch < 0 || max_seq_len < 0 ||
+        max_blocks_per_seq <= 0)
+        return AF_ERR_INVALID_ARG;
+    if (fused ? (!d_slots || !d_positions || !cos_table || !sin_table || max_pos <= 0 ||
+                 !aligned16(cos_table) || !aligned16(sin_table))
+              : !d_seq_lens)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers) return AF_ERR_INVALID_ARG;
     const int hd = pool->head_dim, nkv = pool->n_kv_heads;
@@ -702,9 +968,9 @@ extern "C" int af_paged_attention(const void* q, int q_stride, const af_kv_pool*
     const AttnWorkspace w = attn_workspace_carve(workspace, batch, n_q_heads, num_splits);
     const size_t esz = fp8 ? 1 : 2;
     const size_t slab = size_t(pool->total_blocks) * bs * nkv * hd * esz;
-    const uint8_t* base = static_cast<const uint8_t*>(pool->base);
+    uint8_t* base = static_cast<uint8_t*>(pool->base);
     AttnArgs a{};
-    a.q = static_cast<const uint16_t*>(q);
+    a.q = static_cast<uint16_t*>(q);
     a.q_stride = q_stride;
     a.k = base + size_t(2 * layer) * slab;
     a.v = base + size_t(2 * layer + 1) * slab;
@@ -716,6 +982,14 @@ extern "C" int af_paged_attention(const void* q, int q_stride, const af_kv_pool*
     a.seq_lens = d_seq_lens;
     a.seq_len_host = 0;
     a.max_seq_len = max_seq_len;
+    if (fused) {
+        a.positions = d_positions;
+        a.slots = d_slots;
+        a.max_rows = int64_t(pool->total_blocks) * bs;
+        a.cos_t = cos_table;
+        a.sin_t = sin_table;
+        a.max_pos = max_pos;
+    }
     a.out = static_cast<uint16_t*>(out);
     a.out_stride = out_stride;
     a.n_kv_heads = nkv;
@@ -728,5 +1002,31 @@ extern "C" int af_paged_attention(const void* q, int q_stride, const af_kv_pool*
     a.counters = w.counters;
     const int64_t grid = int64_t(batch) * num_splits * nkv;
     if (grid > INT32_MAX) return AF_ERR_UNSUPPORTED;
-    return dispatch(a, hd, n_q_heads / nkv, fp8, true, int(grid), static_cast<hipStream_t>(stream));
+    return dispatch(a, hd, n_q_heads / nkv, fp8, true, fused, int(grid), stream);
+}
+
+extern "C" int af_paged_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                                  const int32_t* d_block_tables, int max_blocks_per_seq,
+                                  const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
+                                  int out_stride, int n_q_heads, int num_splits, void* workspace,
+                                  size_t workspace_bytes, af_stream_t stream) {
+    return paged_attention(const_cast<void*>(q), q_stride, pool, layer, d_block_tables,
+                           max_blocks_per_seq, d_seq_lens, batch, max_seq_len, out, out_stride,
+                           n_q_heads, num_splits, workspace, workspace_bytes, false, nullptr,
+                           nullptr, nullptr, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_paged_decode_fused(void* qkv_out, int batch, const af_kv_pool* pool, int layer,
+                                     const int64_t* d_slots, const int32_t* d_positions,
+                                     const float* cos_table, const float* sin_table, int max_pos,
+                                     const int32_t* d_block_tables, int max_blocks_per_seq,
+                                     int max_seq_len, void* out, int out_stride, int n_q_heads,
+                                     int num_splits, void* workspace, size_t workspace_bytes,
+                                     af_stream_t stream) {
+    if (!pool) return AF_ERR_INVALID_ARG;
+    const int qkv_stride = (n_q_heads + 2 * pool->n_kv_heads) * pool->head_dim;
+    return paged_attention(qkv_out, qkv_stride, pool, layer, d_block_tables, max_blocks_per_seq,
+                           nullptr, batch, max_seq_len, out, out_stride, n_q_heads, num_splits,
+                           workspace, workspace_bytes, true, d_slots, d_positions, cos_table,
+                           sin_table, max_pos, static_cast<hipStream_t>(stream));
 }

@@ -91,6 +91,17 @@ def launch_cached_attention_ex(q, k_cache, v_cache, out, seq_len, max_seq_len, h
                                        _s(stream)), "launch_cached_attention_ex")
 
 
+def launch_decode_attention_fused(qkv_out, k_cache, v_cache, cos_table, sin_table, pos, max_seq,
+                                  out, n_q_heads, n_kv_heads, head_dim, workspace, num_splits=0,
+                                  d_pos=None, d_status=None, stream=None):
+    """launch_rope_append(pos) + attention over pos + 1 tokens, one kernel."""
+    check(lib().af_decode_attention_fused(_p(qkv_out), _p(k_cache), _p(v_cache), _p(cos_table),
+                                          _p(sin_table), pos, _p(d_pos), max_seq, _p(out),
+                                          n_q_heads, n_kv_heads, head_dim, num_splits,
+                                          workspace.ptr, workspace.nbytes, _p(d_status),
+                                          _s(stream)), "launch_decode_attention_fused")
+
+
 # ---- a6-a8: paged pool -----------------------------------------------------
 def make_pool(base, dtype, block_size, n_layers, n_kv_heads, head_dim, total_blocks, scales=None):
     p = _abi.KvPool()
@@ -124,6 +135,17 @@ def launch_paged_attention(q, q_stride, pool, layer, d_block_tables, max_blocks_
                                    max_blocks_per_seq, _p(d_seq_lens), batch, max_seq_len, _p(out),
                                    out_stride, n_q_heads, num_splits, workspace.ptr,
                                    workspace.nbytes, _s(stream)), "launch_paged_attention")
+
+
+def launch_paged_decode_fused(qkv_out, batch, pool, layer, d_slots, d_positions, cos_table,
+                              sin_table, max_pos, d_block_tables, max_blocks_per_seq, max_seq_len,
+                              out, out_stride, n_q_heads, workspace, num_splits=0, stream=None):
+    """Paged RoPE+append then attention (lengths = positions + 1), one kernel."""
+    check(lib().af_paged_decode_fused(_p(qkv_out), batch, ctypes.byref(pool), layer, _p(d_slots),
+                                      _p(d_positions), _p(cos_table), _p(sin_table), max_pos,
+                                      _p(d_block_tables), max_blocks_per_seq, max_seq_len, _p(out),
+                                      out_stride, n_q_heads, num_splits, workspace.ptr,
+                                      workspace.nbytes, _s(stream)), "launch_paged_decode_fused")
 
 
 def paged_gather(pool, layer, d_block_table, seq_len, k_dst, v_dst, stream=None):
@@ -267,7 +289,8 @@ def _nonneg(r, what):
 __all__ = [
     "AF_KV_FP16", "AF_KV_FP8_E4M3", "AttentionWorkspace", "BlockManager", "build_rope_cache",
     "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
-    "launch_cached_attention_ex", "launch_paged_attention", "launch_paged_rope_append",
+    "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
+    "launch_paged_decode_fused", "launch_paged_rope_append",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

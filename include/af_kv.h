@@ -129,6 +129,19 @@ int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cac
                            int n_q_heads, int n_kv_heads, int num_splits, void* workspace,
                            size_t workspace_bytes, af_stream_t stream);
 
+/* One-launch decode layer step: af_rope_append(pos) followed by
+ * af_cached_attention_ex(seq_len = pos + 1) fused into one kernel
+ * (src/core/engine.cu:326-370 issues them as three launches). Same outputs bit
+ * for bit as the two separate calls with the same num_splits: Q and K rotated
+ * in place in qkv_out, rotated K and V written to row pos, attention into out.
+ * Position: *d_pos when d_pos != NULL, else pos; a device position >= max_seq
+ * writes nothing and stores AF_ERR_OUT_OF_RANGE into *d_status (if given). */
+int af_decode_attention_fused(void* qkv_out, void* k_cache, void* v_cache, const float* cos_table,
+                              const float* sin_table, int pos, const int32_t* d_pos, int max_seq,
+                              void* out, int n_q_heads, int n_kv_heads, int head_dim,
+                              int num_splits, void* workspace, size_t workspace_bytes,
+                              int32_t* d_status, af_stream_t stream);
+
 /* ======================================================================== */
 /* a6-a8. Paged KV pool                                                      */
 /* ======================================================================== */
@@ -173,6 +186,17 @@ int af_paged_attention(const void* q, int q_stride, const af_kv_pool* pool, int 
                        const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
                        int out_stride, int n_q_heads, int num_splits, void* workspace,
                        size_t workspace_bytes, af_stream_t stream);
+
+/* Paged decode layer step in one launch: af_paged_rope_append followed by
+ * af_paged_attention with d_seq_lens[b] = d_positions[b] + 1 (the block tables
+ * already map the new position to d_slots[b], as af_bm_plan_decode leaves
+ * them). qkv_out rows are [batch, (n_q_heads + 2 n_kv_heads) * head_dim]. */
+int af_paged_decode_fused(void* qkv_out, int batch, const af_kv_pool* pool, int layer,
+                          const int64_t* d_slots, const int32_t* d_positions,
+                          const float* cos_table, const float* sin_table, int max_pos,
+                          const int32_t* d_block_tables, int max_blocks_per_seq, int max_seq_len,
+                          void* out, int out_stride, int n_q_heads, int num_splits,
+                          void* workspace, size_t workspace_bytes, af_stream_t stream);
 
 /* Gathers one sequence's first seq_len logical rows of `layer` into
  * contiguous [seq_len, kv_dim] buffers (K and V; elements copied bit for bit). */

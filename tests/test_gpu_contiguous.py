@@ -149,7 +149,7 @@ def test_cached_attention_gqa_ratios(gpu, shape, L):
                       what=f"{shape} L={L}")
 
 
-@pytest.mark.parametrize("splits", [1, 2, 7, 64, 256])
+@pytest.mark.parametrize("splits", [1, 2, 7, 33, 64])
 def test_cached_attention_split_counts_agree(gpu, splits):
     L = 3001
     say(f"cached_attention_ex splits={splits} L={L}")
@@ -164,6 +164,15 @@ def test_cached_attention_split_counts_agree(gpu, splits):
     # counters are re-armed: a second launch gives identical bits
     kv.launch_cached_attention_ex(d_q, d_k, d_v, d_o, L, L, HD, NQ, NKV, ws, num_splits=splits)
     assert np.array_equal(bits(d_o.download(np.float16)), bits(got))
+
+
+def test_cached_attention_rejects_too_many_splits(gpu):
+    q, k, v = _attention_case(100, 100, NQ, NKV, HD, 404)
+    d_q, d_k, d_v = up(q), up(k), up(v)
+    d_o = dev.DeviceBuffer(Q_DIM * 2)
+    ws = kv.AttentionWorkspace(1, NQ, NKV, HD, 64)
+    with pytest.raises(Exception, match="invalid argument"):
+        kv.launch_cached_attention_ex(d_q, d_k, d_v, d_o, 100, 100, HD, NQ, NKV, ws, num_splits=65)
 
 
 def test_cached_attention_device_length_equals_host_length(gpu):
@@ -260,5 +269,71 @@ def test_graph_replay_equals_eager_steps(gpu):
             for a, b in zip(eager[l], graphed[l]):
                 assert np.array_equal(a.download(np.uint16), b.download(np.uint16)), (step, l)
     assert list(d_state.download(np.int32)) == [pos0 + steps, pos0 + steps + 1]
+    graph.destroy()
+    stream.destroy()
+
+
+@pytest.mark.parametrize("pos", [0, 1, 17, 512, 8192])
+@pytest.mark.parametrize("splits", [0, 1, 5, 64])
+def test_fused_decode_equals_append_then_attention(gpu, pos, splits):
+    """af_decode_attention_fused == af_rope_append + af_cached_attention_ex, bit for bit."""
+    say(f"fused decode pos={pos} splits={splits}")
+    max_seq = pos + 33
+    c, s = oracle.rope_table(max_seq, HD, THETA)
+    qkv, k, v = contiguous_case(max_seq, pos, 600 + pos)
+    k[pos + 1:] = np.float16(np.nan)  # rows past the new token must never be read
+    v[pos + 1:] = np.float16(np.nan)
+    d_c, d_s = up(c), up(s)
+    a_qkv, a_k, a_v, a_o = up(qkv), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2)
+    b_qkv, b_k, b_v, b_o = up(qkv), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2)
+    ws = kv.AttentionWorkspace(1, NQ, NKV, HD, 64)
+    kv.launch_rope_append(a_qkv, a_k, a_v, d_c, d_s, pos, max_seq, NQ, NKV, HD)
+    kv.launch_cached_attention_ex(a_qkv, a_k, a_v, a_o, pos + 1, max_seq, HD, NQ, NKV, ws,
+                                  num_splits=splits)
+    kv.launch_decode_attention_fused(b_qkv, b_k, b_v, d_c, d_s, pos, max_seq, b_o, NQ, NKV, HD,
+                                     ws, num_splits=splits)
+    for x, y in ((a_qkv, b_qkv), (a_k, b_k), (a_v, b_v), (a_o, b_o)):
+        assert np.array_equal(x.download(np.uint16), y.download(np.uint16))
+    rq = oracle.rope_append(qkv, k, v, c, s, pos, NQ, NKV, HD)
+    assert_attn_close(b_o.download(np.float16),
+                      oracle.cached_attention_f64(rq[:Q_DIM], k, v, pos + 1, NQ, NKV, HD),
+                      what=f"fused pos={pos}")
+
+
+def test_fused_graph_replay_advances_position(gpu):
+    """A captured fused step with a device position, replayed N times == N eager two-call steps."""
+    layers, max_seq, pos0, steps, splits = 3, 4096, 2000, 4, 48
+    say("fused graph replay")
+    c, s = oracle.rope_table(max_seq, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    host = [contiguous_case(max_seq, pos0, 800 + l) for l in range(layers)]
+    eager = [(up(q), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2)) for (q, k, v) in host]
+    fused = [(up(q), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2)) for (q, k, v) in host]
+    stream = dev.Stream()
+    ws_e = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
+    ws_f = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
+    d_pos = up(np.array([pos0], np.int32))
+    d_st = up(np.array([0], np.int32))
+
+    def step():
+        for (qkv, k, v, o) in fused:
+            kv.launch_decode_attention_fused(qkv, k, v, d_c, d_s, -1, max_seq, o, NQ, NKV, HD,
+                                             ws_f, num_splits=splits, d_pos=d_pos,
+                                             d_status=d_st, stream=stream)
+        dev.add_i32(d_pos.ptr, 1, 1, stream)
+
+    graph = dev.Graph.capture(stream, step)
+    for i in range(steps):
+        for (qkv, k, v, o) in eager:
+            kv.launch_rope_append(qkv, k, v, d_c, d_s, pos0 + i, max_seq, NQ, NKV, HD,
+                                  stream=stream)
+            kv.launch_cached_attention_ex(qkv, k, v, o, pos0 + i + 1, max_seq, HD, NQ, NKV, ws_e,
+                                          num_splits=splits, stream=stream)
+        graph.launch(stream)
+        stream.sync()
+        for l in range(layers):
+            for a, b in zip(eager[l], fused[l]):
+                assert np.array_equal(a.download(np.uint16), b.download(np.uint16)), (i, l)
+    assert d_pos.download(np.int32)[0] == pos0 + steps and d_st.download(np.int32)[0] == 0
     graph.destroy()
     stream.destroy()
