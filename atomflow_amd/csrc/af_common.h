@@ -27,7 +27,7 @@ namespace af {
 constexpr int kWave = 64;
 // Longest split grid; bounds the per-(sequence, head) partial buffers and lets
 // the combine read every partial in one round of loads.
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 128;
 // Fewest tokens a split may own: below this the partial (m, l, o[]) traffic and
 // the combine cost more than the split saves.
 constexpr int kMinSpan = 64;
@@ -72,7 +72,7 @@ inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, 
 // Number of compute units of the current device (cached per device).
 int device_compute_units();
 
-// Default split count: enough workgroups for ~2 per CU, each split at least
+// Default split count: about 3/4 of a workgroup per CU, each split at least
 // kMinSpan tokens, at most kMaxSplits.
 int default_splits(int max_seq_len, int batch, int n_kv_heads);
 

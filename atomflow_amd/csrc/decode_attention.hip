@@ -43,6 +43,8 @@ constexpr int kThreads = kWaves * 64;  // 256
 constexpr int kLanesPerRow = 8;        // lanes that share one token row of one head
 constexpr int kRowsPerStep = 64 / kLanesPerRow;  // 8 tokens per wave load step
 constexpr int kMaxTableLds = 1024;     // block-table entries staged per split
+constexpr float kLazyLog2 = 8.0f;      // running-max slack before a rescale (log2 units)
+constexpr float kEmptyMax = -1.0e30f;  // running max of a lane group that has seen no row
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -227,12 +229,16 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
-    int span = max(ceil_div_d(L, a.num_splits), a.min_span);
-    span = (span + CHUNK - 1) / CHUNK * CHUNK;
-    const int n_active = (L + span - 1) / span;
+    // Balanced partition in whole chunks: split s of n_active owns chunks
+    // [s*C/n, (s+1)*C/n), so equal-work splits map evenly onto the CUs.
+    const int total_chunks = (L + CHUNK - 1) / CHUNK;
+    const int min_chunks = max(1, a.min_span / CHUNK);
+    const int n_active = max(1, min(a.num_splits, total_chunks / min_chunks));
     if (split >= n_active) return;
-    const int t_begin = split * span;
-    const int t_end = min(L, t_begin + span);
+    const int chunk_begin = int(int64_t(split) * total_chunks / n_active);
+    const int chunk_end = int(int64_t(split + 1) * total_chunks / n_active);
+    const int t_begin = chunk_begin * CHUNK;
+    const int t_end = min(L, chunk_end * CHUNK);
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -390,7 +396,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     float m_run[GROUP], l_run[GROUP], acc[GROUP][EPL];
 #pragma unroll
     for (int gh = 0; gh < GROUP; ++gh) {
-        m_run[gh] = -INFINITY;
+        m_run[gh] = kEmptyMax;  // finite: exp2(-inf - kEmptyMax) = 0 for masked rows
         l_run[gh] = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[gh][e] = 0.f;
@@ -452,10 +458,13 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                 cmax[gh] = fmaxf(cmax[gh], s[r][gh]);
             }
         }
+        // Per-lane running max with a lazy rescale: the reference point only
+        // moves when a score exceeds it by more than 2^kLazyLog2, so p <= 2^8
+        // and the (rare) accumulator rescale replaces a cross-lane max per chunk.
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh) {
-            const float m_new = fmaxf(m_run[gh], wave_max_of_groups(cmax[gh]));
-            if (m_new > m_run[gh]) {  // wave-uniform
+            if (cmax[gh] > m_run[gh] + kLazyLog2) {
+                const float m_new = cmax[gh];
                 const float alpha = fast_exp2(m_run[gh] - m_new);
                 l_run[gh] *= alpha;
 #pragma unroll
@@ -518,9 +527,15 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         }
     }
 
-    // ---- merge the wave's 8 token groups (m is wave-uniform: plain sums) ----
+    // ---- merge the wave's 8 token groups onto the wave's largest reference ---
 #pragma unroll
     for (int gh = 0; gh < GROUP; ++gh) {
+        const float mw = wave_max_of_groups(m_run[gh]);
+        const float f = fast_exp2(m_run[gh] - mw);  // groups that saw no row hold l = acc = 0
+        m_run[gh] = mw;
+        l_run[gh] *= f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[gh][e] *= f;
         float l = l_run[gh];
         l += dpp<0x128>(l);
         l += __shfl_xor(l, 16);
@@ -793,7 +808,10 @@ int device_compute_units() {
 int default_splits(int max_seq_len, int batch, int n_kv_heads) {
     if (max_seq_len <= 0) return 1;
     const int pairs = std::max(1, batch * n_kv_heads);
-    int splits = ceil_div(2 * device_compute_units(), pairs);
+    // About 3/4 of a workgroup per CU: measured best on MI355X for batch 1
+    // (the split-K combine grows with the split count faster than more
+    // workgroups add bandwidth).
+    int splits = std::max(1, (3 * device_compute_units()) / (4 * pairs));
     splits = std::max(splits, ceil_div(max_seq_len, 1024));  // long sequences: bounded spans
     splits = std::min(splits, std::max(1, ceil_div(max_seq_len, kMinSpan)));
     return std::min(std::max(splits, 1), kMaxSplits);

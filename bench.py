@@ -1,22 +1,28 @@
 """Benchmark of the KV-cache hot path on one MI355X (BASELINE.json metric).
 
-Default workload = BASELINE configs[1] at ctx 8192: a 28-layer contiguous KV
-stack (Llama-3.2-3B attention shape: 24 Q heads, 8 KV heads, head_dim 128,
-fp16), batch 1. One step = per layer fused RoPE+append at pos = ctx, then GQA
-decode attention over L = ctx + 1 tokens; the 56 launches are captured in one
-hipGraph. Inputs are synthetic N(0,1) fp16, generated on the device and
-resident in HBM before timing.
+Default (``--config 2``) = BASELINE configs[1] at ctx 8192: a 28-layer
+contiguous KV stack (Llama-3.2-3B attention shape: 24 Q heads, 8 KV heads,
+head_dim 128, fp16), batch 1. One decode step = per layer RoPE+append at
+pos = ctx and GQA attention over L = ctx + 1 tokens, as one fused launch per
+layer (af_decode_attention_fused); the 28 launches are one hipGraph. Inputs are
+synthetic N(0,1) fp16 generated on the device and resident in HBM before timing.
 
-Printed JSON line:
-  value      whole-step KV-read throughput: 28 * L * 4096 B / step time (GB/s)
-  roofline   attention kernel alone: algorithmic KV bytes per launch / its mean
-             duration (HIP events around a graph of 28 attention launches, on
-             the stream they run on), against 8 TB/s HBM; traffic = HBM bytes
-             per launch from the committed rocprofv3 PMC summary, or null
-  cpu_baseline  the scalar C++ oracle (oracle/) timed on this host on one full
+``--config 3|4|5`` run the paged workloads (BASELINE configs[2..4]) through the
+BlockManager: paged fp16 (B=32, L~U[128,8192], 16-token blocks), paged with a
+2048-token shared prefix (64 forks, copy-on-write measured separately), FP8
+E4M3 paged (B=128, L~U[8192,16384], 32-token blocks, ~100 GB pool).
+
+Printed JSON line (one per run):
+  value      KV-read throughput of the whole step: layers * KV bytes attended /
+             step time (GB/s); ms_per_step and us_per_layer_step alongside
+  roofline   the attention kernel alone: algorithmic KV bytes per launch / its
+             mean duration (HIP events around a graph of 28 attention launches,
+             on the stream they run on) against 8 TB/s; traffic = HBM bytes per
+             launch from the committed rocprofv3 PMC summary (configs[1] only)
+  cpu_baseline  (default config) the scalar C++ oracle timed on this host on one
              28-layer step, 1 thread
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 8192]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2..5] [--ctx 8192]
 """
 import argparse
 import json
@@ -35,6 +41,7 @@ QKV = Q_DIM + 2 * KV_DIM
 THETA = 500000.0
 HBM_PEAK_GBS = 8000.0
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx8k_pmc.txt")
+METRIC = "decode-attn KV-read GB/s (% of 8 TB/s HBM) + us/layer-step at ctx 8k"
 
 
 def log(msg):
@@ -46,6 +53,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
+                    help="BASELINE configs[n-1]: 2 contiguous, 3 paged, 4 paged+CoW, 5 paged FP8")
     ap.add_argument("--ctx", type=int, default=8192, choices=[1024, 8192, 32768])
     ap.add_argument("--splits", type=int, default=0, help="attention split count (0 = library default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -54,9 +63,9 @@ def parse():
     return ap.parse_args()
 
 
-def read_traffic(ctx):
+def read_traffic():
     """HBM bytes per attention launch from the committed PMC summary (or None)."""
-    if ctx != 8192 or not os.path.exists(PMC_SUMMARY):
+    if not os.path.exists(PMC_SUMMARY):
         return None
     for line in open(PMC_SUMMARY):
         if line.startswith("traffic_bytes_per_launch:"):
@@ -88,26 +97,33 @@ def cpu_baseline(ctx):
             "ms_per_step": round(dt * 1e3, 1)}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the KV path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
-        sys.exit(2)
+class Timer:
+    def __init__(self, dev, stream, warmup):
+        self.dev, self.stream, self.warmup = dev, stream, warmup
+        self.e0, self.e1 = dev.Event(), dev.Event()
 
+    def graph_ms(self, graph, reps):
+        """Mean ms per replay of `graph`, HIP events on the replay stream."""
+        for _ in range(self.warmup):
+            graph.launch(self.stream)
+        self.dev.synchronize()
+        self.e0.record(self.stream)
+        for _ in range(reps):
+            graph.launch(self.stream)
+        self.e1.record(self.stream)
+        self.e1.sync()
+        self.dev.synchronize()
+        return self.e0.elapsed_ms(self.e1) / reps
+
+
+def bench_contiguous(args, dev, kv, lib, info):
     import atomflow_amd
-    from atomflow_amd import device as dev
-    from atomflow_amd import kv
 
-    atomflow_amd.lib()
-    dev.set_device(0)
-    info = dev.device_info()
     ctx = args.ctx
     L = ctx + 1
     max_seq = (L + 127) // 128 * 128
     slab = max_seq * KV_DIM * 2
-    log(f"device {info}; ctx {ctx}, cache rows {max_seq}, pool {LAYERS * 2 * slab / 2**30:.2f} GiB")
-
+    log(f"configs[1]: ctx {ctx}, cache rows {max_seq}, pool {LAYERS * 2 * slab / 2**30:.2f} GiB")
     stream = dev.Stream()
     pool = dev.DeviceBuffer(LAYERS * 2 * slab)          # [L0_K | L0_V | L1_K | ...]
     qkv = dev.DeviceBuffer(LAYERS * QKV * 2)             # one qkv_out row per layer
@@ -115,113 +131,224 @@ def main():
     d_cos = dev.DeviceBuffer(max_seq * HD // 2 * 4)
     d_sin = dev.DeviceBuffer(max_seq * HD // 2 * 4)
     kv.build_rope_cache(d_cos, d_sin, max_seq, HD, THETA, stream)
-    lib = atomflow_amd.lib()
     atomflow_amd.check(lib.af_rt_fill_randn_f16(pool.ptr, LAYERS * 2 * slab // 2, 7, 1.0, stream.handle))
     atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, LAYERS * QKV, 11, 1.0, stream.handle))
     splits = args.splits or kv.default_splits(L, 1, NKV)
     ws = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
     stream.sync()
 
-    def k_ptr(l):
-        return pool.ptr + (2 * l) * slab
+    def ptrs(l):
+        return (qkv.ptr + l * QKV * 2, pool.ptr + 2 * l * slab, pool.ptr + (2 * l + 1) * slab,
+                out.ptr + l * Q_DIM * 2)
 
-    def v_ptr(l):
-        return pool.ptr + (2 * l + 1) * slab
-
-    def step():
+    def step():  # one fused launch per layer: RoPE + append + attention
         for l in range(LAYERS):
-            q = qkv.ptr + l * QKV * 2
-            kv.launch_rope_append(q, k_ptr(l), v_ptr(l), d_cos, d_sin, ctx, max_seq, NQ, NKV, HD,
-                                  stream=stream)
-            kv.launch_cached_attention_ex(q, k_ptr(l), v_ptr(l), out.ptr + l * Q_DIM * 2, L,
-                                          max_seq, HD, NQ, NKV, ws, num_splits=splits,
-                                          stream=stream)
+            q, k, v, o = ptrs(l)
+            kv.launch_decode_attention_fused(q, k, v, d_cos, d_sin, ctx, max_seq, o, NQ, NKV, HD,
+                                             ws, num_splits=splits, stream=stream)
+
+    def step_two_launch():  # the reference's order as two launches: append, then attention
+        for l in range(LAYERS):
+            q, k, v, o = ptrs(l)
+            kv.launch_rope_append(q, k, v, d_cos, d_sin, ctx, max_seq, NQ, NKV, HD, stream=stream)
+            kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws,
+                                          num_splits=splits, stream=stream)
 
     def attention_only():
         for l in range(LAYERS):
-            q = qkv.ptr + l * QKV * 2
-            kv.launch_cached_attention_ex(q, k_ptr(l), v_ptr(l), out.ptr + l * Q_DIM * 2, L,
-                                          max_seq, HD, NQ, NKV, ws, num_splits=splits,
-                                          stream=stream)
+            q, k, v, o = ptrs(l)
+            kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws,
+                                          num_splits=splits, stream=stream)
 
-    def append_only():
-        for l in range(LAYERS):
-            q = qkv.ptr + l * QKV * 2
-            kv.launch_rope_append(q, k_ptr(l), v_ptr(l), d_cos, d_sin, ctx, max_seq, NQ, NKV, HD,
-                                  stream=stream)
-
-    g_step = dev.Graph.capture(stream, step)
-    g_attn = dev.Graph.capture(stream, attention_only)
-    g_app = dev.Graph.capture(stream, append_only)
-    e0, e1 = dev.Event(), dev.Event()
-
-    def timed(graph, reps):
-        for _ in range(args.warmup):
-            graph.launch(stream)
-        dev.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            graph.launch(stream)
-        e1.record(stream)
-        e1.sync()
-        dev.synchronize()
-        return e0.elapsed_ms(e1) / reps
-
+    graphs = {name: dev.Graph.capture(stream, fn) for name, fn in
+              (("step", step), ("two", step_two_launch), ("attn", attention_only))}
+    t = Timer(dev, stream, args.warmup)
     log(f"splits {splits}; warmup {args.warmup}, timing {args.steps} graph replays")
-    ms_step = timed(g_step, args.steps)
-    ms_attn = timed(g_attn, args.steps) / LAYERS
-    ms_app = timed(g_app, args.steps) / LAYERS
-    log(f"step {ms_step * 1e3:.1f} us, attention {ms_attn * 1e3:.2f} us/launch, "
-        f"append {ms_app * 1e3:.2f} us/launch")
+    ms_step = t.graph_ms(graphs["step"], args.steps)
+    ms_two = t.graph_ms(graphs["two"], args.steps)
+    ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
+    log(f"step {ms_step * 1e3:.1f} us (two-launch {ms_two * 1e3:.1f} us), "
+        f"attention {ms_attn * 1e3:.2f} us/launch")
+    for g in graphs.values():
+        g.destroy()
 
     kv_bytes = L * KV_DIM * 2 * 2          # K and V rows attended, each byte once
     step_gbs = LAYERS * kv_bytes / (ms_step * 1e-3) / 1e9
     attn_gbs = kv_bytes / (ms_attn * 1e-3) / 1e9
-    traffic = read_traffic(ctx)
-
     result = {
-        "metric": "decode-attn KV-read GB/s (% of 8 TB/s HBM) + us/layer-step at ctx 8k",
-        "value": round(step_gbs, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "metric": METRIC, "value": round(step_gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "us_per_layer_step": round(ms_step * 1e3 / LAYERS, 3),
         "pct_of_hbm_peak": round(100 * step_gbs / HBM_PEAK_GBS, 1),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16 (fp32 accumulate)",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 KV, fp32 softmax/accumulate",
         "data": "synthetic N(0,1) fp16 K/V/qkv generated on device",
         "config": {"workload": f"BASELINE configs[1]: 28-layer contiguous KV, batch 1, ctx {ctx}, "
-                               "24 Q / 8 KV heads x 128, fp16, hipGraph step = 28 x "
-                               "(RoPE+append + GQA attention)",
+                               "24 Q / 8 KV heads x 128, fp16, hipGraph step = 28 fused "
+                               "RoPE+append+GQA-attention launches",
                    "ctx": ctx, "attended_tokens": L, "layers": LAYERS, "splits": splits,
                    "device": info["name"], "arch": info["arch"], "cus": info["compute_units"]},
         "kernels": {"decode_attn_us": round(ms_attn * 1e3, 3),
-                    "rope_append_us": round(ms_app * 1e3, 3),
+                    "two_launch_us_per_layer_step": round(ms_two * 1e3 / LAYERS, 3),
                     "attn_kv_bytes_per_launch": kv_bytes},
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic},
+                     "traffic": read_traffic() if ctx == 8192 else None},
         "cpu_baseline": None,
     }
-    if not args.no_cpu:
-        log("cpu baseline (scalar oracle, 1 thread) ...")
-        result["cpu_baseline"] = cpu_baseline(ctx)
-    print(json.dumps(result), flush=True)
-    for g in (g_step, g_attn, g_app):
-        g.destroy()
     if args.calibrate_copy:
-        calibrate_copy(stream)
+        calibrate_copy(dev, kv, stream)
+    return result
 
 
-def calibrate_copy(stream, mib=256, reps=3):
+def bench_paged(args, dev, kv, lib, info):
+    import atomflow_amd
+    from atomflow_amd import AF_KV_FP16, AF_KV_FP8_E4M3
+
+    cfg = args.config
+    r = np.random.Generator(np.random.PCG64(0xA70F10 + cfg))
+    if cfg == 3:
+        bs, fp8 = 16, False
+        ctx_lens = r.integers(128, 8193, 32)
+    elif cfg == 4:
+        bs, fp8 = 16, False
+        suffix = r.integers(1, 1025, 64)
+    else:
+        bs, fp8 = 32, True
+        ctx_lens = r.integers(8192, 16385, 128)
+    esz = 1 if fp8 else 2
+    if cfg == 4:
+        prefix = 2048
+        B = len(suffix)
+        lens_after = prefix + suffix + 1
+        unique_tokens = prefix + int(suffix.sum()) + B
+        need = prefix // bs + sum((int(s) + 1 + bs - 1) // bs for s in suffix)
+    else:
+        B = len(ctx_lens)
+        lens_after = ctx_lens + 1
+        unique_tokens = int(lens_after.sum())
+        need = sum((int(n) + bs - 1) // bs for n in lens_after)
+    total_blocks = int(need * 1.1) + 8        # 10% free-list headroom
+    bm = kv.BlockManager(total_blocks, bs, LAYERS, NKV, HD, AF_KV_FP8_E4M3 if fp8 else AF_KV_FP16)
+    ids = [bm.allocate_block() for _ in range(total_blocks)]
+    for b in r.permutation(ids):               # blocks come back in random order
+        bm.free_block(int(b))
+    if cfg == 4:
+        root = bm.seq_create()
+        bm.seq_extend(root, prefix)
+        seqs = [root] + [bm.seq_fork(root) for _ in range(B - 1)]
+        for s, n in zip(seqs, suffix):
+            assert not isinstance(bm.seq_extend(s, int(n)), int)
+    else:
+        seqs = []
+        for n in ctx_lens:
+            s = bm.seq_create()
+            assert not isinstance(bm.seq_extend(s, int(n)), int)
+            seqs.append(s)
+    plan = bm.plan_decode(seqs)
+    assert not isinstance(plan, int), plan
+    slots, positions, copies = plan
+    max_len = int(lens_after.max())
+    max_blocks = (max_len + bs - 1) // bs
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    assert np.array_equal(lens, lens_after)
+    desc = bm.pool()
+    nbytes = kv.pool_bytes(desc)
+    log(f"configs[{cfg - 1}]: B {B}, block {bs}, {total_blocks} blocks, pool {nbytes / 2**30:.1f} GiB, "
+        f"max len {max_len}, fp8 {fp8}")
+    stream = dev.Stream()
+    pool = dev.DeviceBuffer(nbytes)
+    scales = None
+    if fp8:  # N(0,1) values, absmax-style scale fixed at 5 sigma / 448
+        scale = 5.0 / 448.0
+        scales = dev.DeviceBuffer.from_array(np.full((LAYERS, 2, NKV), scale, np.float32))
+        atomflow_amd.check(lib.af_rt_fill_randn_fp8(pool.ptr, nbytes, 7, 1.0 / scale, stream.handle))
+    else:
+        atomflow_amd.check(lib.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, stream.handle))
+    bm.attach_pool(pool.ptr, scales.ptr if scales else None)
+    desc = bm.pool()
+    max_pos = max_len + 1
+    d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    kv.build_rope_cache(d_cos, d_sin, max_pos, HD, THETA, stream)
+    qkv = dev.DeviceBuffer(LAYERS * B * QKV * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, LAYERS * B * QKV, 11, 1.0, stream.handle))
+    out = dev.DeviceBuffer(LAYERS * B * Q_DIM * 2)
+    d_tables, d_lens = dev.DeviceBuffer.from_array(tables), dev.DeviceBuffer.from_array(lens)
+    d_slots, d_pos = dev.DeviceBuffer.from_array(slots), dev.DeviceBuffer.from_array(positions)
+    splits = args.splits or max(kv.default_splits(max_len, B, NKV), 1)
+    ws = kv.AttentionWorkspace(B, NQ, NKV, HD, splits, stream)
+    stream.sync()
+
+    def step():
+        for l in range(LAYERS):
+            kv.launch_paged_decode_fused(qkv.ptr + l * B * QKV * 2, B, desc, l, d_slots, d_pos,
+                                         d_cos, d_sin, max_pos, d_tables, max_blocks, max_len,
+                                         out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ, ws,
+                                         num_splits=splits, stream=stream)
+
+    def attention_only():
+        for l in range(LAYERS):
+            kv.launch_paged_attention(qkv.ptr + l * B * QKV * 2, QKV, desc, l, d_tables,
+                                      max_blocks, d_lens, B, max_len,
+                                      out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ, ws,
+                                      num_splits=splits, stream=stream)
+
+    graphs = {"step": dev.Graph.capture(stream, step), "attn": dev.Graph.capture(stream, attention_only)}
+    t = Timer(dev, stream, args.warmup)
+    ms_step = t.graph_ms(graphs["step"], args.steps)
+    ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
+    for g in graphs.values():
+        g.destroy()
+    row = KV_DIM * esz
+    logical = int(lens_after.sum()) * row * 2
+    step_gbs = LAYERS * logical / (ms_step * 1e-3) / 1e9
+    attn_gbs = logical / (ms_attn * 1e-3) / 1e9
+    result = {
+        "metric": METRIC + f" [paged configs[{cfg - 1}]]", "value": round(step_gbs, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4), "us_per_layer_step": round(ms_step * 1e3 / LAYERS, 3),
+        "pct_of_hbm_peak": round(100 * step_gbs / HBM_PEAK_GBS, 1), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": ("fp8 e4m3" if fp8 else "f16") + " KV, fp32 softmax/accumulate",
+        "data": "synthetic N(0,1) KV generated on device; block tables from the BlockManager "
+                "over a randomly permuted free list",
+        "config": {"workload": f"BASELINE configs[{cfg - 1}]", "batch": B, "block_size": bs,
+                   "total_blocks": total_blocks, "pool_gib": round(nbytes / 2**30, 2),
+                   "max_len": max_len, "mean_len": float(lens_after.mean()), "splits": splits,
+                   "logical_kv_bytes_per_layer": logical,
+                   "unique_kv_bytes_per_layer": unique_tokens * row * 2, "layers": LAYERS},
+        "kernels": {"paged_attn_us": round(ms_attn * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    if cfg == 4:
+        result["kernels"].update(cow_copy_timing(dev, kv, bm, prefix, B, stream, desc))
+    return result
+
+
+def cow_copy_timing(dev, kv, bm, prefix, B, stream, desc):
+    """configs[3] with a shared partial tail: fork -> first append triggers B-1 copies."""
+    root = bm.seq_create()
+    if isinstance(bm.seq_extend(root, prefix + 8), int):
+        return {"cow": "skipped: pool full"}
+    forks = [bm.seq_fork(root) for _ in range(B - 1)]
+    plan = bm.plan_decode([root] + forks, max_copies=B)
+    if isinstance(plan, int):
+        return {"cow": f"skipped: status {plan}"}
+    copies = plan[2]
+    d_copies = dev.DeviceBuffer.from_array(np.ascontiguousarray(copies, np.int32))
+    d_count = dev.DeviceBuffer.from_array(np.array([len(copies)], np.int32))
+    g = dev.Graph.capture(stream, lambda: kv.kv_copy_blocks(desc, d_copies, d_count, B, stream))
+    ms = Timer(dev, stream, 3).graph_ms(g, 20)
+    g.destroy()
+    return {"cow_copies": len(copies), "cow_rows_per_copy": int(copies[0][2]) if len(copies) else 0,
+            "cow_copy_us_all_layers": round(ms * 1e3, 3)}
+
+
+def calibrate_copy(dev, kv, stream, mib=256, reps=3):
     """paged_gather over an identity table: reads 2 x `mib` MiB, writes 2 x `mib` MiB."""
-    from atomflow_amd import device as dev
-    from atomflow_amd import kv
-
     rows = mib * 2**20 // (KV_DIM * 2)
     src = dev.DeviceBuffer(2 * rows * KV_DIM * 2)
     dst_k = dev.DeviceBuffer(rows * KV_DIM * 2)
@@ -233,6 +360,30 @@ def calibrate_copy(stream, mib=256, reps=3):
         kv.paged_gather(pool, 0, table, rows, dst_k, dst_v, stream)
     stream.sync()
     log(f"copy calibration: {reps} x paged_gather of {2 * rows * KV_DIM * 2} B read + same written")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the KV path is single-GPU; DESIGN.md describes how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    import atomflow_amd
+    from atomflow_amd import device as dev
+    from atomflow_amd import kv
+
+    lib = atomflow_amd.lib()
+    dev.set_device(0)
+    info = dev.device_info()
+    log(f"device {info}")
+    if args.config == 2:
+        result = bench_contiguous(args, dev, kv, lib, info)
+        if not args.no_cpu:
+            log("cpu baseline (scalar oracle, 1 thread) ...")
+            result["cpu_baseline"] = cpu_baseline(args.ctx)
+    else:
+        result = bench_paged(args, dev, kv, lib, info)
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":
