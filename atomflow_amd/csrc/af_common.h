@@ -39,8 +39,9 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 //   [0, kCounterBytes)           arrival counters, one per (sequence, KV head),
 //                                zero between launches (each launch re-zeroes
 //                                the counters it used)
-//   [kCounterBytes, ...)         part_ml [batch][n_q_heads][splits][2] (max, sum)
-//   then                         part_o  [batch][n_q_heads][splits][head_dim]
+//   [kCounterBytes, ...)         part_ml [batch][n_kv_heads][splits][2 * group]
+//                                (group = n_q_heads / n_kv_heads: max..., sum...)
+//   then                         part_o  [batch][n_kv_heads][splits][group * head_dim]
 // The counter region has a fixed size and position, so one workspace serves
 // launches of any batch / split count without re-initialisation.
 constexpr size_t kCounterBytes = 64 * 1024;
