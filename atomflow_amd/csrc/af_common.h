@@ -42,8 +42,9 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 //   [kCounterBytes, ...)         part_ml [batch][n_kv_heads][splits][2 * group]
 //                                (group = n_q_heads / n_kv_heads: max..., sum...)
 //   then                         part_o  [batch][n_kv_heads][splits][group * head_dim]
-// The counter region has a fixed size and position, so one workspace serves
-// launches of any batch / split count without re-initialisation.
+// The counter region has a fixed size and position and is zero between
+// launches (each launch re-zeroes the counters it used), so one workspace
+// serves launches of any batch / split count without re-initialisation.
 constexpr size_t kCounterBytes = 64 * 1024;
 constexpr int kMaxCounters = int(kCounterBytes / sizeof(uint32_t));
 

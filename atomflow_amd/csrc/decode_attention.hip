@@ -41,8 +41,10 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kThreads = kWaves * 64;  // 256
 constexpr int kLanesPerRow = 8;        // lanes that share one token row of one head
-constexpr int kRowsPerStep = 64 / kLanesPerRow;  // 8 tokens per wave load step
+constexpr int kRowsPerStep = 64 / kLanesPerRow;      // 8 tokens per wave row-step
+constexpr int kStepTokens = kWaves * kRowsPerStep;   // 64 tokens per workgroup step
 constexpr int kMaxTableLds = 1024;     // block-table entries staged per split
+constexpr int kRingBudget = 126;       // VGPRs shared by the row ring and the accumulators
 constexpr float kLazyLog2 = 8.0f;      // running-max slack before a rescale (log2 units)
 constexpr float kEmptyMax = -1.0e30f;  // running max of a lane group that has seen no row
 
@@ -72,15 +74,51 @@ __device__ __forceinline__ float wave_max_of_groups(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Cross-row exchanges of gfx950 (VALU, no LDS round trip). With a = b = v on
+// entry, v_permlane16_swap leaves rows (v0, v0, v2, v2) in a and (v1, v1, v3, v3)
+// in b (rows of 16 lanes); v_permlane32_swap leaves (lo, lo) in a and (hi, hi)
+// in b (halves of 32 lanes). Written as inline asm with both operands
+// read-write: the compiler's builtin returns the first result for both. The
+// s_nop provides the two wait states the swap needs after a VALU write.
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Sum / max over the four 16-lane rows of values that are uniform per row.
+__device__ __forceinline__ float rows_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = b = __builtin_bit_cast(uint32_t, v);
+    swap32(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float rows_max(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = b = __builtin_bit_cast(uint32_t, v);
+    swap32(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+// Sum over the 8 token groups of the lanes that share lane & 7.
+__device__ __forceinline__ float groups_sum(float v) { return rows_sum(v + dpp<0x128>(v)); }
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x128>(v);
+    return rows_sum(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    return rows_max(v);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -184,18 +222,18 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
     constexpr int EPL = LY::kEpl;
-    constexpr int R = 2;                     // token rows per lane per chunk
-    constexpr int CHUNK = R * kRowsPerStep;  // tokens per wave chunk (16)
     constexpr int GHD = GROUP * HD;
-    constexpr int PER64 = (GHD / 2 + 63) / 64;             // 64-bit partial slots per lane
-    constexpr int SB = (24 / PER64) < 1 ? 1 : ((24 / PER64) > 8 ? 8 : (24 / PER64));
+    // Row-steps in flight per lane: as many as fit beside the accumulators.
+    constexpr int kRowRegs = 2 * LOADS * 4;
+    constexpr int kFree = kRingBudget - GROUP * (EPL + EPL / 2 + 2);
+    constexpr int NB = kFree / kRowRegs < 2 ? 2 : (kFree / kRowRegs > 8 ? 8 : kFree / kRowRegs);
 
-    __shared__ float s_o[kWaves][GHD];
-    __shared__ float s_m[kWaves][GROUP];
-    __shared__ float s_l[kWaves][GROUP];
+    __shared__ __align__(16) float s_acc[4 * kWaves][GHD];  // per-row partial o of every wave
+    __shared__ float s_pm[4 * kWaves][GROUP];
+    __shared__ float s_pl[4 * kWaves][GROUP];
     __shared__ int32_t s_tab[PAGED ? kMaxTableLds : 1];
-    __shared__ float s_ml[2 * GROUP * kMaxSplits];  // (m, l) of every split, then weights
-    __shared__ float s_wt[GROUP][kMaxSplits];
+    __shared__ float s_ml[2 * GROUP * kMaxSplits];  // (m, l) of every split
+    __shared__ __align__(16) float s_wt[GROUP][kMaxSplits];
     __shared__ uint16_t s_q[FUSED ? GHD : 1];
     __shared__ uint4 s_new[FUSED ? 2 * LY::kRowBytes / 16 : 1];  // new token's K then V row (head h)
     __shared__ int s_last;
@@ -229,16 +267,17 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
-    // Balanced partition in whole chunks: split s of n_active owns chunks
-    // [s*C/n, (s+1)*C/n), so equal-work splits map evenly onto the CUs.
-    const int total_chunks = (L + CHUNK - 1) / CHUNK;
-    const int min_chunks = max(1, a.min_span / CHUNK);
-    const int n_active = max(1, min(a.num_splits, total_chunks / min_chunks));
+    // Balanced partition in whole workgroup steps (kStepTokens rows): split s
+    // of n_active owns steps [s*C/n, (s+1)*C/n).
+    const int total_steps = (L + kStepTokens - 1) / kStepTokens;
+    const int min_steps = max(1, a.min_span / kStepTokens);
+    const int n_active = max(1, min(a.num_splits, total_steps / min_steps));
     if (split >= n_active) return;
-    const int chunk_begin = int(int64_t(split) * total_chunks / n_active);
-    const int chunk_end = int(int64_t(split + 1) * total_chunks / n_active);
-    const int t_begin = chunk_begin * CHUNK;
-    const int t_end = min(L, chunk_end * CHUNK);
+    const int step_begin = int(int64_t(split) * total_steps / n_active);
+    const int step_end = int(int64_t(split + 1) * total_steps / n_active);
+    const int t_begin = step_begin * kStepTokens;
+    const int t_end = min(L, step_end * kStepTokens);
+    const int n_steps = step_end - step_begin;  // >= 1
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -256,16 +295,17 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         __syncthreads();
     }
 
-    const int n_chunks = (t_end - t_begin + CHUNK - 1) / CHUNK;
     const uint8_t* kbase = a.k + size_t(h) * LY::kRowBytes + j * 16;
     const uint8_t* vbase = a.v + size_t(h) * LY::kRowBytes + j * 16;
     // Rows that may be read from memory: [0, L) unfused; [0, L-1) fused (row
     // L-1 is the token being appended and comes from LDS).
     const int last_row = FUSED ? max(L - 2, 0) : L - 1;
+    // Token of this lane in step s: waves interleave 8-row slices of each step.
+    const int lane_t0 = t_begin + wave * kRowsPerStep + g;
 
-    struct Chunk {
-        uint4 k[R][LOADS];
-        uint4 v[R][LOADS];
+    struct Row {
+        uint4 k[LOADS];
+        uint4 v[LOADS];
     };
 
     auto row_offset = [&](int t) -> int64_t {
@@ -279,46 +319,93 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         }
     };
 
-    auto load_chunk = [&](Chunk& c, int chunk) {
-        const int t0 = t_begin + chunk * CHUNK + g;
+    auto load_row = [&](Row& r, int step) {
+        const int64_t off = row_offset(lane_t0 + step * kStepTokens);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t off = row_offset(t0 + r * kRowsPerStep);
-#pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                c.k[r][i] = *reinterpret_cast<const uint4*>(kbase + off + i * 128);
-                c.v[r][i] = *reinterpret_cast<const uint4*>(vbase + off + i * 128);
-            }
+        for (int i = 0; i < LOADS; ++i) {
+            r.k[i] = *reinterpret_cast<const uint4*>(kbase + off + i * 128);
+            r.v[i] = *reinterpret_cast<const uint4*>(vbase + off + i * 128);
         }
     };
 
-    // First chunk in flight before the query set-up.
-    Chunk ca, cb;
-    int c = wave;
-    if (c < n_chunks) load_chunk(ca, c);
-
-    // ---- query fragment -----------------------------------------------------
-    half2_t qv[GROUP][EPL / 2];
+    // ---- query inputs first ---------------------------------------------------
+    // The vector-memory counter retires loads in issue order: whatever the
+    // set-up waits for is issued before the ring prologue, so that wait does
+    // not also wait for the KV rows.
+    constexpr int kQLoads = LOADS * (LY::kElemsPerLoad / 8);  // 16-B query loads per head
+    constexpr int kRopeItems = (GROUP + 1) * (HD / 2);        // Q pairs, then K pairs
+    constexpr int RIT = (kRopeItems + kThreads - 1) / kThreads;
+    uint16_t rx[RIT], ry[RIT];
+    float rc[RIT], rs[RIT];
+    uint16_t vnew = 0;
+    uint4 qraw[FUSED ? 1 : GROUP][kQLoads];
     if constexpr (FUSED) {
-        // RoPE of the GROUP query heads into LDS (every split computes the same
-        // bits); the owner also rotates K head h, and stages the new K/V row.
         const int half = HD / 2;
         const uint16_t* qkv = a.q + size_t(b) * a.q_stride;
         const float* crow = a.cos_t + size_t(pos) * half;
         const float* srow = a.sin_t + size_t(pos) * half;
         const int nq = nkv * GROUP;
-        for (int it = tid; it < (GROUP + 1) * half; it += kThreads) {
+#pragma unroll
+        for (int r = 0; r < RIT; ++r) {
+            const int it = tid + r * kThreads;
             const int gh = it / half, d = it % half;
+            rx[r] = ry[r] = 0;
+            rc[r] = rs[r] = 0.f;
+            if (it < kRopeItems && (gh < GROUP || owner)) {
+                const uint16_t* src = qkv + size_t(gh < GROUP ? h * GROUP + gh : nq + h) * HD;
+                rx[r] = src[d];
+                ry[r] = src[d + half];
+                rc[r] = crow[d];
+                rs[r] = srow[d];
+            }
+        }
+        if (owner && tid < HD) vnew = qkv[size_t(nq + nkv + h) * HD + tid];
+    } else {
+        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
+#pragma unroll
+        for (int gh = 0; gh < GROUP; ++gh)
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i)
+#pragma unroll
+                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w)
+                    qraw[gh][i * (LY::kElemsPerLoad / 8) + w] =
+                        *reinterpret_cast<const uint4*>(qb + gh * HD + LY::dim(i, j, 0) + w * 8);
+    }
+
+    // ---- ring prologue: the first NB row-steps go in flight ----------------
+    // (the scheduling barrier keeps the query loads ahead of the KV loads)
+    __builtin_amdgcn_sched_barrier(0);
+    Row ring[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) load_row(ring[i], min(i, n_steps - 1));
+
+    // ---- query fragment -----------------------------------------------------
+    half2_t qv[GROUP][EPL / 2];
+    auto unpack_q = [&](int gh, int slot, const uint4 raw) {
+        const int i = slot / (LY::kElemsPerLoad / 8), w = slot % (LY::kElemsPerLoad / 8);
+        const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
+        qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
+        qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
+        qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
+        qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
+    };
+    if constexpr (FUSED) {
+        // RoPE of the GROUP query heads into LDS (every split computes the same
+        // bits); the owner also rotates K head h, and stages the new K/V row.
+        const int half = HD / 2;
+        const int nq = nkv * GROUP;
+#pragma unroll
+        for (int r = 0; r < RIT; ++r) {
+            const int it = tid + r * kThreads;
+            const int gh = it / half, d = it % half;
+            if (it >= kRopeItems || !(gh < GROUP || owner)) continue;
+            uint16_t xo, yo;
+            rotate_pair(rx[r], ry[r], rc[r], rs[r], xo, yo);
             if (gh < GROUP) {
-                const uint16_t* src = qkv + size_t(h * GROUP + gh) * HD;
-                uint16_t xo, yo;
-                rotate_pair(src[d], src[d + half], crow[d], srow[d], xo, yo);
                 s_q[gh * HD + d] = xo;
                 s_q[gh * HD + d + half] = yo;
-            } else if (owner) {
-                uint16_t* kh = const_cast<uint16_t*>(qkv) + size_t(nq + h) * HD;
-                uint16_t xo, yo;
-                rotate_pair(kh[d], kh[d + half], crow[d], srow[d], xo, yo);
+            } else {
+                uint16_t* kh = a.q + size_t(b) * a.q_stride + size_t(nq + h) * HD;
                 kh[d] = xo;  // K is rotated in place (only this workgroup reads K head h)
                 kh[d + half] = yo;
                 if constexpr (FP8) {
@@ -332,15 +419,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                 }
             }
         }
-        if (owner) {
-            const uint16_t* vh = qkv + size_t(nq + nkv + h) * HD;
-            for (int d = tid; d < HD; d += kThreads) {
-                if constexpr (FP8) {
-                    reinterpret_cast<uint8_t*>(s_new)[LY::kRowBytes + d] =
-                        uint8_t(quantize_fp8_dev(vh[d], a.scales[nkv + h]));
-                } else {
-                    reinterpret_cast<uint16_t*>(s_new)[HD + d] = vh[d];
-                }
+        if (owner && tid < HD) {
+            if constexpr (FP8) {
+                reinterpret_cast<uint8_t*>(s_new)[LY::kRowBytes + tid] =
+                    uint8_t(quantize_fp8_dev(vnew, a.scales[nkv + h]));
+            } else {
+                reinterpret_cast<uint16_t*>(s_new)[HD + tid] = vnew;
             }
         }
         __syncthreads();
@@ -356,34 +440,16 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh)
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i)
-#pragma unroll
-                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w) {
-                    const uint4 raw =
-                        *reinterpret_cast<const uint4*>(&s_q[gh * HD + LY::dim(i, j, 0) + w * 8]);
-                    const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
-                    qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
-                    qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
-                    qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
-                    qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
-                }
+            for (int sl = 0; sl < kQLoads; ++sl) {
+                const int i = sl / (LY::kElemsPerLoad / 8), w = sl % (LY::kElemsPerLoad / 8);
+                unpack_q(gh, sl,
+                         *reinterpret_cast<const uint4*>(&s_q[gh * HD + LY::dim(i, j, 0) + w * 8]));
+            }
     } else {
-        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh)
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint16_t* src = qb + gh * HD + LY::dim(i, j, 0);
-#pragma unroll
-                for (int w = 0; w < LY::kElemsPerLoad / 8; ++w) {
-                    const uint4 raw = *reinterpret_cast<const uint4*>(src + w * 8);
-                    const int p0 = i * (LY::kElemsPerLoad / 2) + w * 4;
-                    qv[gh][p0 + 0] = __builtin_bit_cast(half2_t, raw.x);
-                    qv[gh][p0 + 1] = __builtin_bit_cast(half2_t, raw.y);
-                    qv[gh][p0 + 2] = __builtin_bit_cast(half2_t, raw.z);
-                    qv[gh][p0 + 3] = __builtin_bit_cast(half2_t, raw.w);
-                }
-            }
+            for (int sl = 0; sl < kQLoads; ++sl) unpack_q(gh, sl, qraw[gh][sl]);
     }
 
     float qk_scale = a.qk_scale;
@@ -402,69 +468,57 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         for (int e = 0; e < EPL; ++e) acc[gh][e] = 0.f;
     }
 
-    auto process_chunk = [&](Chunk& c, int chunk) {
-        const int t0 = t_begin + chunk * CHUNK + g;
+    auto process_row = [&](Row& r, int step) {
+        const int t = lane_t0 + step * kStepTokens;
         if constexpr (FUSED) {
             // The new token (and padding past it) takes the appended row from LDS.
+            if (t >= L - 1) {
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (t0 + r * kRowsPerStep >= L - 1) {
-#pragma unroll
-                    for (int i = 0; i < LOADS; ++i) {
-                        c.k[r][i] = s_new[(i * 128 + j * 16) / 16];
-                        c.v[r][i] = s_new[LY::kRowBytes / 16 + (i * 128 + j * 16) / 16];
-                    }
-                }
-        }
-        float s[R][GROUP];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int gh = 0; gh < GROUP; ++gh) s[r][gh] = 0.f;
-#pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint32_t w4[4] = {c.k[r][i].x, c.k[r][i].y, c.k[r][i].z, c.k[r][i].w};
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    if constexpr (FP8) {
-                        const half2_t k01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w4[w]), 1.0f, false);
-                        const half2_t k23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w4[w]), 1.0f, true);
-                        const int p = i * 8 + w * 2;
-#pragma unroll
-                        for (int gh = 0; gh < GROUP; ++gh) {
-                            s[r][gh] = __builtin_amdgcn_fdot2(k01, qv[gh][p], s[r][gh], false);
-                            s[r][gh] = __builtin_amdgcn_fdot2(k23, qv[gh][p + 1], s[r][gh], false);
-                        }
-                    } else {
-                        const half2_t kk = __builtin_bit_cast(half2_t, w4[w]);
-                        const int p = i * 4 + w;
-#pragma unroll
-                        for (int gh = 0; gh < GROUP; ++gh)
-                            s[r][gh] = __builtin_amdgcn_fdot2(kk, qv[gh][p], s[r][gh], false);
-                    }
+                for (int i = 0; i < LOADS; ++i) {
+                    r.k[i] = s_new[(i * 128 + j * 16) / 16];
+                    r.v[i] = s_new[LY::kRowBytes / 16 + (i * 128 + j * 16) / 16];
                 }
             }
         }
-        float cmax[GROUP];
+        float s[GROUP];
 #pragma unroll
-        for (int gh = 0; gh < GROUP; ++gh) cmax[gh] = -INFINITY;
+        for (int gh = 0; gh < GROUP; ++gh) s[gh] = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const bool valid = (t0 + r * kRowsPerStep) < t_end;
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t w4[4] = {r.k[i].x, r.k[i].y, r.k[i].z, r.k[i].w};
 #pragma unroll
-            for (int gh = 0; gh < GROUP; ++gh) {
-                const float x = group8_sum(s[r][gh]) * qk_scale;
-                s[r][gh] = valid ? x : -INFINITY;
-                cmax[gh] = fmaxf(cmax[gh], s[r][gh]);
+            for (int w = 0; w < 4; ++w) {
+                if constexpr (FP8) {
+                    const half2_t k01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w4[w]), 1.0f, false);
+                    const half2_t k23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w4[w]), 1.0f, true);
+                    const int p = i * 8 + w * 2;
+#pragma unroll
+                    for (int gh = 0; gh < GROUP; ++gh) {
+                        s[gh] = __builtin_amdgcn_fdot2(k01, qv[gh][p], s[gh], false);
+                        s[gh] = __builtin_amdgcn_fdot2(k23, qv[gh][p + 1], s[gh], false);
+                    }
+                } else {
+                    const half2_t kk = __builtin_bit_cast(half2_t, w4[w]);
+                    const int p = i * 4 + w;
+#pragma unroll
+                    for (int gh = 0; gh < GROUP; ++gh)
+                        s[gh] = __builtin_amdgcn_fdot2(kk, qv[gh][p], s[gh], false);
+                }
             }
+        }
+        const bool valid = t < t_end;
+#pragma unroll
+        for (int gh = 0; gh < GROUP; ++gh) {
+            const float x = group8_sum(s[gh]) * qk_scale;
+            s[gh] = valid ? x : -INFINITY;
         }
         // Per-lane running max with a lazy rescale: the reference point only
         // moves when a score exceeds it by more than 2^kLazyLog2, so p <= 2^8
-        // and the (rare) accumulator rescale replaces a cross-lane max per chunk.
+        // and the (rare) accumulator rescale replaces a cross-lane max per row.
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh) {
-            if (cmax[gh] > m_run[gh] + kLazyLog2) {
-                const float m_new = cmax[gh];
+            if (s[gh] > m_run[gh] + kLazyLog2) {
+                const float m_new = s[gh];
                 const float alpha = fast_exp2(m_run[gh] - m_new);
                 l_run[gh] *= alpha;
 #pragma unroll
@@ -472,119 +526,132 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                 m_run[gh] = m_new;
             }
         }
+        float p[GROUP];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float p[GROUP];
+        for (int gh = 0; gh < GROUP; ++gh) {
+            p[gh] = fast_exp2(s[gh] - m_run[gh]);
+            l_run[gh] += p[gh];
+        }
 #pragma unroll
-            for (int gh = 0; gh < GROUP; ++gh) {
-                p[gh] = fast_exp2(s[r][gh] - m_run[gh]);
-                l_run[gh] += p[gh];
-            }
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t w4[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint32_t w4[4] = {c.v[r][i].x, c.v[r][i].y, c.v[r][i].z, c.v[r][i].w};
+            for (int w = 0; w < 4; ++w) {
+                if constexpr (FP8) {
+                    const float2_t v01 = __builtin_amdgcn_cvt_pk_f32_fp8(int(w4[w]), false);
+                    const float2_t v23 = __builtin_amdgcn_cvt_pk_f32_fp8(int(w4[w]), true);
+                    const int e = i * 16 + w * 4;
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    if constexpr (FP8) {
-                        const float2_t v01 = __builtin_amdgcn_cvt_pk_f32_fp8(int(w4[w]), false);
-                        const float2_t v23 = __builtin_amdgcn_cvt_pk_f32_fp8(int(w4[w]), true);
-                        const int e = i * 16 + w * 4;
+                    for (int gh = 0; gh < GROUP; ++gh) {
+                        acc[gh][e + 0] = fmaf(p[gh], v01[0], acc[gh][e + 0]);
+                        acc[gh][e + 1] = fmaf(p[gh], v01[1], acc[gh][e + 1]);
+                        acc[gh][e + 2] = fmaf(p[gh], v23[0], acc[gh][e + 2]);
+                        acc[gh][e + 3] = fmaf(p[gh], v23[1], acc[gh][e + 3]);
+                    }
+                } else {
+                    const half2_t vv = __builtin_bit_cast(half2_t, w4[w]);
+                    const int e = i * 8 + w * 2;
 #pragma unroll
-                        for (int gh = 0; gh < GROUP; ++gh) {
-                            acc[gh][e + 0] = fmaf(p[gh], v01[0], acc[gh][e + 0]);
-                            acc[gh][e + 1] = fmaf(p[gh], v01[1], acc[gh][e + 1]);
-                            acc[gh][e + 2] = fmaf(p[gh], v23[0], acc[gh][e + 2]);
-                            acc[gh][e + 3] = fmaf(p[gh], v23[1], acc[gh][e + 3]);
-                        }
-                    } else {
-                        const half2_t vv = __builtin_bit_cast(half2_t, w4[w]);
-                        const int e = i * 8 + w * 2;
-#pragma unroll
-                        for (int gh = 0; gh < GROUP; ++gh) {
-                            acc[gh][e + 0] = fmaf(p[gh], float(vv[0]), acc[gh][e + 0]);
-                            acc[gh][e + 1] = fmaf(p[gh], float(vv[1]), acc[gh][e + 1]);
-                        }
+                    for (int gh = 0; gh < GROUP; ++gh) {
+                        acc[gh][e + 0] = fmaf(p[gh], float(vv[0]), acc[gh][e + 0]);
+                        acc[gh][e + 1] = fmaf(p[gh], float(vv[1]), acc[gh][e + 1]);
                     }
                 }
             }
         }
     };
 
-    // ---- main loop: wave w takes chunks w, w+4, ... -------------------------
-    // The next chunk's loads are issued before the current chunk is consumed.
-    // The prefetch is unconditional (the last one re-reads the wave's final
-    // chunk, an L2 hit) so no control-flow join forces a full vmcnt wait.
-    if (c < n_chunks) {
-        for (;;) {
-            load_chunk(cb, min(c + kWaves, n_chunks - 1));
-            process_chunk(ca, c);
-            c += kWaves;
-            if (c >= n_chunks) break;
-            load_chunk(ca, min(c + kWaves, n_chunks - 1));
-            process_chunk(cb, c);
-            c += kWaves;
-            if (c >= n_chunks) break;
+    // ---- main loop: a ring of NB row-steps per lane -------------------------
+    // Each slot is consumed and refilled with the step NB ahead (past the end
+    // the refill re-reads the split's last step, a cache hit). Whole rounds
+    // keep the loop single-exit with the same load sequence on every path, so
+    // the compiler waits only for the slot being consumed; the last partial
+    // round is drained without refills.
+    const int n_full = n_steps / NB;
+    for (int round = 0; round < n_full; ++round) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int step = round * NB + i;
+            process_row(ring[i], step);
+            load_row(ring[i], min(step + NB, n_steps - 1));
         }
+    }
+    {
+        const int rem = n_steps - n_full * NB;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (i < rem) process_row(ring[i], n_full * NB + i);
     }
 
-    // ---- merge the wave's 8 token groups onto the wave's largest reference ---
+    // ---- merge: token-group pairs in registers, then the workgroup in LDS ---
+    // Lanes i and i+8 of a 16-lane row hold token groups g, g^1 with the same
+    // head-dim slice; one row_ror:8 DPP add merges the pair onto its larger
+    // reference. Lanes 0..7 of each row then hold one partial (m, l, o[]) and
+    // the kParts = 4 * kWaves partials per head are summed through LDS.
+    constexpr int kParts = 4 * kWaves;
 #pragma unroll
     for (int gh = 0; gh < GROUP; ++gh) {
-        const float mw = wave_max_of_groups(m_run[gh]);
-        const float f = fast_exp2(m_run[gh] - mw);  // groups that saw no row hold l = acc = 0
-        m_run[gh] = mw;
-        l_run[gh] *= f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[gh][e] *= f;
-        float l = l_run[gh];
-        l += dpp<0x128>(l);
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        l_run[gh] = l;
+        const float mp = fmaxf(m_run[gh], dpp<0x128>(m_run[gh]));
+        const float f = fast_exp2(m_run[gh] - mp);  // groups that saw no row hold l = acc = 0
+        const float l = l_run[gh] * f;
+        l_run[gh] = l + dpp<0x128>(l);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            float x = acc[gh][e];
-            x += dpp<0x128>(x);
-            x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            acc[gh][e] = x;
+            const float x = acc[gh][e] * f;
+            acc[gh][e] = x + dpp<0x128>(x);
         }
+        m_run[gh] = mp;
     }
-    if (lane < kLanesPerRow) {
+    {
+        const int part = wave * 4 + (lane >> 4);
+        if ((lane & 15) < kLanesPerRow) {
 #pragma unroll
-        for (int gh = 0; gh < GROUP; ++gh) {
+            for (int gh = 0; gh < GROUP; ++gh) {
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i)
+                for (int i = 0; i < LOADS; ++i)
 #pragma unroll
-                for (int u = 0; u < LY::kElemsPerLoad; ++u)
-                    s_o[wave][gh * HD + LY::dim(i, j, u)] = acc[gh][i * LY::kElemsPerLoad + u];
-            if (lane == 0) {
-                s_m[wave][gh] = m_run[gh];
-                s_l[wave][gh] = l_run[gh];
+                    for (int u = 0; u < LY::kElemsPerLoad; u += 4)
+                        *reinterpret_cast<float4*>(&s_acc[part][gh * HD + LY::dim(i, j, u)]) =
+                            make_float4(acc[gh][i * LY::kElemsPerLoad + u],
+                                        acc[gh][i * LY::kElemsPerLoad + u + 1],
+                                        acc[gh][i * LY::kElemsPerLoad + u + 2],
+                                        acc[gh][i * LY::kElemsPerLoad + u + 3]);
+                if (j == 0) {
+                    s_pm[part][gh] = m_run[gh];
+                    s_pl[part][gh] = l_run[gh];
+                }
             }
         }
     }
     __syncthreads();
 
-    // ---- merge the 4 waves; write the output or this split's partial -------
+    // ---- merge the partials: the output, or this split's partial ------------
+    // Thread t owns head-dim pair (2t, 2t+1).
     const size_t rec = (size_t(b) * nkv + h) * a.num_splits;  // first record of (b, h)
-    for (int o = tid; o < GHD; o += kThreads) {
-        const int gh = o / HD;
+    for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
+        const int gh = (2 * q2) / HD;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][gh]);
-        float lsum = 0.f, osum = 0.f;
+        for (int p = 0; p < kParts; ++p) M = fmaxf(M, s_pm[p][gh]);
+        float lsum = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float f = fast_exp2(s_m[w][gh] - M);  // 0 for a wave that saw no token
-            lsum += f * s_l[w][gh];
-            osum += f * s_o[w][o];
+        for (int p = 0; p < kParts; ++p) {
+            const float f = fast_exp2(s_pm[p][gh] - M);  // 0 for a partial that saw no token
+            lsum += f * s_pl[p][gh];
+            const float2 v = *reinterpret_cast<const float2*>(&s_acc[p][2 * q2]);
+            o0 += f * v.x;
+            o1 += f * v.y;
         }
         if (n_active == 1) {
-            out_b[o] = __builtin_bit_cast(uint16_t, f16(osum * v_scale / lsum));
-        } else {
-            store_agent(a.part_o + (rec + split) * GHD + o, osum * v_scale);
-            if (o % HD == 0) {
+            const uint32_t pair = uint32_t(__builtin_bit_cast(uint16_t, f16(o0 * v_scale / lsum))) |
+                                  (uint32_t(__builtin_bit_cast(uint16_t, f16(o1 * v_scale / lsum))) << 16);
+            *reinterpret_cast<uint32_t*>(out_b + 2 * q2) = pair;
+        } else {  // the partial, as 64-bit agent-scope stores
+            const uint64_t v = uint64_t(__builtin_bit_cast(uint32_t, o0 * v_scale)) |
+                               (uint64_t(__builtin_bit_cast(uint32_t, o1 * v_scale)) << 32);
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_o + (rec + split) * GHD) + q2, v,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((2 * q2) % HD == 0) {
                 store_agent(a.part_ml + (rec + split) * 2 * GROUP + gh, M);
                 store_agent(a.part_ml + (rec + split) * 2 * GROUP + GROUP + gh, lsum);
             }
@@ -619,73 +686,74 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     __syncthreads();
     if (!s_last) return;
 
-    // ---- combine: every partial load is issued before any is used ----------
-    // Wave w owns splits w*SB .. w*SB+SB-1 of each round of 4*SB splits; lane
-    // slot i holds floats 2*(lane + 64 i) and +1 of a record (GROUP*HD floats).
+    // ---- combine ------------------------------------------------------------
+    // Thread t owns output floats 2t, 2t+1 and reads them from CB splits per
+    // batch. The (m, l) loads and the first batch are issued before anything
+    // waits on them; the split weights are computed while the batch is in
+    // flight.
+    constexpr int CB = 16;  // splits per batch
+    constexpr int MLPT = (2 * GROUP * kMaxSplits + kThreads - 1) / kThreads;
+    const int n_ml = n_active * 2 * GROUP;
     const float* ml = a.part_ml + rec * 2 * GROUP;
-    for (int e = tid; e < n_active * 2 * GROUP; e += kThreads) s_ml[e] = load_agent(ml + e);
-    float racc[PER64][2];
+    const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + rec * GHD);
+    float mlv[MLPT];
 #pragma unroll
-    for (int i = 0; i < PER64; ++i) racc[i][0] = racc[i][1] = 0.f;
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    for (int base = 0; base < n_active; base += kWaves * SB) {
-        uint64_t val[SB][PER64];
+    for (int r = 0; r < MLPT; ++r) {
+        const int e = tid + r * kThreads;
+        mlv[r] = e < n_ml ? load_agent(ml + e) : 0.f;
+    }
+    uint64_t val[CB];
+    auto issue = [&](int q2, int base) {
 #pragma unroll
-        for (int k = 0; k < SB; ++k) {
-            const int sp = base + wave_u * SB + k;  // wave-uniform: scalar base address
-            const float* rp = a.part_o + (rec + min(sp, n_active - 1)) * GHD;
+        for (int k = 0; k < CB; ++k)
+            val[k] = __hip_atomic_load(po + size_t(min(base + k, n_active - 1)) * (GHD / 2) + q2,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    issue(min(tid, GHD / 2 - 1), 0);
 #pragma unroll
-            for (int i = 0; i < PER64; ++i) {
-                const int q2 = min(lane + 64 * i, GHD / 2 - 1);
-                val[k][i] = load_agent_u64(rp + 2 * q2);
-            }
-        }
-        if (base == 0) {  // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s
-            __syncthreads();
-            for (int gh = wave; gh < GROUP; gh += kWaves) {
-                float mx = -INFINITY;
-                for (int sp = lane; sp < n_active; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
-                mx = wave_max(mx);
-                float ls = 0.f;
-                for (int sp = lane; sp < n_active; sp += 64)
-                    ls += fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * s_ml[sp * 2 * GROUP + GROUP + gh];
-                const float inv = 1.0f / wave_sum(ls);
-                for (int sp = lane; sp < n_active; sp += 64)
-                    s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * inv;
-            }
-            __syncthreads();
-        }
+    for (int r = 0; r < MLPT; ++r) {
+        const int e = tid + r * kThreads;
+        if (e < n_ml) s_ml[e] = mlv[r];
+    }
+    __syncthreads();
+    // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s, one wave per head
+    for (int gh = wave; gh < GROUP; gh += kWaves) {
+        float mx = -INFINITY;
+        for (int sp = lane; sp < n_active; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
+        mx = wave_max(mx);
+        float ls = 0.f;
+        for (int sp = lane; sp < n_active; sp += 64)
+            ls += fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * s_ml[sp * 2 * GROUP + GROUP + gh];
+        const float inv = 1.0f / wave_sum(ls);
+        for (int sp = lane; sp < n_active; sp += 64)
+            s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * inv;
+    }
+    __syncthreads();
+    for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
+        const int gh = (2 * q2) / HD;
+        float r0 = 0.f, r1 = 0.f;
+        for (int base = 0; base < n_active; base += CB) {
+            if (base > 0 || q2 != tid) issue(q2, base);
 #pragma unroll
-        for (int k = 0; k < SB; ++k) {
-            const int sp = base + wave_u * SB + k;
-            if (sp >= n_active) break;
+            for (int k4 = 0; k4 < CB; k4 += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(&s_wt[gh][base + k4]);
+                const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int i = 0; i < PER64; ++i) {
-                const int q2 = lane + 64 * i;
-                if (q2 < GHD / 2) {
-                    const float w = s_wt[(2 * q2) / HD][sp];
-                    racc[i][0] = fmaf(w, __builtin_bit_cast(float, uint32_t(val[k][i])), racc[i][0]);
-                    racc[i][1] = fmaf(w, __builtin_bit_cast(float, uint32_t(val[k][i] >> 32)), racc[i][1]);
+                for (int u = 0; u < 4; ++u) {
+                    if (base + k4 + u < n_active) {
+                        const uint64_t v = val[k4 + u];
+                        r0 = fmaf(wk[u], __builtin_bit_cast(float, uint32_t(v)), r0);
+                        r1 = fmaf(wk[u], __builtin_bit_cast(float, uint32_t(v >> 32)), r1);
+                    }
                 }
             }
         }
-    }
-    // cross-wave sum, then the fp16 output (and, fused, the rotated Q in place)
-#pragma unroll
-    for (int i = 0; i < PER64; ++i) {
-        const int q2 = lane + 64 * i;
-        if (q2 < GHD / 2) {
-            s_o[wave][2 * q2] = racc[i][0];
-            s_o[wave][2 * q2 + 1] = racc[i][1];
-        }
-    }
-    __syncthreads();
-    for (int o = tid; o < GHD; o += kThreads) {
-        float x = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) x += s_o[w][o];
-        out_b[o] = __builtin_bit_cast(uint16_t, f16(x));
-        if constexpr (FUSED) a.q[size_t(b) * a.q_stride + size_t(h) * GHD + o] = s_q[o];
+        const uint32_t pair = uint32_t(__builtin_bit_cast(uint16_t, f16(r0))) |
+                              (uint32_t(__builtin_bit_cast(uint16_t, f16(r1))) << 16);
+        *reinterpret_cast<uint32_t*>(out_b + 2 * q2) = pair;
+        if constexpr (FUSED)
+            *reinterpret_cast<uint32_t*>(a.q + size_t(b) * a.q_stride + size_t(h) * GHD + 2 * q2) =
+                *reinterpret_cast<const uint32_t*>(&s_q[2 * q2]);
     }
 }
 
@@ -743,6 +811,12 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 float qk_scale_for(int head_dim) { return float(1.4426950408889634 / std::sqrt(double(head_dim))); }
 
+// Zero arrival counters (the state each launch leaves behind).
+int init_workspace(void* ws, size_t bytes, hipStream_t stream) {
+    (void)bytes;
+    return fill_u32(ws, 0u, kCounterBytes / 4, stream);
+}
+
 // Library-owned workspace of af_cached_attention (one per device).
 struct OwnedWorkspace {
     void* ptr = nullptr;
@@ -773,7 +847,7 @@ int owned_workspace(int batch, int n_q_heads, int head_dim, hipStream_t stream, 
         }
         void* p = nullptr;
         AF_TRY_HIP(hipMalloc(&p, need));
-        int st = fill_u32(p, 0u, kCounterBytes / 4, stream);
+        int st = init_workspace(p, need, stream);
         if (st) {
             (void)hipFree(p);
             return st;
@@ -819,7 +893,7 @@ int default_splits(int max_seq_len, int batch, int n_kv_heads) {
 
 // Smallest split count whose span fits the LDS-staged block table.
 static int min_splits_for_table(int max_seq_len, int block_size) {
-    const int max_span = (kMaxTableLds - 2) * block_size - 16;
+    const int max_span = (kMaxTableLds - 2) * block_size - 2 * kStepTokens;
     return ceil_div(max_seq_len, max_span);
 }
 
@@ -837,7 +911,7 @@ extern "C" size_t af_attention_workspace_size(int batch, int n_q_heads, int n_kv
 extern "C" int af_attention_workspace_init(void* workspace, size_t workspace_bytes,
                                            af_stream_t stream) {
     if (!workspace || workspace_bytes < kCounterBytes) return AF_ERR_WORKSPACE;
-    return fill_u32(workspace, 0u, kCounterBytes / 4, static_cast<hipStream_t>(stream));
+    return init_workspace(workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int af_attention_default_splits(int max_seq_len, int batch, int n_kv_heads) {
