@@ -28,9 +28,11 @@ constexpr int kWave = 64;
 // Longest split grid; bounds the per-(sequence, head) partial buffers and lets
 // the combine read every partial in one round of loads.
 constexpr int kMaxSplits = 128;
-// Fewest tokens a split may own: below this the partial (m, l, o[]) traffic and
-// the combine cost more than the split saves.
+// Target tokens per split of small launches: below this the partial (m, l, o[])
+// traffic and the combine cost more than the split saves.
 constexpr int kMinSpan = 64;
+// Target tokens per split of batched launches (equal work per workgroup).
+constexpr int kBatchSpan = 512;
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -74,9 +76,12 @@ inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, 
 // Number of compute units of the current device (cached per device).
 int device_compute_units();
 
-// Default split count: about 3/4 of a workgroup per CU, each split at least
-// kMinSpan tokens, at most kMaxSplits.
+// Default split count: batched launches cover about kBatchSpan tokens per
+// split; small ones about 3/4 of a workgroup per CU, each split at least
+// kMinSpan tokens; at most kMaxSplits.
 int default_splits(int max_seq_len, int batch, int n_kv_heads);
+// Target tokens per split that goes with default_splits.
+int default_span(int batch, int n_kv_heads);
 
 // Fill kernel launcher shared by the runtime ABI and workspace init.
 int fill_u32(void* dst, uint32_t value, size_t n_words, hipStream_t stream);

@@ -160,7 +160,7 @@ struct AttnArgs {
     int64_t out_stride;
     int32_t n_kv_heads;
     int32_t num_splits;
-    int32_t min_span;
+    int32_t span_tokens;  // target tokens per split: a sequence uses ceil(L / span) splits
     float qk_scale;       // log2(e) / sqrt(head_dim)
     const float* scales;  // FP8: [2][n_kv_heads] (K, V) of this layer
     float* part_o;        // [batch][n_kv_heads][splits][GROUP * head_dim]
@@ -267,11 +267,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
-    // Balanced partition in whole workgroup steps (kStepTokens rows): split s
-    // of n_active owns steps [s*C/n, (s+1)*C/n).
+    // Balanced partition in whole workgroup steps (kStepTokens rows): a
+    // sequence of C steps uses n = min(num_splits, ceil(C / span)) splits and
+    // split s owns steps [s*C/n, (s+1)*C/n).
     const int total_steps = (L + kStepTokens - 1) / kStepTokens;
-    const int min_steps = max(1, a.min_span / kStepTokens);
-    const int n_active = max(1, min(a.num_splits, total_steps / min_steps));
+    const int span_steps = max(1, a.span_tokens / kStepTokens);
+    const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
     if (split >= n_active) return;
     const int step_begin = int(int64_t(split) * total_steps / n_active);
     const int step_end = int(int64_t(split + 1) * total_steps / n_active);
@@ -879,8 +880,18 @@ int device_compute_units() {
     return cache[dev];
 }
 
+// Batches with at least half a (sequence, KV head) pair per CU balance the work
+// per workgroup: every split covers about kBatchSpan tokens, so a sequence's
+// split count follows its length. Smaller launches split every sequence the
+// same way to fill the CUs.
+int default_span(int batch, int n_kv_heads) {
+    return int64_t(batch) * n_kv_heads * 2 >= device_compute_units() ? kBatchSpan : kMinSpan;
+}
+
 int default_splits(int max_seq_len, int batch, int n_kv_heads) {
     if (max_seq_len <= 0) return 1;
+    if (default_span(batch, n_kv_heads) == kBatchSpan)
+        return std::min(std::max(ceil_div(max_seq_len, kBatchSpan), 1), kMaxSplits);
     const int pairs = std::max(1, batch * n_kv_heads);
     // About 3/4 of a workgroup per CU: measured best on MI355X for batch 1
     // (the split-K combine grows with the split count faster than more
@@ -961,7 +972,7 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     a.out_stride = int64_t(n_q_heads) * head_dim;
     a.n_kv_heads = n_kv_heads;
     a.num_splits = num_splits;
-    a.min_span = kMinSpan;
+    a.span_tokens = kMinSpan;
     a.qk_scale = qk_scale_for(head_dim);
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
@@ -1050,10 +1061,13 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     if (batch == 0) return AF_OK;
     if (int64_t(batch) * nkv > kMaxCounters) return AF_ERR_UNSUPPORTED;
     const int min_sp = min_splits_for_table(std::max(max_seq_len, 1), bs);
-    if (num_splits <= 0)
+    int span = kMinSpan;
+    if (num_splits <= 0) {
         num_splits = std::max(default_splits(max_seq_len, batch, nkv), min_sp);
-    else if (num_splits < min_sp)
+        span = default_span(batch, nkv);
+    } else if (num_splits < min_sp) {
         return AF_ERR_INVALID_ARG;
+    }
     if (num_splits > kMaxSplits) return AF_ERR_OUT_OF_RANGE;
     if (!workspace || workspace_bytes < attn_workspace_bytes(batch, n_q_heads, hd, num_splits))
         return AF_ERR_WORKSPACE;
@@ -1086,7 +1100,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     a.out_stride = out_stride;
     a.n_kv_heads = nkv;
     a.num_splits = num_splits;
-    a.min_span = kMinSpan;
+    a.span_tokens = span;
     a.qk_scale = qk_scale_for(hd);
     a.scales = fp8 ? pool->scales + size_t(layer) * 2 * nkv : nullptr;
     a.part_o = w.part_o;

@@ -276,6 +276,9 @@ def bench_paged(args, dev, kv, lib, info):
     out = dev.DeviceBuffer(LAYERS * B * Q_DIM * 2)
     d_tables, d_lens = dev.DeviceBuffer.from_array(tables), dev.DeviceBuffer.from_array(lens)
     d_slots, d_pos = dev.DeviceBuffer.from_array(slots), dev.DeviceBuffer.from_array(positions)
+    # 0 = the library's default partition (for batches: ~512 tokens per split,
+    # so each sequence's split count follows its length)
+    launch_splits = args.splits
     splits = args.splits or max(kv.default_splits(max_len, B, NKV), 1)
     ws = kv.AttentionWorkspace(B, NQ, NKV, HD, splits, stream)
     stream.sync()
@@ -285,14 +288,14 @@ def bench_paged(args, dev, kv, lib, info):
             kv.launch_paged_decode_fused(qkv.ptr + l * B * QKV * 2, B, desc, l, d_slots, d_pos,
                                          d_cos, d_sin, max_pos, d_tables, max_blocks, max_len,
                                          out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ, ws,
-                                         num_splits=splits, stream=stream)
+                                         num_splits=launch_splits, stream=stream)
 
     def attention_only():
         for l in range(LAYERS):
             kv.launch_paged_attention(qkv.ptr + l * B * QKV * 2, QKV, desc, l, d_tables,
                                       max_blocks, d_lens, B, max_len,
                                       out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ, ws,
-                                      num_splits=splits, stream=stream)
+                                      num_splits=launch_splits, stream=stream)
 
     graphs = {"step": dev.Graph.capture(stream, step), "attn": dev.Graph.capture(stream, attention_only)}
     t = Timer(dev, stream, args.warmup)
