@@ -40,4 +40,56 @@ __device__ __forceinline__ uint32_t quantize_fp8(uint16_t h, float scale) {
     return e4m3_encode(v);
 }
 
+// ---- cross-lane reductions (wave64) -----------------------------------------
+// DPP move of v (row_mask, bank_mask all lanes; no bound_ctrl).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Cross-row exchanges of gfx950 (VALU, no LDS round trip). With a = b = v on
+// entry, v_permlane16_swap leaves rows (v0, v0, v2, v2) in a and (v1, v1, v3, v3)
+// in b (rows of 16 lanes); v_permlane32_swap leaves (lo, lo) in a and (hi, hi)
+// in b (halves of 32 lanes). Written as inline asm with both operands
+// read-write: the compiler's builtin returns the first result for both. The
+// s_nop provides the two wait states the swap needs after a VALU write.
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Sum / max over the four 16-lane rows of values that are uniform per row.
+__device__ __forceinline__ float rows_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = b = __builtin_bit_cast(uint32_t, v);
+    swap32(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float rows_max(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = b = __builtin_bit_cast(uint32_t, v);
+    swap32(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x128>(v);
+    return rows_sum(v);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    return rows_max(v);
+}
+
 }  // namespace af

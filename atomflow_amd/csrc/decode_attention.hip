@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "af_common.h"
+#include "af_device.h"
 
 namespace af {
 namespace {
@@ -47,12 +48,6 @@ constexpr int kMaxTableLds = 1024;     // block-table entries staged per split
 constexpr int kRingBudget = 126;       // VGPRs shared by the row ring and the accumulators
 constexpr float kLazyLog2 = 8.0f;      // running-max slack before a rescale (log2 units)
 constexpr float kEmptyMax = -1.0e30f;  // running max of a lane group that has seen no row
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
 
 // Sum over the 8 lanes of a token group; every lane receives the same bits.
 __device__ __forceinline__ float group8_sum(float v) {
@@ -74,52 +69,8 @@ __device__ __forceinline__ float wave_max_of_groups(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
-// Cross-row exchanges of gfx950 (VALU, no LDS round trip). With a = b = v on
-// entry, v_permlane16_swap leaves rows (v0, v0, v2, v2) in a and (v1, v1, v3, v3)
-// in b (rows of 16 lanes); v_permlane32_swap leaves (lo, lo) in a and (hi, hi)
-// in b (halves of 32 lanes). Written as inline asm with both operands
-// read-write: the compiler's builtin returns the first result for both. The
-// s_nop provides the two wait states the swap needs after a VALU write.
-__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-// Sum / max over the four 16-lane rows of values that are uniform per row.
-__device__ __forceinline__ float rows_sum(float v) {
-    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
-    swap16(a, b);
-    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-    a = b = __builtin_bit_cast(uint32_t, v);
-    swap32(a, b);
-    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-}
-__device__ __forceinline__ float rows_max(float v) {
-    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
-    swap16(a, b);
-    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-    a = b = __builtin_bit_cast(uint32_t, v);
-    swap32(a, b);
-    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
 // Sum over the 8 token groups of the lanes that share lane & 7.
 __device__ __forceinline__ float groups_sum(float v) { return rows_sum(v + dpp<0x128>(v)); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x141>(v);
-    v += dpp<0x128>(v);
-    return rows_sum(v);
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp<0xB1>(v));
-    v = fmaxf(v, dpp<0x4E>(v));
-    v = fmaxf(v, dpp<0x141>(v));
-    v = fmaxf(v, dpp<0x128>(v));
-    return rows_max(v);
-}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

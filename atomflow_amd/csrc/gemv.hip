@@ -1,0 +1,277 @@
+// gemv.hip — W8A16 GEMV (FP8 E4M3 weights with fp16 group scales, fp16
+// activations) and the fused decode QKV projection + RoPE + KV append, gfx950.
+//
+// y[n] = sum_k e4m3(W[n, k]) * scale[n, k / group] * x[k]   (the reference's
+// w8a16_gemv_kernel, src/kernel/qkv_gemm.cu:32-110), fp32 accumulation, fp16
+// output. M = 1: every weight byte is read once, so the roofline is HBM.
+//
+// Design:
+//  * One wave owns RPW (2..5) rows, chosen so the waves make a whole number of
+//    rounds of one wave per SIMD. A weight row is read in 1 KB chunks, 16
+//    bytes per lane (global_load_dwordx4); the activation slice of a chunk is
+//    loaded once and shared by the wave's rows. All of a pass's loads (NCH
+//    chunks x RPW rows; one pass for K up to 8 KB) are issued before any is used.
+//  * E4M3 -> fp16 is exact (v_cvt_scalef32_pk_f16_fp8, scale 1), the product of
+//    two fp16 values is exact in fp32, so each 16-element slice is summed with
+//    v_dot2c_f32_f16 in fp32 and scaled once by its group scale.
+//  * Lane partials are summed with DPP and v_permlane16/32_swap (no LDS).
+//  * The fused QKV kernel gives each wave two rotation pairs (d, d+HD/2) and
+//    (d+1, d+1+HD/2) of one head, so RoPE and the KV append run on the rounded
+//    fp16 results in registers: the output equals af_w8a16_gemv followed by
+//    af_rope_append bit for bit (a row's arithmetic does not depend on which
+//    wave computes it or on the chunks per pass).
+#include <algorithm>
+#include <cmath>
+
+#include "af_common.h"
+#include "af_device.h"
+
+namespace af {
+namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kGemvWaves = 4;                 // plain GEMV: waves per workgroup
+constexpr int kGemvThreads = kGemvWaves * 64;
+constexpr int kQkvWaves = 5;                  // fused QKV: 2 rotation pairs per wave
+constexpr int kQkvThreads = kQkvWaves * 64;
+constexpr int kChunkBytes = 64 * 16;          // one weight-row chunk per wave load
+
+// sum_i e4m3(w_i) * x_i over the 16 codes of `w` and 16 fp16 activations.
+__device__ __forceinline__ float dot16(const uint4 w, const uint4 xa, const uint4 xb) {
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t xx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(ww[i]), 1.0f, false);
+        const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(ww[i]), 1.0f, true);
+        acc = __builtin_amdgcn_fdot2(w01, __builtin_bit_cast(half2_t, xx[2 * i]), acc, false);
+        acc = __builtin_amdgcn_fdot2(w23, __builtin_bit_cast(half2_t, xx[2 * i + 1]), acc, false);
+    }
+    return acc;
+}
+
+// Lane partials of rows[r] (r < RPW) over the whole K dimension, NCH chunks
+// per pass. Chunks past K are read at a clamped address and contribute 0.
+template <int RPW, int NCH>
+__device__ __forceinline__ void row_partials(const uint8_t* __restrict__ w,
+                                             const uint16_t* __restrict__ x,
+                                             const uint16_t* __restrict__ scales,
+                                             const int (&rows)[RPW], int k, int group_size,
+                                             int groups, int lane, float (&acc)[RPW]) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
+    for (int base = 0; base < k; base += NCH * kChunkBytes) {
+        uint4 xa[NCH], xb[NCH], wv[NCH][RPW];
+        uint16_t sc[NCH][RPW];
+        bool in[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int k0 = base + c * kChunkBytes + lane * 16;
+            in[c] = k0 < k;
+            const int kk = in[c] ? k0 : 0;
+            xa[c] = *reinterpret_cast<const uint4*>(x + kk);
+            xb[c] = *reinterpret_cast<const uint4*>(x + kk + 8);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                wv[c][r] = *reinterpret_cast<const uint4*>(w + size_t(rows[r]) * k + kk);
+                sc[c][r] = scales[size_t(rows[r]) * groups + kk / group_size];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const float part = dot16(wv[c][r], xa[c], xb[c]);
+                acc[r] = in[c] ? fmaf(h2f(sc[c][r]), part, acc[r]) : acc[r];
+            }
+    }
+}
+
+// ---- plain GEMV: wave w of block b owns rows (4b + w) * RPW .. + RPW - 1 ----
+// RPW is picked so there is about one wave per SIMD of the device, NCH so one
+// pass covers K for the usual widths.
+template <int RPW, int NCH>
+__global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(
+    const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y, int n, int k, int group_size) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kGemvWaves + wave) * RPW;
+    if (row0 >= n) return;
+    int rows[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rows[r] = min(row0 + r, n - 1);
+    float acc[RPW];
+    row_partials<RPW, NCH>(w, x, scales, rows, k, group_size, k / group_size, lane, acc);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const float tot = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < n) y[row0 + r] = f2h(tot);
+    }
+}
+
+// ---- fused decode QKV projection + RoPE + KV append --------------------------
+// Output rows of qkv_out = [Q heads | K heads | V heads] x head_dim. Rotation
+// pairs are numbered p = head * HD/2 + d; wave w of block b takes pairs
+// 2(b*kQkvWaves + w) and +1, i.e. rows (head, d), (head, d+1) and their
+// partners + HD/2.
+template <int NCH>
+__global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(
+    const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ scales, int k, int group_size, uint16_t* __restrict__ qkv,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos_host,
+    const int32_t* __restrict__ d_pos, int max_seq, int n_q_heads, int n_kv_heads, int head_dim,
+    int32_t* __restrict__ d_status) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int half = head_dim / 2;
+    const int n_pairs = (n_q_heads + 2 * n_kv_heads) * half;
+    const int p0 = 2 * (blockIdx.x * kQkvWaves + wave);
+    if (p0 >= n_pairs) return;  // half is even, so pair p0 + 1 is in the same head
+    const int head = p0 / half;
+    const int dA = p0 % half;  // pairs (dA, dA+half), (dA+1, dA+1+half)
+    const int hrow = head * head_dim;
+    const int rows[4] = {hrow + dA, hrow + dA + 1, hrow + dA + half, hrow + dA + 1 + half};
+    float acc[4];
+    row_partials<4, NCH>(w, x, scales, rows, k, group_size, k / group_size, lane, acc);
+    uint16_t yv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) yv[r] = f2h(wave_sum(acc[r]));
+    // The position is read once the weight loads are in flight; an
+    // out-of-range one writes nothing.
+    const int pos = d_pos ? *d_pos : pos_host;
+    if (pos < 0 || pos >= max_seq) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && d_status) *d_status = AF_ERR_OUT_OF_RANGE;
+        return;
+    }
+    if (lane != 0) return;
+    const int kv_dim = n_kv_heads * head_dim;
+    const int kind = head < n_q_heads ? 0 : (head < n_q_heads + n_kv_heads ? 1 : 2);  // Q, K, V
+    uint16_t out[4] = {yv[0], yv[1], yv[2], yv[3]};
+    if (kind < 2) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {  // the reference's rope_kernel arithmetic, rope.cu:30-45
+            const float c = cos_t[size_t(pos) * half + dA + p];
+            const float s = sin_t[size_t(pos) * half + dA + p];
+            const float xf = h2f(yv[p]), yf = h2f(yv[2 + p]);
+            const float xc = xf * c;
+            const float ys = yf * s;
+            const float xs = xf * s;
+            const float yc = yf * c;
+            out[p] = f2h(xc - ys);
+            out[2 + p] = f2h(xs + yc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qkv[rows[r]] = out[r];
+    if (kind > 0) {
+        uint16_t* cache = kind == 1 ? k_cache : v_cache;
+        const int hk = head - n_q_heads - (kind == 2 ? n_kv_heads : 0);
+        uint16_t* dst = cache + size_t(pos) * kv_dim + size_t(hk) * head_dim;
+        dst[dA] = out[0];
+        dst[dA + 1] = out[1];
+        dst[dA + half] = out[2];
+        dst[dA + 1 + half] = out[3];
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_gemv_shape(const void* x, const uint8_t* w, const void* scales, int n, int k,
+                     int group_size) {
+    if (!x || !w || !scales || n <= 0 || k <= 0 || group_size <= 0) return AF_ERR_INVALID_ARG;
+    if (k % 16 || group_size % 16 || k % group_size) return AF_ERR_UNSUPPORTED;
+    if (!aligned16(x) || !aligned16(w)) return AF_ERR_INVALID_ARG;
+    return AF_OK;
+}
+
+// Chunks per pass: all of K in one pass for the usual widths.
+int chunks_per_pass(int k) {
+    if (k == 3 * kChunkBytes || k == 6 * kChunkBytes) return 3;
+    if (k > 4 * kChunkBytes && k <= 8 * kChunkBytes) return 8;
+    return 4;
+}
+
+template <int RPW>
+void launch_gemv(int nch, hipStream_t s, const uint8_t* w, const uint16_t* x, const uint16_t* sc,
+                 uint16_t* y, int n, int k, int group_size) {
+    const int grid = (n + kGemvWaves * RPW - 1) / (kGemvWaves * RPW);
+    if (nch == 3)
+        hipLaunchKernelGGL((w8a16_gemv_kernel<RPW, 3>), dim3(grid), dim3(kGemvThreads), 0, s, w, x,
+                           sc, y, n, k, group_size);
+    else if (nch == 8)
+        hipLaunchKernelGGL((w8a16_gemv_kernel<RPW, 8>), dim3(grid), dim3(kGemvThreads), 0, s, w, x,
+                           sc, y, n, k, group_size);
+    else
+        hipLaunchKernelGGL((w8a16_gemv_kernel<RPW, 4>), dim3(grid), dim3(kGemvThreads), 0, s, w, x,
+                           sc, y, n, k, group_size);
+}
+
+}  // namespace
+}  // namespace af
+
+using namespace af;
+
+extern "C" int af_w8a16_gemv(const void* x, const uint8_t* weight, const void* scales, void* y,
+                             int n, int k, int group_size, af_stream_t stream) {
+    if (int st = check_gemv_shape(x, weight, scales, n, k, group_size)) return st;
+    if (!y) return AF_ERR_INVALID_ARG;
+    // Rows per wave: the fewest whole rounds of one wave per SIMD with at most
+    // 5 rows per wave, then rows spread evenly over those rounds (2..5).
+    const int simds = 4 * device_compute_units();
+    const int rounds = std::max(1, (n + 5 * simds - 1) / (5 * simds));
+    const int rpw = std::min(5, std::max(2, (n + simds * rounds - 1) / (simds * rounds)));
+    const int nch = chunks_per_pass(k);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* xw = static_cast<const uint16_t*>(x);
+    const auto* sw = static_cast<const uint16_t*>(scales);
+    auto* yw = static_cast<uint16_t*>(y);
+    switch (rpw) {
+        case 2: launch_gemv<2>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
+        case 3: launch_gemv<3>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
+        case 4: launch_gemv<4>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
+        default: launch_gemv<5>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
+    }
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}
+
+extern "C" int af_qkv_rope_append(const void* x, const uint8_t* w_qkv, const void* scales, int k,
+                                  int group_size, void* qkv_out, void* k_cache, void* v_cache,
+                                  const float* cos_table, const float* sin_table, int pos,
+                                  const int32_t* d_pos, int max_seq, int n_q_heads,
+                                  int n_kv_heads, int head_dim, int32_t* d_status,
+                                  af_stream_t stream) {
+    if (n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0) return AF_ERR_INVALID_ARG;
+    const int n = (n_q_heads + 2 * n_kv_heads) * head_dim;
+    if (int st = check_gemv_shape(x, w_qkv, scales, n, k, group_size)) return st;
+    if (!qkv_out || !k_cache || !v_cache || !cos_table || !sin_table || max_seq <= 0)
+        return AF_ERR_INVALID_ARG;
+    if (head_dim % 4) return AF_ERR_UNSUPPORTED;  // two rotation pairs per wave, one head
+    if (!d_pos && (pos < 0 || pos >= max_seq)) return AF_ERR_OUT_OF_RANGE;
+    const int n_pairs = n / 2;
+    const int grid = (n_pairs + 2 * kQkvWaves - 1) / (2 * kQkvWaves);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* xw = static_cast<const uint16_t*>(x);
+    const auto* sw = static_cast<const uint16_t*>(scales);
+    auto* qw = static_cast<uint16_t*>(qkv_out);
+    auto* kc = static_cast<uint16_t*>(k_cache);
+    auto* vc = static_cast<uint16_t*>(v_cache);
+    const int nch = chunks_per_pass(k);
+    if (nch == 3)
+        hipLaunchKernelGGL(qkv_rope_append_kernel<3>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
+                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
+                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
+    else if (nch == 8)
+        hipLaunchKernelGGL(qkv_rope_append_kernel<8>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
+                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
+                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
+    else
+        hipLaunchKernelGGL(qkv_rope_append_kernel<4>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
+                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
+                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}

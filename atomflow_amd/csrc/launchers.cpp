@@ -58,6 +58,29 @@ void launch_rope_append(View& qkv_out, View& k_cache, View& v_cache, const float
           "launch_rope_append");
 }
 
+void launch_w8a16_gemv(const View& act_x, const View& weight, const View& scales, View& output,
+                       int group_size, hipStream_t stream) {
+    // Same shape reading as the reference launcher (qkv_gemm.cu:136-139).
+    const int n = int(weight.dims[0]);
+    const int k = int(weight.dims[1]);
+    check(af_w8a16_gemv(act_x.data_ptr, static_cast<const uint8_t*>(weight.data_ptr),
+                        scales.data_ptr, output.data_ptr, n, k, group_size, stream),
+          "launch_w8a16_gemv");
+}
+
+void launch_qkv_rope_append(const View& act_x, const View& w_qkv, const View& scales,
+                            int group_size, View& qkv_out, View& k_cache, View& v_cache,
+                            const float* cos_table, const float* sin_table, int pos,
+                            const int32_t* d_pos, int n_q_heads, int n_kv_heads, int head_dim,
+                            hipStream_t stream) {
+    const int max_seq = int(k_cache.dims[0] < v_cache.dims[0] ? k_cache.dims[0] : v_cache.dims[0]);
+    check(af_qkv_rope_append(act_x.data_ptr, static_cast<const uint8_t*>(w_qkv.data_ptr),
+                             scales.data_ptr, int(w_qkv.dims[1]), group_size, qkv_out.data_ptr,
+                             k_cache.data_ptr, v_cache.data_ptr, cos_table, sin_table, pos, d_pos,
+                             max_seq, n_q_heads, n_kv_heads, head_dim, nullptr, stream),
+          "launch_qkv_rope_append");
+}
+
 void launch_cached_attention_ws(const __half* q, const __half* k_cache, const __half* v_cache,
                                 __half* out, int seq_len, const int32_t* d_seq_len,
                                 int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,

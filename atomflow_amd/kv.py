@@ -54,6 +54,23 @@ def launch_rope_append(qkv_out, k_cache, v_cache, cos_table, sin_table, pos, max
                                head_dim, _p(d_status), _s(stream)), "launch_rope_append")
 
 
+# ---- W8A16 GEMV (qkv_gemm.cu launch_w8a16_gemv) and the fused QKV step -------
+def launch_w8a16_gemv(x, weight, scales, y, n, k, group_size=128, stream=None):
+    """y[n] = sum_k e4m3(weight[n,k]) * scales[n, k/group_size] * x[k] (fp16 out)."""
+    check(lib().af_w8a16_gemv(_p(x), _p(weight), _p(scales), _p(y), n, k, group_size, _s(stream)),
+          "launch_w8a16_gemv")
+
+
+def launch_qkv_rope_append(x, w_qkv, scales, k, qkv_out, k_cache, v_cache, cos_table, sin_table,
+                           pos, max_seq, n_q_heads, n_kv_heads, head_dim, group_size=128,
+                           d_pos=None, d_status=None, stream=None):
+    """QKV projection into qkv_out, RoPE of Q and K, K/V appended at row pos."""
+    check(lib().af_qkv_rope_append(_p(x), _p(w_qkv), _p(scales), k, group_size, _p(qkv_out),
+                                   _p(k_cache), _p(v_cache), _p(cos_table), _p(sin_table), pos,
+                                   _p(d_pos), max_seq, n_q_heads, n_kv_heads, head_dim,
+                                   _p(d_status), _s(stream)), "launch_qkv_rope_append")
+
+
 # ---- a5 ---------------------------------------------------------------------
 def launch_cached_attention(q, k_cache, v_cache, out, seq_len, head_dim, n_q_heads, n_kv_heads,
                             stream=None):
@@ -290,7 +307,8 @@ __all__ = [
     "AF_KV_FP16", "AF_KV_FP8_E4M3", "AttentionWorkspace", "BlockManager", "build_rope_cache",
     "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
-    "launch_paged_decode_fused", "launch_paged_rope_append",
+    "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
+    "launch_w8a16_gemv",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

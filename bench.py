@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 NQ, NKV, HD, LAYERS = 24, 8, 128, 28
 Q_DIM, KV_DIM = NQ * HD, NKV * HD
 QKV = Q_DIM + 2 * KV_DIM
+HIDDEN = 3072                              # model width: the QKV projection's input
 THETA = 500000.0
 HBM_PEAK_GBS = 8000.0
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx8k_pmc.txt")
@@ -135,6 +136,16 @@ def bench_contiguous(args, dev, kv, lib, info):
     atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, LAYERS * QKV, 11, 1.0, stream.handle))
     splits = args.splits or kv.default_splits(L, 1, NKV)
     ws = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
+    # The projection either side of the path: FP8 E4M3 QKV weights [QKV, HIDDEN]
+    # with fp16 per-128 group scales and an fp16 activation row, per layer.
+    w_qkv = dev.DeviceBuffer(LAYERS * QKV * HIDDEN)
+    s_qkv = dev.DeviceBuffer(LAYERS * QKV * (HIDDEN // 128) * 2)
+    x_act = dev.DeviceBuffer(LAYERS * HIDDEN * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_fp8(w_qkv.ptr, LAYERS * QKV * HIDDEN, 13, 20.0,
+                                                stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(s_qkv.ptr, LAYERS * QKV * (HIDDEN // 128), 17,
+                                                0.002, stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(x_act.ptr, LAYERS * HIDDEN, 19, 1.0, stream.handle))
     stream.sync()
 
     def ptrs(l):
@@ -160,19 +171,43 @@ def bench_contiguous(args, dev, kv, lib, info):
             kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws,
                                           num_splits=splits, stream=stream)
 
+    def qkv_args(l):
+        return (x_act.ptr + l * HIDDEN * 2, w_qkv.ptr + l * QKV * HIDDEN,
+                s_qkv.ptr + l * QKV * (HIDDEN // 128) * 2)
+
+    def step_with_projection():  # QKV GEMV + RoPE + append, then attention
+        for l in range(LAYERS):
+            q, k, v, o = ptrs(l)
+            x, w, sc = qkv_args(l)
+            kv.launch_qkv_rope_append(x, w, sc, HIDDEN, q, k, v, d_cos, d_sin, ctx, max_seq, NQ, NKV,
+                                      HD, stream=stream)
+            kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws,
+                                          num_splits=splits, stream=stream)
+
+    def projection_only():
+        for l in range(LAYERS):
+            q, k, v, _ = ptrs(l)
+            x, w, sc = qkv_args(l)
+            kv.launch_qkv_rope_append(x, w, sc, HIDDEN, q, k, v, d_cos, d_sin, ctx, max_seq, NQ, NKV,
+                                      HD, stream=stream)
+
     graphs = {name: dev.Graph.capture(stream, fn) for name, fn in
-              (("step", step), ("two", step_two_launch), ("attn", attention_only))}
+              (("step", step), ("two", step_two_launch), ("attn", attention_only),
+               ("proj_step", step_with_projection), ("proj", projection_only))}
     t = Timer(dev, stream, args.warmup)
     log(f"splits {splits}; warmup {args.warmup}, timing {args.steps} graph replays")
     ms_step = t.graph_ms(graphs["step"], args.steps)
     ms_two = t.graph_ms(graphs["two"], args.steps)
     ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
+    ms_proj_step = t.graph_ms(graphs["proj_step"], args.steps)
+    ms_proj = t.graph_ms(graphs["proj"], args.steps) / LAYERS
     log(f"step {ms_step * 1e3:.1f} us (two-launch {ms_two * 1e3:.1f} us), "
         f"attention {ms_attn * 1e3:.2f} us/launch")
     for g in graphs.values():
         g.destroy()
 
     kv_bytes = L * KV_DIM * 2 * 2          # K and V rows attended, each byte once
+    proj_bytes = QKV * HIDDEN + QKV * (HIDDEN // 128) * 2 + HIDDEN * 2 + QKV * 2
     step_gbs = LAYERS * kv_bytes / (ms_step * 1e-3) / 1e9
     attn_gbs = kv_bytes / (ms_attn * 1e-3) / 1e9
     result = {
@@ -190,7 +225,11 @@ def bench_contiguous(args, dev, kv, lib, info):
                    "device": info["name"], "arch": info["arch"], "cus": info["compute_units"]},
         "kernels": {"decode_attn_us": round(ms_attn * 1e3, 3),
                     "two_launch_us_per_layer_step": round(ms_two * 1e3 / LAYERS, 3),
-                    "attn_kv_bytes_per_launch": kv_bytes},
+                    "attn_kv_bytes_per_launch": kv_bytes,
+                    "qkv_rope_append_us": round(ms_proj * 1e3, 3),
+                    "qkv_weight_bytes_per_launch": proj_bytes,
+                    "qkv_rope_append_gbs": round(proj_bytes / (ms_proj * 1e-3) / 1e9, 1),
+                    "layer_step_with_qkv_projection_us": round(ms_proj_step * 1e3 / LAYERS, 3)},
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic() if ctx == 8192 else None},

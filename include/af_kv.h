@@ -213,6 +213,31 @@ int af_kv_copy_blocks(const af_kv_pool* pool, const int32_t* d_copies, const int
 int af_fp8_quantize(const void* src_f16, uint8_t* dst, size_t n, float scale, af_stream_t stream);
 
 /* ======================================================================== */
+/* b1. W8A16 GEMV either side of the path (QKV projection, output proj.)   */
+/* ======================================================================== */
+/* Replaces launch_w8a16_gemv (include/ops/kernel.h:138-145,
+ * src/kernel/qkv_gemm.cu:32-152): y[n] = sum_k e4m3(weight[n,k]) *
+ * scales[n, k/group_size] * x[k], fp32 accumulation, fp16 output.
+ * x: [k] fp16, weight: [n, k] E4M3 codes row-major, scales: [n, k/group_size]
+ * fp16, y: [n] fp16. k and group_size multiples of 16 (the engine uses 128);
+ * x and weight 16-byte aligned. */
+int af_w8a16_gemv(const void* x, const uint8_t* weight, const void* scales, void* y, int n, int k,
+                  int group_size, af_stream_t stream);
+
+/* Decode QKV projection, RoPE and KV append in one launch: af_w8a16_gemv of the
+ * fused QKV weight into qkv_out ([Q | K | V] heads, the engine's layout,
+ * src/core/engine.cu:310-331) followed by af_rope_append(pos) — the same
+ * outputs bit for bit (src/core/engine.cu:315-355 issues the three launches).
+ * Position: *d_pos when d_pos != NULL, else pos; a device position >= max_seq
+ * writes nothing and stores AF_ERR_OUT_OF_RANGE into *d_status (if given).
+ * head_dim a multiple of 16. */
+int af_qkv_rope_append(const void* x, const uint8_t* w_qkv, const void* scales, int k,
+                       int group_size, void* qkv_out, void* k_cache, void* v_cache,
+                       const float* cos_table, const float* sin_table, int pos,
+                       const int32_t* d_pos, int max_seq, int n_q_heads, int n_kv_heads,
+                       int head_dim, int32_t* d_status, af_stream_t stream);
+
+/* ======================================================================== */
 /* a6. BlockManager (host bookkeeping, optional device pool)                */
 /* ======================================================================== */
 /* Contract of atomflow::server::BlockManager

@@ -34,7 +34,20 @@ void launch_write_kv_cache(const View& qkv_out, View& k_cache, View& v_cache, in
 void build_rope_cache(float* d_cos, float* d_sin, int max_seq, int head_dim, float base,
                       hipStream_t stream);
 
+// W8A16 GEMV (kernel.h:138-145 of the reference): FP16 act_x [1, K], FP8
+// weight [N, K], FP16 scales [N, K/GS], FP16 output [1, N].
+void launch_w8a16_gemv(const View& act_x, const View& weight, const View& scales, View& output,
+                       int group_size, hipStream_t stream);
+
 // ---- added by this build ---------------------------------------------------
+// Decode QKV projection + RoPE + KV append (launch_w8a16_gemv, launch_rope and
+// launch_write_kv_cache at position pos in one kernel; d_pos overrides pos).
+void launch_qkv_rope_append(const View& act_x, const View& w_qkv, const View& scales,
+                            int group_size, View& qkv_out, View& k_cache, View& v_cache,
+                            const float* cos_table, const float* sin_table, int pos,
+                            const int32_t* d_pos, int n_q_heads, int n_kv_heads, int head_dim,
+                            hipStream_t stream);
+
 // launch_rope(pos) + launch_write_kv_cache(pos) in one kernel. d_pos (device,
 // nullable) overrides pos so a captured graph can advance the position.
 void launch_rope_append(View& qkv_out, View& k_cache, View& v_cache, const float* cos_table,

@@ -55,6 +55,8 @@ def lib():
             "ok_paged_attention_fp8": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I]),
             "ok_paged_write_f16": (None, [_P, _P, _P, _P, _I64, _I]),
             "ok_paged_write_fp8": (None, [_P, _P, _P, _P, _I64, _I, _I, _P, _P]),
+            "ok_w8a16_gemv": (None, [_P, _P, _P, _P, _I, _I, _I]),
+            "ok_w8a16_gemv_f64": (None, [_P, _P, _P, _P, _I, _I, _I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -220,3 +222,28 @@ def paged_write_fp8(k_row, v_row, k_slab, v_slab, slot, kv_dim, head_dim, k_scal
     vs = _c(v_scales, np.float32)
     lib().ok_paged_write_fp8(_ptr(k_row), _ptr(v_row), _ptr(k_slab), _ptr(v_slab), slot, kv_dim,
                              head_dim, _ptr(ks), _ptr(vs))
+
+
+def w8a16_gemv(w, x, scales, group_size=128):
+    """y[n] = sum_k e4m3(w[n,k]) * scales[n, k/group_size] * x[k] in the reference
+    kernel's fp32 summation order, rounded to fp16 (qkv_gemm.cu:32-110).
+    w: uint8 [n, k] E4M3 codes, x: float16 [k], scales: float16 [n, k/group_size]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    scales = np.ascontiguousarray(scales, dtype=np.float16)
+    n, k = w.shape
+    assert x.shape == (k,) and scales.shape == (n, k // group_size)
+    y = np.empty(n, dtype=np.float16)
+    lib().ok_w8a16_gemv(w.ctypes.data, x.ctypes.data, scales.ctypes.data, y.ctypes.data, n, k, group_size)
+    return y
+
+
+def w8a16_gemv_f64(w, x, scales, group_size=128):
+    """The same products summed in float64 (an order-free reference)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    scales = np.ascontiguousarray(scales, dtype=np.float16)
+    n, k = w.shape
+    y = np.empty(n, dtype=np.float64)
+    lib().ok_w8a16_gemv_f64(w.ctypes.data, x.ctypes.data, scales.ctypes.data, y.ctypes.data, n, k, group_size)
+    return y

@@ -375,3 +375,62 @@ void ok_paged_write_fp8(const uint16_t* k_row, const uint16_t* v_row, uint8_t* k
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// W8A16 GEMV (src/kernel/qkv_gemm.cu:32-110, launched with BLOCK_DIM = 256,
+// one block per output row, qkv_gemm.cu:136-151).
+// Thread t of 256 accumulates elements k = 4t + 1024 j + v (v < 4), each term
+// as (w * s) * x added with one rounding (nvcc contracts the multiply-add into
+// an FMA by default): qkv_gemm.cu:63-90. Then each 32-thread warp reduces with
+// shuffle-down offsets 16, 8, 4, 2, 1 (qkv_gemm.cu:94-96) and thread 0 adds the
+// 8 warp sums in order (qkv_gemm.cu:104-109). The reference indexes scales by
+// k / 128 whatever group_size says (qkv_gemm.cu:74); this restatement uses
+// k / group_size, which is the same for the 128 every caller passes.
+// ---------------------------------------------------------------------------
+void ok_w8a16_gemv(const uint8_t* w, const uint16_t* x, const uint16_t* scales, uint16_t* y,
+                   int n, int k, int group_size) {
+    float lut[256];
+    for (int c = 0; c < 256; ++c) lut[c] = ok_e4m3_decode(uint8_t(c));
+    const int groups = k / group_size;
+    std::vector<float> xf(k);
+    for (int i = 0; i < k; ++i) xf[i] = ok_f16_to_f32(x[i]);
+    float sum[256];
+    for (int row = 0; row < n; ++row) {
+        const uint8_t* wr = w + size_t(row) * k;
+        const uint16_t* sr = scales + size_t(row) * groups;
+        for (int t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int kv = 4 * t; kv < k; kv += 1024) {
+                const float s = ok_f16_to_f32(sr[kv / group_size]);
+                for (int v = 0; v < 4; ++v) {
+                    const float ws = lut[wr[kv + v]] * s;
+                    acc = std::fma(ws, xf[kv + v], acc);
+                }
+            }
+            sum[t] = acc;
+        }
+        float warp[8];
+        for (int wi = 0; wi < 8; ++wi) {
+            float* l = sum + 32 * wi;
+            for (int off = 16; off > 0; off >>= 1)
+                for (int i = 0; i < off; ++i) l[i] = l[i] + l[i + off];
+            warp[wi] = l[0];
+        }
+        float total = 0.0f;
+        for (int wi = 0; wi < 8; ++wi) total = total + warp[wi];
+        y[row] = ok_f32_to_f16(total);
+    }
+}
+
+void ok_w8a16_gemv_f64(const uint8_t* w, const uint16_t* x, const uint16_t* scales, double* y,
+                       int n, int k, int group_size) {
+    const int groups = k / group_size;
+    for (int row = 0; row < n; ++row) {
+        double acc = 0.0;
+        for (int i = 0; i < k; ++i)
+            acc += double(ok_e4m3_decode(w[size_t(row) * k + i])) *
+                   double(ok_f16_to_f32(scales[size_t(row) * groups + i / group_size])) *
+                   double(ok_f16_to_f32(x[i]));
+        y[row] = acc;
+    }
+}

@@ -18,6 +18,8 @@
  *                                  key, permutation invariance, torch SDPA (fp64)
  *   ok_e4m3_encode / decode        exhaustive vs torch.float8_e4m3fn
  *   ok_paged_gather                contiguous identity table, permuted tables
+ *   ok_w8a16_gemv                  identity weights -> x, power-of-two group
+ *                                  scales (exact sums), float64 matmul bound
  * The reference ships no golden vectors for this path (its ground_truth *.bin files
  * are full-model activations at seq_len 1).
  */
@@ -91,6 +93,16 @@ void ok_paged_write_f16(const uint16_t* k_row, const uint16_t* v_row, uint16_t* 
 void ok_paged_write_fp8(const uint16_t* k_row, const uint16_t* v_row, uint8_t* k_slab,
                         uint8_t* v_slab, int64_t slot, int kv_dim, int head_dim,
                         const float* k_scales, const float* v_scales);
+
+/* W8A16 GEMV: y[n] = sum_k e4m3(w[n,k]) * scale[n, k/group_size] * x[k], fp32,
+ * rounded to fp16 (src/kernel/qkv_gemm.cu:32-110), in the reference kernel's
+ * summation order. w: [n, k] E4M3 codes, x: [k] fp16, scales: [n, k/group_size]
+ * fp16, y: [n] fp16. */
+void ok_w8a16_gemv(const uint8_t* w, const uint16_t* x, const uint16_t* scales, uint16_t* y,
+                   int n, int k, int group_size);
+/* Same products summed in double (order-free reference for tolerances). */
+void ok_w8a16_gemv_f64(const uint8_t* w, const uint16_t* x, const uint16_t* scales, double* y,
+                       int n, int k, int group_size);
 
 #ifdef __cplusplus
 }

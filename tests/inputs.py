@@ -46,3 +46,62 @@ def assert_attn_close(got, ref, atol=ATOL_F16, rtol=RTOL_F16, what=""):
     assert not bad.any(), (f"{what}: {bad.sum()} elements outside atol={atol} rtol={rtol}; "
                            f"max abs err {err.max():.3e} at {int(err.argmax())}")
     return float(err.max())
+
+
+# ---- W8A16 GEMV inputs (FP8 E4M3 weights with fp16 group scales) ------------
+_E4M3_POS = None
+
+
+def _e4m3_positive_values():
+    """Finite positive E4M3FN values, indexed by code 0..126 (0x7F is NaN)."""
+    global _E4M3_POS
+    if _E4M3_POS is None:
+        vals = []
+        for c in range(127):
+            e, m = c >> 3, c & 7
+            vals.append(m * 2.0 ** -9 if e == 0 else (8 + m) * 2.0 ** (e - 10))
+        _E4M3_POS = np.array(vals, np.float64)
+    return _E4M3_POS
+
+
+def e4m3_encode_np(x):
+    """Round-to-nearest-even E4M3FN codes of float values already within +-448."""
+    vals = _e4m3_positive_values()
+    a = np.abs(np.asarray(x, np.float64))
+    hi = np.clip(np.searchsorted(vals, a), 1, 126)
+    lo = hi - 1
+    d_lo, d_hi = a - vals[lo], vals[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    return code | np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
+
+
+def gemv_case(n, k, seed, group=128, wscale=0.05):
+    """Weights ~ N(0, wscale) quantised per (row, group) with scale = absmax / 448
+    (1 for an all-zero group) in fp16 and RNE E4M3 codes (the convention of
+    tools/quantize_weights.py:249-260); activation ~ N(0, 1) fp16."""
+    r = rng(seed)
+    wf = r.standard_normal((n, k)) * wscale
+    g = wf.reshape(n, k // group, group)
+    absmax = np.abs(g).max(axis=2)
+    scales = np.where(absmax > 0, absmax / 448.0, 1.0).astype(np.float16)
+    q = np.clip(g / scales.astype(np.float64)[..., None], -448.0, 448.0)
+    codes = e4m3_encode_np(q).reshape(n, k)
+    x = r.standard_normal(k).astype(np.float16)
+    return codes, x, scales
+
+
+def gemv_abs_terms(codes, x, scales, group=128):
+    """sum_k |e4m3(w) * s * x| per row (float64), the scale of fp32 summation error."""
+    vals = np.concatenate([_e4m3_positive_values(), [np.nan]])
+    mag = vals[codes & 0x7f]
+    n, k = codes.shape
+    s = np.repeat(np.abs(scales.astype(np.float64)), group, axis=1)
+    return (mag * s * np.abs(x.astype(np.float64))[None, :]).sum(axis=1)
+
+
+def fp16_ulp(v):
+    """Spacing of fp16 values at |v| (2^-24 below the normal range)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)

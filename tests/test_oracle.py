@@ -315,3 +315,47 @@ def test_fixture_files_are_small():
         assert os.path.getsize(os.path.join(GOLDEN, f)) < 512 * 1024, f
     h = hashlib.sha256(open(os.path.join(GOLDEN, "sdpa_cases.npz"), "rb").read()).hexdigest()
     assert len(h) == 64
+
+
+# ---- W8A16 GEMV (qkv_gemm.cu:32-110) ----------------------------------------
+def test_gemv_identity_weights_return_x():
+    """W = I (code 0x38 = 1.0), scales 1: each row has one nonzero product."""
+    from inputs import rng
+    n = k = 256
+    w = np.zeros((n, k), np.uint8)
+    w[np.arange(n), np.arange(n)] = 0x38
+    x = randn_f16(k, 41)
+    s = np.ones((n, k // 128), np.float16)
+    assert np.array_equal(oracle.w8a16_gemv(w, x, s).view(np.uint16), x.view(np.uint16))
+    # a row permutation of W permutes y: pins the row/column indexing
+    perm = rng(42).permutation(n)
+    y = oracle.w8a16_gemv(w[perm], x, s)
+    assert np.array_equal(y.view(np.uint16), x[perm].view(np.uint16))
+
+
+def test_gemv_group_scales_exact():
+    """All-ones weights and activation: y[n] = 128 * sum_g s[n, g], exact with
+    power-of-two scales; a scale applied to the wrong group or row shows."""
+    n, k = 8, 1024
+    w = np.full((n, k), 0x38, np.uint8)
+    x = np.ones(k, np.float16)
+    s = np.array([[2.0 ** -((r + 3 * g) % 7) for g in range(k // 128)] for r in range(n)],
+                 np.float16)
+    y = oracle.w8a16_gemv(w, x, s).astype(np.float64)
+    assert np.array_equal(y, 128.0 * s.astype(np.float64).sum(axis=1))
+
+
+@pytest.mark.parametrize("n,k", [(64, 3072), (32, 8192), (5, 1024)])
+def test_gemv_random_vs_float64(n, k):
+    from inputs import fp16_ulp, gemv_abs_terms, gemv_case
+    w, x, s = gemv_case(n, k, 43 + n)
+    y = oracle.w8a16_gemv(w, x, s).astype(np.float64)
+    y64 = oracle.w8a16_gemv_f64(w, x, s)
+    # fp32 summation of K terms + one fp16 rounding
+    tol = 0.5 * fp16_ulp(y64) + k * 2.0 ** -24 * gemv_abs_terms(w, x, s)
+    assert np.all(np.abs(y - y64) <= tol)
+    # and an independent numpy dequantise-and-multiply agrees to the same bound
+    from inputs import _e4m3_positive_values
+    vals = np.concatenate([_e4m3_positive_values(), [np.nan]])
+    wf = vals[w & 0x7f] * np.where(w & 0x80, -1.0, 1.0) * np.repeat(s.astype(np.float64), 128, axis=1)
+    assert np.allclose(wf @ x.astype(np.float64), y64, rtol=1e-12, atol=1e-12)
