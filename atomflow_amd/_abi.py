@@ -56,6 +56,9 @@ PROTOTYPES = {
     "af_fp8_quantize": (I, [P, P, SZ, F, P]),
     "af_w8a16_gemv": (I, [P, P, P, P, I, I, I, P]),
     "af_qkv_rope_append": (I, [P, P, P, I, I, P, P, P, P, P, I, P, I, I, I, I, P, P]),
+    "af_prefill_rope_append": (I, [P, I, P, P, P, P, I, P, I, I, I, I, P, P]),
+    "af_prefill_attention": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, P]),
+    "af_tiled_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
     "af_bm_create": (I, [I, I, I, I, I, I, I, ctypes.POINTER(P)]),
     "af_bm_destroy": (I, [P]),
     "af_bm_attach_pool": (I, [P, P, P]),

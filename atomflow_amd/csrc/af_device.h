@@ -40,6 +40,9 @@ __device__ __forceinline__ uint32_t quantize_fp8(uint16_t h, float scale) {
     return e4m3_encode(v);
 }
 
+// 2^x on v_exp_f32 (1 ulp; flushes below 2^-126, 2^-inf = 0).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ---- cross-lane reductions (wave64) -----------------------------------------
 // DPP move of v (row_mask, bank_mask all lanes; no bound_ctrl).
 template <int CTRL>

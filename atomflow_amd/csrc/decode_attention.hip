@@ -72,8 +72,6 @@ __device__ __forceinline__ float wave_max_of_groups(float v) {
 // Sum over the 8 token groups of the lanes that share lane & 7.
 __device__ __forceinline__ float groups_sum(float v) { return rows_sum(v + dpp<0x128>(v)); }
 
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 __device__ __forceinline__ int ceil_div_d(int a, int b) { return (a + b - 1) / b; }
 
 // Agent-scope (all XCDs) relaxed atomic store / load of split-K partials.

@@ -81,6 +81,39 @@ void launch_qkv_rope_append(const View& act_x, const View& w_qkv, const View& sc
           "launch_qkv_rope_append");
 }
 
+template <typename T>
+void launch_tiled_attention_kernel(const T* q_base, const T* k_base, const T* v_base, T* out,
+                                   int seq_q, int seq_kv, int head_dim, int n_q_heads,
+                                   int n_kv_heads, hipStream_t stream) {
+    static_assert(sizeof(T) == 2, "fp16 only, as the reference instantiates it");
+    check(af_tiled_attention(q_base, k_base, v_base, out, seq_q, seq_kv, head_dim, n_q_heads,
+                             n_kv_heads, stream),
+          "launch_tiled_attention_kernel");
+}
+template void launch_tiled_attention_kernel<__half>(const __half*, const __half*, const __half*,
+                                                    __half*, int, int, int, int, int,
+                                                    hipStream_t);
+
+void launch_prefill_rope_append(View& qkv_out, int n, View& k_cache, View& v_cache,
+                                const float* cos_table, const float* sin_table, int p0,
+                                int n_q_heads, int n_kv_heads, int head_dim, hipStream_t stream) {
+    const int max_seq = int(k_cache.dims[0] < v_cache.dims[0] ? k_cache.dims[0] : v_cache.dims[0]);
+    check(af_prefill_rope_append(qkv_out.data_ptr, n, k_cache.data_ptr, v_cache.data_ptr,
+                                 cos_table, sin_table, p0, nullptr, max_seq, n_q_heads, n_kv_heads,
+                                 head_dim, nullptr, stream),
+          "launch_prefill_rope_append");
+}
+
+void launch_prefill_attention(const __half* q, int q_stride, const View& k_cache,
+                              const View& v_cache, __half* out, int out_stride, int p0, int n,
+                              int kv_len, int n_q_heads, int n_kv_heads, int head_dim,
+                              hipStream_t stream) {
+    const int max_seq = int(k_cache.dims[0] < v_cache.dims[0] ? k_cache.dims[0] : v_cache.dims[0]);
+    check(af_prefill_attention(q, q_stride, k_cache.data_ptr, v_cache.data_ptr, out, out_stride,
+                               p0, n, kv_len, max_seq, n_q_heads, n_kv_heads, head_dim, stream),
+          "launch_prefill_attention");
+}
+
 void launch_cached_attention_ws(const __half* q, const __half* k_cache, const __half* v_cache,
                                 __half* out, int seq_len, const int32_t* d_seq_len,
                                 int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,

@@ -105,6 +105,8 @@ struct RopeAppendArgs {
     int32_t max_pos;        // rows in the RoPE table
     const int32_t* d_pos;   // [batch] positions, or NULL -> pos_host
     int32_t pos_host;
+    int32_t d_pos_shared;   // 1: every row reads d_pos[0]
+    int32_t pos_inc;        // row b adds b * pos_inc (1 for the rows of a prompt chunk)
     const int64_t* d_slots; // [batch] destination rows, or NULL -> row = position
     int64_t max_rows;       // rows in the destination
     uint8_t* k_dst;         // destination bases (fp16 or fp8 elements)
@@ -120,7 +122,7 @@ struct RopeAppendArgs {
 template <bool FP8>
 __global__ __launch_bounds__(256) void rope_append_kernel(const RopeAppendArgs a) {
     const int b = blockIdx.x;
-    const int pos = a.d_pos ? a.d_pos[b] : a.pos_host;
+    const int pos = (a.d_pos ? a.d_pos[a.d_pos_shared ? 0 : b] : a.pos_host) + a.pos_inc * b;
     const int64_t row = a.d_slots ? a.d_slots[b] : int64_t(pos);
     if (pos < 0 || pos >= a.max_pos || row < 0 || row >= a.max_rows) {
         if (threadIdx.x == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
@@ -301,6 +303,44 @@ extern "C" int af_rope_append(void* qkv_out, void* k_cache, void* v_cache, const
     a.head_dim = head_dim;
     a.d_status = d_status;
     hipLaunchKernelGGL(rope_append_kernel<false>, dim3(1), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}
+
+// ---- b2: multi-token append ----------------------------------------------------
+extern "C" int af_prefill_rope_append(void* qkv_out, int n, void* k_cache, void* v_cache,
+                                      const float* cos_table, const float* sin_table, int p0,
+                                      const int32_t* d_p0, int max_seq, int n_q_heads,
+                                      int n_kv_heads, int head_dim, int32_t* d_status,
+                                      af_stream_t stream) {
+    if (!qkv_out || !k_cache || !v_cache || !cos_table || !sin_table || n < 0 || max_seq <= 0 ||
+        n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 8)
+        return AF_ERR_INVALID_ARG;
+    if (!aligned16(qkv_out) || !aligned16(k_cache) || !aligned16(v_cache) ||
+        !aligned16(cos_table) || !aligned16(sin_table))
+        return AF_ERR_INVALID_ARG;
+    if (!d_p0 && (p0 < 0 || int64_t(p0) + n > max_seq)) return AF_ERR_OUT_OF_RANGE;
+    if (n == 0) return AF_OK;
+    RopeAppendArgs a{};
+    a.qkv = static_cast<uint16_t*>(qkv_out);
+    a.qkv_stride = int64_t(n_q_heads + 2 * n_kv_heads) * head_dim;
+    a.cos_t = cos_table;
+    a.sin_t = sin_table;
+    a.max_pos = max_seq;
+    a.d_pos = d_p0;
+    a.pos_host = p0;
+    a.d_pos_shared = 1;
+    a.pos_inc = 1;
+    a.d_slots = nullptr;
+    a.max_rows = max_seq;
+    a.k_dst = static_cast<uint8_t*>(k_cache);
+    a.v_dst = static_cast<uint8_t*>(v_cache);
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.d_status = d_status;
+    hipLaunchKernelGGL(rope_append_kernel<false>, dim3(n), dim3(256), 0,
                        static_cast<hipStream_t>(stream), a);
     AF_TRY_LAUNCH();
     return AF_OK;

@@ -71,6 +71,33 @@ def launch_qkv_rope_append(x, w_qkv, scales, k, qkv_out, k_cache, v_cache, cos_t
                                    _p(d_status), _s(stream)), "launch_qkv_rope_append")
 
 
+# ---- prefill (multi-token append, causal attention over a prompt chunk) -----
+def launch_prefill_rope_append(qkv_out, n, k_cache, v_cache, cos_table, sin_table, p0, max_seq,
+                               n_q_heads, n_kv_heads, head_dim, d_p0=None, d_status=None,
+                               stream=None):
+    """RoPE of n qkv rows at positions p0.. and their K/V written to cache rows p0.."""
+    check(lib().af_prefill_rope_append(_p(qkv_out), n, _p(k_cache), _p(v_cache), _p(cos_table),
+                                       _p(sin_table), p0, _p(d_p0), max_seq, n_q_heads,
+                                       n_kv_heads, head_dim, _p(d_status), _s(stream)),
+          "launch_prefill_rope_append")
+
+
+def launch_prefill_attention(q, q_stride, k_cache, v_cache, out, out_stride, p0, n, kv_len,
+                             max_seq, n_q_heads, n_kv_heads, head_dim, stream=None):
+    """Causal attention: query i attends cache rows [0, min(p0 + i + 1, kv_len))."""
+    check(lib().af_prefill_attention(_p(q), q_stride, _p(k_cache), _p(v_cache), _p(out),
+                                     out_stride, p0, n, kv_len, max_seq, n_q_heads, n_kv_heads,
+                                     head_dim, _s(stream)), "launch_prefill_attention")
+
+
+def launch_tiled_attention_kernel(q, k, v, out, seq_q, seq_kv, head_dim, n_q_heads, n_kv_heads,
+                                  stream=None):
+    """tiled_attention.cu launch_tiled_attention_kernel<half>: query i attends keys s <= i."""
+    check(lib().af_tiled_attention(_p(q), _p(k), _p(v), _p(out), seq_q, seq_kv, head_dim,
+                                   n_q_heads, n_kv_heads, _s(stream)),
+          "launch_tiled_attention_kernel")
+
+
 # ---- a5 ---------------------------------------------------------------------
 def launch_cached_attention(q, k_cache, v_cache, out, seq_len, head_dim, n_q_heads, n_kv_heads,
                             stream=None):
@@ -308,7 +335,8 @@ __all__ = [
     "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
     "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
-    "launch_w8a16_gemv",
+    "launch_w8a16_gemv", "launch_prefill_rope_append", "launch_prefill_attention",
+    "launch_tiled_attention_kernel",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

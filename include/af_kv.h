@@ -238,6 +238,45 @@ int af_qkv_rope_append(const void* x, const uint8_t* w_qkv, const void* scales, 
                        int head_dim, int32_t* d_status, af_stream_t stream);
 
 /* ======================================================================== */
+/* b2. Prefill: multi-token append and causal attention over a prompt chunk */
+/* ======================================================================== */
+/* Multi-token form of af_rope_append: n rows of qkv_out ([n, (n_q_heads +
+ * 2*n_kv_heads)*head_dim], the QKV projection of n prompt tokens) get RoPE with
+ * table rows p0 .. p0+n-1 (rope.cu:22-45 with seq_len = n, rope.cu:59-60) and
+ * their K/V rows are written to cache rows p0 .. p0+n-1 (helpers.cu:126-139 per
+ * token). Start position: *d_p0 when d_p0 != NULL, else p0. With a host p0 the
+ * whole chunk must fit (p0 + n <= max_seq, else AF_ERR_OUT_OF_RANGE and nothing
+ * is launched); with a device p0 each row past max_seq is skipped and
+ * AF_ERR_OUT_OF_RANGE is stored into *d_status (if given). */
+int af_prefill_rope_append(void* qkv_out, int n, void* k_cache, void* v_cache,
+                           const float* cos_table, const float* sin_table, int p0,
+                           const int32_t* d_p0, int max_seq, int n_q_heads, int n_kv_heads,
+                           int head_dim, int32_t* d_status, af_stream_t stream);
+
+/* Causal GQA attention of a chunk of n query tokens at cache positions
+ * p0 .. p0+n-1 over the contiguous cache: query i attends cache rows
+ * [0, min(p0 + i + 1, kv_len)). Generalises gqa_attention_kernel
+ * (src/kernel/tiled_attention.cu:34-130), whose form is p0 = 0, kv_len = seq_kv.
+ * q: row i at q + i*q_stride (elements), head h at +h*head_dim (the roped Q of
+ * af_prefill_rope_append's qkv_out has q_stride = (n_q_heads+2*n_kv_heads)*head_dim);
+ * k_cache/v_cache: [max_seq, n_kv_heads*head_dim]; out: row i at
+ * out + i*out_stride. head_dim 128 (else AF_ERR_UNSUPPORTED); 1 <= kv_len <= max_seq.
+ * fp16 in and out; scores and softmax in fp32, probabilities rounded to fp16 for
+ * the P.V product, fp32 accumulation. */
+int af_prefill_attention(const void* q, int q_stride, const void* k_cache, const void* v_cache,
+                         void* out, int out_stride, int p0, int n, int kv_len, int max_seq,
+                         int n_q_heads, int n_kv_heads, int head_dim, af_stream_t stream);
+
+/* launch_tiled_attention_kernel<half> (include/ops/kernel.h:73-85,
+ * src/kernel/tiled_attention.cu:136-161): q [seq_q, n_q_heads*head_dim],
+ * k/v [seq_kv, n_kv_heads*head_dim], out [seq_q, n_q_heads*head_dim]; query i
+ * attends keys s <= i, s < seq_kv. seq_kv = 0 writes zeros, as the reference's
+ * empty accumulation does. */
+int af_tiled_attention(const void* q, const void* k, const void* v, void* out, int seq_q,
+                       int seq_kv, int head_dim, int n_q_heads, int n_kv_heads,
+                       af_stream_t stream);
+
+/* ======================================================================== */
 /* a6. BlockManager (host bookkeeping, optional device pool)                */
 /* ======================================================================== */
 /* Contract of atomflow::server::BlockManager

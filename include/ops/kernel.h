@@ -39,7 +39,29 @@ void build_rope_cache(float* d_cos, float* d_sin, int max_seq, int head_dim, flo
 void launch_w8a16_gemv(const View& act_x, const View& weight, const View& scales, View& output,
                        int group_size, hipStream_t stream);
 
+// Legacy causal GQA attention (kernel.h:73-85 of the reference, tiled_attention.cu:
+// 136-161): q [seq_q, n_q_heads*head_dim], k/v [seq_kv, n_kv_heads*head_dim];
+// query i attends keys s <= i, s < seq_kv. Instantiated for __half.
+template <typename T>
+void launch_tiled_attention_kernel(const T* q_base, const T* k_base, const T* v_base, T* out,
+                                   int seq_q, int seq_kv, int head_dim, int n_q_heads,
+                                   int n_kv_heads, hipStream_t stream);
+
 // ---- added by this build ---------------------------------------------------
+// Prefill of a prompt chunk: RoPE of qkv_out's n rows at positions p0.. and their
+// K/V written to cache rows p0.. (launch_rope with seq_len = n, then
+// launch_write_kv_cache per token).
+void launch_prefill_rope_append(View& qkv_out, int n, View& k_cache, View& v_cache,
+                                const float* cos_table, const float* sin_table, int p0,
+                                int n_q_heads, int n_kv_heads, int head_dim, hipStream_t stream);
+
+// Causal attention of the chunk's n queries (row stride q_stride) over cache rows
+// [0, min(p0 + i + 1, kv_len)) into out (row stride out_stride). head_dim 128.
+void launch_prefill_attention(const __half* q, int q_stride, const View& k_cache,
+                              const View& v_cache, __half* out, int out_stride, int p0, int n,
+                              int kv_len, int n_q_heads, int n_kv_heads, int head_dim,
+                              hipStream_t stream);
+
 // Decode QKV projection + RoPE + KV append (launch_w8a16_gemv, launch_rope and
 // launch_write_kv_cache at position pos in one kernel; d_pos overrides pos).
 void launch_qkv_rope_append(const View& act_x, const View& w_qkv, const View& scales,

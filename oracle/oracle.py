@@ -57,6 +57,9 @@ def lib():
             "ok_paged_write_fp8": (None, [_P, _P, _P, _P, _I64, _I, _I, _P, _P]),
             "ok_w8a16_gemv": (None, [_P, _P, _P, _P, _I, _I, _I]),
             "ok_w8a16_gemv_f64": (None, [_P, _P, _P, _P, _I, _I, _I]),
+            "ok_prefill_attention": (None, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I]),
+            "ok_prefill_attention_f64": (None, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+            "ok_prefill_rope_append": (None, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -151,6 +154,42 @@ def cached_attention_f64(q, k_cache, v_cache, seq_len, n_q_heads, n_kv_heads, he
     lib().ok_cached_attention_f64(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), seq_len,
                                   head_dim, n_q_heads, n_kv_heads)
     return out
+
+
+# ---- b2: prefill -------------------------------------------------------------
+def prefill_attention(q, k_cache, v_cache, p0, n, kv_len, n_q_heads, n_kv_heads, head_dim,
+                      threads=1):
+    """q: [n, q_stride] fp16 (Q heads in the first n_q_heads*head_dim columns)."""
+    q = _c(q, np.float16)
+    k_cache = _c(k_cache, np.float16)
+    v_cache = _c(v_cache, np.float16)
+    q_dim = n_q_heads * head_dim
+    out = np.empty((n, q_dim), np.float16)
+    lib().ok_prefill_attention(_ptr(q), q.shape[-1], _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                               q_dim, p0, n, kv_len, head_dim, n_q_heads, n_kv_heads, threads)
+    return out
+
+
+def prefill_attention_f64(q, k_cache, v_cache, p0, n, kv_len, n_q_heads, n_kv_heads, head_dim):
+    q = _c(q, np.float16)
+    k_cache = _c(k_cache, np.float16)
+    v_cache = _c(v_cache, np.float16)
+    out = np.empty((n, n_q_heads * head_dim), np.float64)
+    lib().ok_prefill_attention_f64(_ptr(q), q.shape[-1], _ptr(k_cache), _ptr(v_cache),
+                                   _ptr(out), p0, n, kv_len, head_dim, n_q_heads, n_kv_heads)
+    return out
+
+
+def prefill_rope_append(qkv, k_cache, v_cache, cos, sin, p0, n_q_heads, n_kv_heads, head_dim):
+    """Returns the rotated qkv rows; k_cache / v_cache (C-contiguous fp16) are updated."""
+    qkv = np.array(qkv, np.float16, order="C", copy=True)
+    assert k_cache.dtype == np.float16 and k_cache.flags.c_contiguous
+    assert v_cache.dtype == np.float16 and v_cache.flags.c_contiguous
+    cos = _c(cos, np.float32)
+    sin = _c(sin, np.float32)
+    lib().ok_prefill_rope_append(_ptr(qkv), qkv.shape[0], _ptr(k_cache), _ptr(v_cache),
+                                 _ptr(cos), _ptr(sin), p0, n_q_heads, n_kv_heads, head_dim)
+    return qkv
 
 
 # ---- a8 -------------------------------------------------------------------

@@ -8,6 +8,7 @@
 // products and one fp32 subtraction, each rounded, then one fp32->fp16 RNE.
 #include "oracle_kv.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <thread>
@@ -264,6 +265,119 @@ void ok_cached_attention_f64(const uint16_t* q, const uint16_t* k_cache,
             out[size_t(h) * head_dim + d] = acc / l;
         }
     }
+}
+
+// ---- b2: causal prefill attention — src/kernel/tiled_attention.cu:34-130 -------
+// Per (query token i, head h), one block of head_dim threads in the reference:
+//   kv_h = h*n_kv_heads/n_q_heads                                  (:55)
+//   score[s] = serial_sum_d(q[d]*k[s,d]) * (1/sqrt(head_dim))     (:82-96)
+//   for s < n_keys = min(i+1, seq_kv)                              (:82,:103)
+//   max (from -1e38), p = exp(score - max), serial sum, p /= sum   (:101-116)
+//   out[d] = sum_s p[s]*v[s,d] in fp32, serial in s, fp16 RNE      (:119-126)
+// With a chunk start p0 the key count is min(p0 + i + 1, kv_len).
+static void prefill_rows(const uint16_t* q, int q_stride, const uint16_t* k_cache,
+                         const uint16_t* v_cache, uint16_t* out, int out_stride, int p0,
+                         int i_begin, int i_end, int kv_len, int head_dim, int n_q_heads,
+                         int n_kv_heads) {
+    const size_t row = size_t(n_kv_heads) * head_dim;
+    const float inv_sqrt_hd = 1.0f / std::sqrt(float(head_dim));
+    std::vector<float> scores(kv_len);
+    for (int i = i_begin; i < i_end; ++i) {
+        const int n_keys = std::min(p0 + i + 1, kv_len);
+        for (int h = 0; h < n_q_heads; ++h) {
+            const int kv_h = h * n_kv_heads / n_q_heads;
+            const uint16_t* qh = q + size_t(i) * q_stride + size_t(h) * head_dim;
+            for (int t = 0; t < n_keys; ++t) {
+                const uint16_t* kt = k_cache + size_t(t) * row + size_t(kv_h) * head_dim;
+                float score = 0.0f;
+                for (int d = 0; d < head_dim; ++d)
+                    score += ok_f16_to_f32(qh[d]) * ok_f16_to_f32(kt[d]);
+                scores[t] = score * inv_sqrt_hd;
+            }
+            float max_s = -1e38f;
+            for (int t = 0; t < n_keys; ++t) max_s = std::fmax(max_s, scores[t]);
+            float sum_exp = 0.0f;
+            for (int t = 0; t < n_keys; ++t) {
+                scores[t] = std::exp(scores[t] - max_s);
+                sum_exp += scores[t];
+            }
+            for (int t = 0; t < n_keys; ++t) scores[t] /= sum_exp;
+            uint16_t* oh = out + size_t(i) * out_stride + size_t(h) * head_dim;
+            for (int d = 0; d < head_dim; ++d) {
+                float acc = 0.0f;
+                for (int t = 0; t < n_keys; ++t)
+                    acc += scores[t] *
+                           ok_f16_to_f32(v_cache[size_t(t) * row + size_t(kv_h) * head_dim + d]);
+                oh[d] = ok_f32_to_f16(acc);
+            }
+        }
+    }
+}
+
+void ok_prefill_attention(const uint16_t* q, int q_stride, const uint16_t* k_cache,
+                          const uint16_t* v_cache, uint16_t* out, int out_stride, int p0, int n,
+                          int kv_len, int head_dim, int n_q_heads, int n_kv_heads, int n_threads) {
+    if (n_threads <= 1 || n < 2) {
+        prefill_rows(q, q_stride, k_cache, v_cache, out, out_stride, p0, 0, n, kv_len, head_dim,
+                     n_q_heads, n_kv_heads);
+        return;
+    }
+    if (n_threads > n) n_threads = n;
+    // Rows near the end attend more keys: interleave blocks of rows over threads.
+    std::vector<std::thread> pool;
+    for (int w = 0; w < n_threads; ++w)
+        pool.emplace_back([=] {
+            for (int b = w * 8; b < n; b += 8 * n_threads)
+                prefill_rows(q, q_stride, k_cache, v_cache, out, out_stride, p0, b,
+                             std::min(b + 8, n), kv_len, head_dim, n_q_heads, n_kv_heads);
+        });
+    for (auto& t : pool) t.join();
+}
+
+void ok_prefill_attention_f64(const uint16_t* q, int q_stride, const uint16_t* k_cache,
+                              const uint16_t* v_cache, double* out, int p0, int n, int kv_len,
+                              int head_dim, int n_q_heads, int n_kv_heads) {
+    const size_t row = size_t(n_kv_heads) * head_dim;
+    const double inv_sqrt_hd = 1.0 / std::sqrt(double(head_dim));
+    std::vector<double> scores(kv_len);
+    for (int i = 0; i < n; ++i) {
+        const int n_keys = std::min(p0 + i + 1, kv_len);
+        for (int h = 0; h < n_q_heads; ++h) {
+            const int kv_h = h * n_kv_heads / n_q_heads;
+            const uint16_t* qh = q + size_t(i) * q_stride + size_t(h) * head_dim;
+            double m = -1e300;
+            for (int t = 0; t < n_keys; ++t) {
+                double dot = 0.0;
+                for (int d = 0; d < head_dim; ++d)
+                    dot += double(ok_f16_to_f32(qh[d])) *
+                           double(ok_f16_to_f32(k_cache[size_t(t) * row + size_t(kv_h) * head_dim + d]));
+                scores[t] = dot * inv_sqrt_hd;
+                m = std::fmax(m, scores[t]);
+            }
+            double l = 0.0;
+            for (int t = 0; t < n_keys; ++t) {
+                scores[t] = std::exp(scores[t] - m);
+                l += scores[t];
+            }
+            double* oh = out + (size_t(i) * n_q_heads + h) * head_dim;
+            for (int d = 0; d < head_dim; ++d) {
+                double acc = 0.0;
+                for (int t = 0; t < n_keys; ++t)
+                    acc += scores[t] *
+                           double(ok_f16_to_f32(v_cache[size_t(t) * row + size_t(kv_h) * head_dim + d]));
+                oh[d] = acc / l;
+            }
+        }
+    }
+}
+
+void ok_prefill_rope_append(uint16_t* qkv_out, int n, uint16_t* k_cache, uint16_t* v_cache,
+                            const float* cos_table, const float* sin_table, int p0,
+                            int n_q_heads, int n_kv_heads, int head_dim) {
+    const size_t stride = size_t(n_q_heads + 2 * n_kv_heads) * head_dim;
+    for (int i = 0; i < n; ++i)
+        ok_rope_append(qkv_out + i * stride, k_cache, v_cache, cos_table, sin_table, p0 + i,
+                       n_q_heads, n_kv_heads, head_dim);
 }
 
 // ---- a8: FP8 E4M3 codec ------------------------------------------------------

@@ -19,6 +19,10 @@
  *   ok_e4m3_encode / decode        exhaustive vs torch.float8_e4m3fn
  *   ok_paged_gather                contiguous identity table, permuted tables
  *   ok_w8a16_gemv                  identity weights -> x, power-of-two group
+ *   ok_prefill_attention           row i == ok_cached_attention over p0+i+1
+ *                                  rows; seq_kv 1 -> V row 0; torch sdpa
+ *                                  (causal mask) in float64
+ *   ok_prefill_rope_append         == ok_rope_append row by row
  *                                  scales (exact sums), float64 matmul bound
  * The reference ships no golden vectors for this path (its ground_truth *.bin files
  * are full-model activations at seq_len 1).
@@ -61,6 +65,23 @@ void ok_cached_attention(const uint16_t* q, const uint16_t* k_cache, const uint1
 void ok_cached_attention_f64(const uint16_t* q, const uint16_t* k_cache,
                              const uint16_t* v_cache, double* out, int seq_len, int head_dim,
                              int n_q_heads, int n_kv_heads);
+/* Causal prefill attention, src/kernel/tiled_attention.cu:34-130, generalised to
+ * a chunk at cache position p0: query row i (q + i*q_stride) attends cache rows
+ * [0, min(p0 + i + 1, kv_len)); output row i at out + i*out_stride. p0 = 0 and
+ * kv_len = seq_kv is the reference kernel. Threads split the query rows. */
+void ok_prefill_attention(const uint16_t* q, int q_stride, const uint16_t* k_cache,
+                          const uint16_t* v_cache, uint16_t* out, int out_stride, int p0, int n,
+                          int kv_len, int head_dim, int n_q_heads, int n_kv_heads, int n_threads);
+/* Same in double precision, unrounded output [n, n_q_heads*head_dim]. */
+void ok_prefill_attention_f64(const uint16_t* q, int q_stride, const uint16_t* k_cache,
+                              const uint16_t* v_cache, double* out, int p0, int n, int kv_len,
+                              int head_dim, int n_q_heads, int n_kv_heads);
+/* n rows of qkv_out (row stride (n_q_heads+2*n_kv_heads)*head_dim): ok_rope_append
+ * of row i at position p0 + i (engine.cu:326-355 once per prompt token). */
+void ok_prefill_rope_append(uint16_t* qkv_out, int n, uint16_t* k_cache, uint16_t* v_cache,
+                            const float* cos_table, const float* sin_table, int p0,
+                            int n_q_heads, int n_kv_heads, int head_dim);
+
 /* Multi-threaded form of ok_cached_attention (threads over q heads): the CPU baseline. */
 void ok_cached_attention_mt(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                             uint16_t* out, int seq_len, int head_dim, int n_q_heads,

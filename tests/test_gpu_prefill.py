@@ -1,0 +1,228 @@
+"""GPU parity of the prefill path: multi-token RoPE + append and causal attention
+over a prompt chunk (libatomflow_kv.so vs the CPU oracle).
+
+Append: bit-exact, whole caches compared (untouched rows included). Attention:
+within the fp16 bar (max-abs 2e-3, rel 1e-2) of the float64 oracle and of the
+fp32 oracle of the reference's causal kernel (tiled_attention.cu:34-130); query
+rows whose softmax has a single key are compared bit for bit (out = V row).
+"""
+import numpy as np
+import pytest
+
+import atomflow_amd
+import oracle
+from atomflow_amd import device as dev
+from atomflow_amd import kv
+from inputs import (HD, KV_DIM, NKV, NQ, Q_DIM, QKV, THETA, assert_attn_close, randn_f16, rng)
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def up(a):
+    return dev.DeviceBuffer.from_array(a)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+def rope_tables(max_seq):
+    c, s = oracle.rope_table(max_seq, HD, THETA)
+    return c, s, up(c), up(s)
+
+
+def caches(max_seq, filled, seed):
+    k = randn_f16((max_seq, KV_DIM), seed)
+    v = randn_f16((max_seq, KV_DIM), seed + 1)
+    k[filled:] = np.float16(7.0)  # canaries
+    v[filled:] = np.float16(-7.0)
+    return k, v
+
+
+# ---- multi-token append ------------------------------------------------------
+@pytest.mark.parametrize("p0,n", [(0, 1), (0, 37), (100, 300), (4000, 96)])
+def test_prefill_rope_append_bit_exact(gpu, p0, n):
+    say(f"prefill_rope_append p0={p0} n={n}")
+    max_seq = 4096
+    c, s, d_c, d_s = rope_tables(max_seq)
+    qkv = randn_f16((n, QKV), 0xA70F30 + n)
+    k, v = caches(max_seq, p0, 0xA70F31 + p0)
+    d_qkv, d_k, d_v = up(qkv), up(k), up(v)
+    kv.launch_prefill_rope_append(d_qkv, n, d_k, d_v, d_c, d_s, p0, max_seq, NQ, NKV, HD)
+    ref = oracle.prefill_rope_append(qkv, k, v, c, s, p0, NQ, NKV, HD)
+    assert np.array_equal(bits(d_qkv.download(np.float16, qkv.shape)), bits(ref))
+    assert np.array_equal(bits(d_k.download(np.float16, k.shape)), bits(k))
+    assert np.array_equal(bits(d_v.download(np.float16, v.shape)), bits(v))
+
+
+def test_prefill_rope_append_range_checks(gpu):
+    say("prefill_rope_append: host range error, device start skips rows past max_seq")
+    max_seq = 64
+    c, s, d_c, d_s = rope_tables(max_seq)
+    qkv = randn_f16((10, QKV), 0xA70F32)
+    k, v = caches(max_seq, 60, 0xA70F33)
+    d_qkv, d_k, d_v = up(qkv), up(k), up(v)
+    with pytest.raises(RuntimeError):
+        kv.launch_prefill_rope_append(d_qkv, 10, d_k, d_v, d_c, d_s, 55, max_seq, NQ, NKV, HD)
+    assert np.array_equal(bits(d_k.download(np.float16, k.shape)), bits(k))
+    # device start 58: rows 58..63 written, rows for positions 64..67 skipped + status
+    d_p0 = up(np.array([58], np.int32))
+    status = up(np.zeros(1, np.int32))
+    kv.launch_prefill_rope_append(d_qkv, 10, d_k, d_v, d_c, d_s, 0, max_seq, NQ, NKV, HD,
+                                  d_p0=d_p0, d_status=status)
+    assert status.download(np.int32)[0] == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    ref = oracle.prefill_rope_append(qkv[:6], k, v, c, s, 58, NQ, NKV, HD)
+    got = d_qkv.download(np.float16, qkv.shape)
+    assert np.array_equal(bits(got[:6]), bits(ref))
+    assert np.array_equal(bits(got[6:]), bits(qkv[6:]))  # skipped rows untouched
+    assert np.array_equal(bits(d_k.download(np.float16, k.shape)), bits(k))
+    assert np.array_equal(bits(d_v.download(np.float16, v.shape)), bits(v))
+
+
+# ---- causal attention ----------------------------------------------------------
+def run_prefill(q, k, v, p0, n, kv_len, q_stride, out_stride=Q_DIM):
+    d_q, d_k, d_v = up(q), up(k), up(v)
+    d_o = up(np.full((n, out_stride), np.float16(3.0)))
+    kv.launch_prefill_attention(d_q, q_stride, d_k, d_v, d_o, out_stride, p0, n, kv_len,
+                                k.shape[0], NQ, NKV, HD)
+    return d_o.download(np.float16, (n, out_stride))
+
+
+@pytest.mark.parametrize("p0,n,kv_len", [
+    (0, 1, 1), (0, 17, 17), (0, 64, 64), (0, 200, 200), (0, 300, 300),
+    (100, 77, 177), (1000, 129, 1129), (37, 250, 287), (0, 50, 30), (5, 40, 20)])
+def test_prefill_attention_vs_oracle(gpu, p0, n, kv_len):
+    say(f"prefill_attention p0={p0} n={n} kv_len={kv_len}")
+    max_seq = max(kv_len, p0 + n) + 5
+    q = randn_f16((n, QKV), 0xA70F40 + 3 * n + p0)  # Q heads in the first Q_DIM columns
+    k, v = caches(max_seq, kv_len, 0xA70F41 + kv_len)
+    got = run_prefill(q, k, v, p0, n, kv_len, QKV, out_stride=Q_DIM + 64)
+    assert np.all(got[:, Q_DIM:] == np.float16(3.0))  # nothing past the row's heads
+    got = got[:, :Q_DIM]
+    ref64 = oracle.prefill_attention_f64(q, k, v, p0, n, kv_len, NQ, NKV, HD)
+    assert_attn_close(got, ref64, what="vs fp64")
+    ref32 = oracle.prefill_attention(q, k, v, p0, n, kv_len, NQ, NKV, HD, threads=8)
+    assert_attn_close(got, ref32, what="vs fp32 oracle")
+    single = [i for i in range(n) if min(p0 + i + 1, kv_len) == 1]
+    for i in single:  # one key: softmax weight exactly 1, out = V row 0
+        assert np.array_equal(bits(got[i]), bits(ref32[i])), i
+
+
+def test_prefill_attention_long_chunk_sampled_rows(gpu):
+    say("prefill_attention p0=0 n=2048 (sampled rows vs decode oracle)")
+    n = 2048
+    q = randn_f16((n, Q_DIM), 0xA70F50)
+    k, v = caches(n, n, 0xA70F51)
+    got = run_prefill(q, k, v, 0, n, n, Q_DIM)
+    rows = sorted(set(rng(7).choice(n, 24, replace=False).tolist()) | {0, 127, 128, n - 1})
+    for i in rows:
+        ref = oracle.cached_attention_f64(q[i], k, v, i + 1, NQ, NKV, HD)
+        assert_attn_close(got[i], ref, what=f"row {i}")
+
+
+def test_prefill_attention_large_scores(gpu):
+    say("prefill_attention: scaled inputs (scores up to ~100), lazy rescale path")
+    p0, n, kv_len = 0, 160, 160
+    q = randn_f16((n, Q_DIM), 0xA70F52, scale=3.0)
+    k = randn_f16((kv_len, KV_DIM), 0xA70F53, scale=3.0)
+    v = randn_f16((kv_len, KV_DIM), 0xA70F54)
+    got = run_prefill(q, k, v, p0, n, kv_len, Q_DIM)
+    assert_attn_close(got, oracle.prefill_attention_f64(q, k, v, p0, n, kv_len, NQ, NKV, HD))
+
+
+def test_tiled_attention_reference_form(gpu):
+    say("launch_tiled_attention_kernel: seq_q 70 / seq_kv 70, seq_kv 1, seq_kv 0")
+    n = 70
+    q = randn_f16((n, Q_DIM), 0xA70F55)
+    k = randn_f16((n, KV_DIM), 0xA70F56)
+    v = randn_f16((n, KV_DIM), 0xA70F57)
+    d_q, d_k, d_v, d_o = up(q), up(k), up(v), up(np.zeros((n, Q_DIM), np.float16))
+    kv.launch_tiled_attention_kernel(d_q, d_k, d_v, d_o, n, n, HD, NQ, NKV)
+    ref = oracle.prefill_attention(q, k, v, 0, n, n, NQ, NKV, HD)
+    assert_attn_close(d_o.download(np.float16, (n, Q_DIM)), ref)
+    # seq_kv = 1: every query's output is V row 0 (tiled_attention.cu:57-63), exactly
+    kv.launch_tiled_attention_kernel(d_q, d_k, d_v, d_o, n, 1, HD, NQ, NKV)
+    got = d_o.download(np.float16, (n, Q_DIM))
+    vrow = np.concatenate([v[0, (h * NKV // NQ) * HD:(h * NKV // NQ + 1) * HD] for h in range(NQ)])
+    assert np.array_equal(bits(got), np.tile(bits(vrow), (n, 1)))
+    kv.launch_tiled_attention_kernel(d_q, d_k, d_v, d_o, n, 0, HD, NQ, NKV)
+    assert not d_o.download(np.uint16).any()
+
+
+def test_prefill_attention_rejects_bad_arguments(gpu):
+    say("prefill_attention argument checks")
+    lib = atomflow_amd.lib()
+    b = up(np.zeros((8, QKV), np.float16))
+    assert lib.af_prefill_attention(b.ptr, QKV, b.ptr, b.ptr, b.ptr, Q_DIM, 0, 4, 4, 8, NQ, NKV,
+                                    64, None) == atomflow_amd.AF_ERR_UNSUPPORTED
+    assert lib.af_prefill_attention(b.ptr, QKV, b.ptr, b.ptr, b.ptr, Q_DIM, 0, 4, 9, 8, NQ, NKV,
+                                    HD, None) == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    assert lib.af_prefill_attention(b.ptr, QKV, b.ptr, b.ptr, b.ptr, Q_DIM, 0, 4, 0, 8, NQ, NKV,
+                                    HD, None) == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    assert lib.af_prefill_attention(b.ptr, 100, b.ptr, b.ptr, b.ptr, Q_DIM, 0, 4, 4, 8, NQ, NKV,
+                                    HD, None) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert lib.af_prefill_attention(b.ptr, QKV, b.ptr, b.ptr, b.ptr, Q_DIM, 0, 0, 0, 8, NQ, NKV,
+                                    HD, None) == atomflow_amd.AF_OK
+
+
+# ---- chunked prefill then decode ------------------------------------------------
+def test_chunked_prefill_then_decode_step(gpu):
+    say("prefill 2 chunks (p0 0 / 300) via append+attention, then one decode step")
+    max_seq, chunks = 1024, [(0, 300), (300, 213)]
+    c, s, d_c, d_s = rope_tables(max_seq)
+    k = np.zeros((max_seq, KV_DIM), np.float16)
+    v = np.zeros((max_seq, KV_DIM), np.float16)
+    d_k, d_v = up(k), up(v)
+    for p0, n in chunks:
+        qkv = randn_f16((n, QKV), 0xA70F60 + p0)
+        d_qkv = up(qkv)
+        kv.launch_prefill_rope_append(d_qkv, n, d_k, d_v, d_c, d_s, p0, max_seq, NQ, NKV, HD)
+        d_o = up(np.zeros((n, Q_DIM), np.float16))
+        kv.launch_prefill_attention(d_qkv, QKV, d_k, d_v, d_o, Q_DIM, p0, n, p0 + n, max_seq, NQ,
+                                    NKV, HD)
+        ref_qkv = oracle.prefill_rope_append(qkv, k, v, c, s, p0, NQ, NKV, HD)
+        assert np.array_equal(bits(d_qkv.download(np.float16, qkv.shape)), bits(ref_qkv))
+        ref = oracle.prefill_attention_f64(ref_qkv, k, v, p0, n, p0 + n, NQ, NKV, HD)
+        assert_attn_close(d_o.download(np.float16, (n, Q_DIM)), ref, what=f"chunk p0={p0}")
+    assert np.array_equal(bits(d_k.download(np.float16, k.shape)), bits(k))
+    assert np.array_equal(bits(d_v.download(np.float16, v.shape)), bits(v))
+    pos = 513
+    qkv1 = randn_f16(QKV, 0xA70F62)
+    d_qkv1, d_o1 = up(qkv1), up(np.zeros(Q_DIM, np.float16))
+    kv.launch_rope_append(d_qkv1, d_k, d_v, d_c, d_s, pos, max_seq, NQ, NKV, HD)
+    kv.launch_cached_attention(d_qkv1, d_k, d_v, d_o1, pos + 1, HD, NQ, NKV)
+    r1 = oracle.rope_append(qkv1, k, v, c, s, pos, NQ, NKV, HD)
+    assert_attn_close(d_o1.download(np.float16),
+                      oracle.cached_attention_f64(r1[:Q_DIM], k, v, pos + 1, NQ, NKV, HD))
+
+
+def test_paged_chunk_append_whole_blocks(gpu):
+    say("paged pool: a 48-token chunk appended row by row into 3 whole blocks")
+    bs, nblocks, n, p0 = 16, 12, 48, 32
+    pool_bytes = 2 * nblocks * bs * KV_DIM * 2
+    base = dev.DeviceBuffer(pool_bytes)
+    base.fill_u32(0x47004700)  # 7.0 canaries
+    pool = kv.make_pool(base, atomflow_amd.AF_KV_FP16, bs, 1, NKV, HD, nblocks)
+    table = np.array([7, 2, 9, 4, 0], np.int32)  # positions 0..79 -> blocks
+    pos = np.arange(p0, p0 + n, dtype=np.int32)
+    slots = (table[pos // bs].astype(np.int64) * bs + pos % bs)
+    c, s, d_c, d_s = rope_tables(128)
+    qkv = randn_f16((n, QKV), 0xA70F63)
+    d_qkv = up(qkv)
+    kv.launch_paged_rope_append(d_qkv, n, pool, 0, up(slots), up(pos), d_c, d_s, 128, NQ)
+    slab = base.download(np.float16).reshape(2, nblocks * bs, KV_DIM)
+    ks = np.full((nblocks * bs, KV_DIM), np.float16(7.0))
+    vs = ks.copy()
+    ref = np.empty_like(qkv)
+    for i in range(n):
+        kk = np.zeros((128, KV_DIM), np.float16)
+        vv = np.zeros((128, KV_DIM), np.float16)
+        ref[i] = oracle.rope_append(qkv[i], kk, vv, c, s, p0 + i, NQ, NKV, HD)
+        oracle.paged_write_f16(kk[p0 + i], vv[p0 + i], ks, vs, int(slots[i]), KV_DIM)
+    assert np.array_equal(bits(d_qkv.download(np.float16, qkv.shape)), bits(ref))
+    assert np.array_equal(bits(slab[0]), bits(ks))
+    assert np.array_equal(bits(slab[1]), bits(vs))

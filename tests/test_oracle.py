@@ -359,3 +359,98 @@ def test_gemv_random_vs_float64(n, k):
     vals = np.concatenate([_e4m3_positive_values(), [np.nan]])
     wf = vals[w & 0x7f] * np.where(w & 0x80, -1.0, 1.0) * np.repeat(s.astype(np.float64), 128, axis=1)
     assert np.allclose(wf @ x.astype(np.float64), y64, rtol=1e-12, atol=1e-12)
+
+
+# ---- prefill (causal attention over a prompt chunk, multi-token append) -----
+def _prefill_case(p0, n, kv_len, seed, q_stride=Q_DIM, nq=NQ, nkv=NKV, hd=HD):
+    q = randn_f16((n, q_stride), seed)
+    k = randn_f16((kv_len + 3, nkv * hd), seed + 1)
+    v = randn_f16((kv_len + 3, nkv * hd), seed + 2)
+    return q, k, v
+
+
+@pytest.mark.parametrize("p0,n,kv_len", [(0, 9, 9), (5, 6, 11), (0, 7, 4), (3, 4, 5)])
+def test_prefill_f64_rows_equal_decode_f64(p0, n, kv_len):
+    """Row i of the causal form is a decode query over min(p0+i+1, kv_len) rows:
+    the float64 forms share every operation, so they agree bit for bit. Pins the
+    causal limit, the chunk offset, the GQA head map and the row strides against
+    the decode oracle (pinned by its closed forms)."""
+    q, k, v = _prefill_case(p0, n, kv_len, 300 + 7 * p0 + n, q_stride=Q_DIM + 2 * KV_DIM)
+    got = oracle.prefill_attention_f64(q, k, v, p0, n, kv_len, NQ, NKV, HD)
+    for i in range(n):
+        L = min(p0 + i + 1, kv_len)
+        ref = oracle.cached_attention_f64(q[i, :Q_DIM], k, v, L, NQ, NKV, HD)
+        assert np.array_equal(got[i], ref), i
+
+
+@pytest.mark.parametrize("p0,n,kv_len", [(0, 12, 12), (4, 8, 12), (0, 10, 6)])
+def test_prefill_f64_equals_torch_sdpa(p0, n, kv_len):
+    """torch's scaled_dot_product_attention (float64, boolean causal mask, K/V heads
+    repeated per group) as an independent library routine."""
+    import torch
+    nq, nkv, hd = 6, 2, 32
+    q, k, v = _prefill_case(p0, n, kv_len, 410 + n, q_stride=nq * hd, nq=nq, nkv=nkv, hd=hd)
+    got = oracle.prefill_attention_f64(q, k, v, p0, n, kv_len, nq, nkv, hd)
+    tq = torch.from_numpy(q.astype(np.float64)).view(n, nq, hd).transpose(0, 1)
+    tk = torch.from_numpy(k[:kv_len].astype(np.float64)).view(kv_len, nkv, hd).transpose(0, 1)
+    tv = torch.from_numpy(v[:kv_len].astype(np.float64)).view(kv_len, nkv, hd).transpose(0, 1)
+    tk = tk.repeat_interleave(nq // nkv, dim=0)
+    tv = tv.repeat_interleave(nq // nkv, dim=0)
+    mask = torch.arange(kv_len)[None, :] <= (p0 + torch.arange(n))[:, None]
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask)
+    ref = ref.transpose(0, 1).reshape(n, nq * hd).numpy()
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_closed_forms():
+    """seq_kv = 1: every query sees only key 0, so out = V row 0 of its KV head
+    exactly (tiled_attention.cu:57-63); with p0 = 0, query 0 likewise."""
+    def v_row0(v):  # V row 0 of each Q head's KV head, kv(h) = h*NKV/NQ
+        return np.concatenate([v[0, (h * NKV // NQ) * HD:(h * NKV // NQ + 1) * HD]
+                               for h in range(NQ)]).view(np.uint16)
+
+    n = 5
+    q, k, v = _prefill_case(0, n, 1, 500)
+    out = oracle.prefill_attention(q, k, v, 0, n, 1, NQ, NKV, HD)
+    for i in range(n):
+        assert np.array_equal(out[i].view(np.uint16), v_row0(v))
+    q, k, v = _prefill_case(0, 3, 40, 501)
+    out = oracle.prefill_attention(q, k, v, 0, 3, 40, NQ, NKV, HD)
+    assert np.array_equal(out[0].view(np.uint16), v_row0(v))
+
+
+@pytest.mark.parametrize("p0,n,kv_len", [(0, 20, 20), (7, 9, 16)])
+def test_prefill_fp32_within_rounding_of_f64(p0, n, kv_len):
+    from inputs import fp16_ulp
+    q, k, v = _prefill_case(p0, n, kv_len, 520 + n)
+    got = oracle.prefill_attention(q, k, v, p0, n, kv_len, NQ, NKV, HD, threads=3).astype(np.float64)
+    ref = oracle.prefill_attention_f64(q, k, v, p0, n, kv_len, NQ, NKV, HD)
+    # one fp16 rounding plus fp32 softmax / accumulation error (|v| < 6, L <= 16)
+    assert np.all(np.abs(got - ref) <= fp16_ulp(ref) + 1e-5)
+    one = oracle.prefill_attention(q, k, v, p0, n, kv_len, NQ, NKV, HD, threads=1)
+    assert np.array_equal(one.view(np.uint16), got.astype(np.float16).view(np.uint16))
+
+
+def test_prefill_rope_append_equals_token_loop_and_reference_rope_rows():
+    """Multi-token append == ok_rope_append token by token, and its Q/K rotation
+    == the reference's multi-row rope (rope.cu:22-45, seq_len = n) with the table
+    offset to row p0."""
+    max_seq, p0, n = 64, 11, 9
+    cos, sin = oracle.rope_table(max_seq, HD, THETA)
+    qkv = randn_f16((n, Q_DIM + 2 * KV_DIM), 530)
+    k0 = randn_f16((max_seq, KV_DIM), 531)
+    v0 = randn_f16((max_seq, KV_DIM), 532)
+    k1, v1 = k0.copy(), v0.copy()
+    got = oracle.prefill_rope_append(qkv, k1, v1, cos, sin, p0, NQ, NKV, HD)
+    k2, v2 = k0.copy(), v0.copy()
+    for i in range(n):
+        row = oracle.rope_append(qkv[i], k2, v2, cos, sin, p0 + i, NQ, NKV, HD)
+        assert np.array_equal(got[i].view(np.uint16), row.view(np.uint16))
+    assert np.array_equal(k1.view(np.uint16), k2.view(np.uint16))
+    assert np.array_equal(v1.view(np.uint16), v2.view(np.uint16))
+    rq, rk = oracle.rope(qkv[:, :Q_DIM], qkv[:, Q_DIM:Q_DIM + KV_DIM], cos[p0:p0 + n],
+                         sin[p0:p0 + n], NQ, NKV, HD)
+    assert np.array_equal(got[:, :Q_DIM].view(np.uint16), rq.reshape(n, Q_DIM).view(np.uint16))
+    assert np.array_equal(k1[p0:p0 + n].view(np.uint16), rk.reshape(n, KV_DIM).view(np.uint16))
+    untouched = np.r_[0:p0, p0 + n:max_seq]
+    assert np.array_equal(k1[untouched].view(np.uint16), k0[untouched].view(np.uint16))
