@@ -10,27 +10,37 @@
 // p0 + i and attends rows [0, min(p0 + i + 1, kv_len)). p0 = 0 with
 // kv_len = seq_kv is the reference's form (af_tiled_attention).
 //
-// Design: one workgroup = 128 query tokens of one Q head, 4 waves x 32 queries.
-//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16. The A operand is a K tile read from
-//    LDS, the B operand the wave's 32 queries, held in registers for the whole
-//    launch. Each lane then owns 16 of the 32 scores of one query (its partner
-//    lane l^32 owns the other 16), so the softmax max and sum are in-lane work
-//    plus one v_permlane32_swap.
+// Design: a workgroup is 4 waves of one Q head; each wave owns QB blocks of 32
+// queries (the launch uses QB = 1: 128 queries per workgroup, two workgroups
+// per CU).
+//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: the A operand is a K fragment read
+//    from LDS, the B operand a query block held in registers for the whole
+//    launch. Each K fragment feeds the QB query blocks, so LDS bytes per MFMA fall
+//    with QB (LDS delivers about 64 B/clk per CU, one 1 KB fragment per 16 clk;
+//    an MFMA takes 32).
+//  * Each lane owns 16 of the 32 scores of one query (lane l^32 the other 16):
+//    the softmax is in-lane work plus one v_permlane32_swap.
 //  * O^T += V^T P^T. P^T is the S^T accumulator rounded to fp16: within each
 //    16-key step the keys are numbered with bits 2 and 3 swapped, which makes the
-//    accumulator's register order the operand's k order. V is stored transposed
-//    in LDS in that key order, so each V^T operand is one 16-byte LDS read.
-//  * K and V^T tiles of 64 keys are double-buffered in LDS. The next tile's
-//    global loads are issued before the current tile's matrix work and written to
-//    LDS after it: one barrier per tile.
-//  * Both LDS layouts are XOR-swizzled in 16-byte chunks, so the operand reads
-//    and the tile writes spread over the banks.
+//    accumulator's register order the operand's k order. V stays row-major in LDS
+//    and the V^T operand is read with ds_read_b64_tr_b16 (a 16-lane group reads
+//    a 4-key x 16-d block and gets it transposed: lane l, element t = key t,
+//    d = l%16), two per operand.
+//  * K and V tiles of 64 keys are double-buffered in LDS, XOR-swizzled in 16-byte
+//    chunks (K by row%16 for the b128 operand reads, V by 4*(row%4) for the
+//    transposing reads). They go from global memory straight into LDS
+//    (global_load_lds_dwordx4, no registers); the next tile's loads are issued
+//    before the current tile's matrix work: one barrier per tile.
 //  * Softmax is online in the log2 domain with lazy rescaling: the running max
-//    moves only when a tile's max exceeds it by more than 2^8, so most tiles skip
-//    the O^T rescale.
-//  * Workgroups are launched heaviest first (the last query tiles attend the most
-//    keys); waves skip key tiles that lie wholly above their queries' diagonal.
+//    moves only when a tile's probabilities sum past 2^8 in some lane, so most
+//    tiles skip both the tile max and the O^T rescale. The row sum is taken over
+//    the fp16 probabilities the P.V product uses.
+//  * Workgroups are ordered KV head fastest (consecutive workgroups alternate
+//    XCDs, so each XCD's L2 serves one KV head when n_kv_heads divides 8), then
+//    Q head, then query tile heaviest first; waves skip key tiles that lie wholly
+//    above their queries' diagonal.
 #include <cmath>
+#include <type_traits>
 
 #include "af_common.h"
 #include "af_device.h"
@@ -41,14 +51,13 @@ namespace {
 constexpr int kPfHd = 128;
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
-constexpr int kPfQueries = 32 * kPfWaves;          // query tokens per workgroup
-constexpr int kPfKeys = 64;                        // keys per LDS tile
-constexpr int kKTileBytes = kPfKeys * kPfHd * 2;   // K rows of 256 B
-constexpr int kVTileBytes = kPfHd * kPfKeys * 2;   // V^T rows (one per d) of 128 B
-constexpr float kPfLazyLog2 = 8.0f;
+constexpr int kPfKeys = 64;                      // keys per LDS tile
+constexpr int kTileBytes = kPfKeys * kPfHd * 2;  // one K or V tile: 64 rows of 256 B
+constexpr float kPfSumLimit = 256.0f;  // per-lane tile row sum that forces a rescale
 constexpr float kPfEmptyMax = -1e30f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 struct PrefillArgs {
@@ -57,6 +66,7 @@ struct PrefillArgs {
     const uint16_t* k;   // cache row t at k + t*kv_stride
     const uint16_t* v;
     int64_t kv_stride;
+    uint32_t kv_row_bytes;  // kv_stride * 2; the cache spans less than 4 GiB
     uint16_t* out;       // output row i at out + i*out_stride
     int64_t out_stride;
     int32_t p0;
@@ -64,85 +74,57 @@ struct PrefillArgs {
     int32_t kv_len;
     int32_t n_q_heads;
     int32_t n_kv_heads;
-    int32_t n_tiles;     // ceil(n / kPfQueries)
+    int32_t n_tiles;     // ceil(n / queries per workgroup)
     float scale_log2;    // log2(e) / sqrt(head_dim)
 };
 
-// Byte offset of 16-byte chunk `chunk` (0..15) of K tile row `row`.
+// Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
 __device__ __forceinline__ uint32_t k_off(int row, int chunk) {
     return uint32_t(row) * 256u + 16u * uint32_t(chunk ^ (row & 15));
 }
-// Byte offset of 16-byte chunk `chunk` (0..7) of V^T tile row `d`.
-__device__ __forceinline__ uint32_t vt_off(int d, int chunk) {
-    return uint32_t(d) * 128u + 16u * uint32_t(chunk ^ ((d ^ (d >> 3)) & 7));
+// Same in a V tile.
+__device__ __forceinline__ uint32_t v_off(int row, int chunk) {
+    return uint32_t(row) * 256u + 16u * uint32_t(chunk ^ (4 * (row & 3)));
 }
-
-__device__ __forceinline__ uint32_t word(const uint4& u, int p) {
-    return p == 0 ? u.x : p == 1 ? u.y : p == 2 ? u.z : u.w;
-}
-
-// One 64-key tile in flight: thread (c = tid/16, e = tid%16) holds keys
-// key0 + 4c .. +3, elements 8e .. 8e+7 of the head, for K and V. Named fields,
-// not arrays: an array here is promoted to LDS by the compiler, which then
-// waits for the loads right after issuing them.
-struct TileRegs {
-    uint4 k0, k1, k2, k3;
-    uint4 v0, v1, v2, v3;
-};
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
-__device__ __forceinline__ void load_tile(const uint16_t* kb, const uint16_t* vb,
-                                          int64_t kv_stride, int key0, int kv_len, int c, int e,
-                                          TileRegs& t) {
-    // Rows past kv_len load row kv_len-1: finite data whose scores are masked.
-    const int r = key0 + 4 * c;
-    const size_t o0 = size_t(min(r, kv_len - 1)) * kv_stride + 8 * e;
-    const size_t o1 = size_t(min(r + 1, kv_len - 1)) * kv_stride + 8 * e;
-    const size_t o2 = size_t(min(r + 2, kv_len - 1)) * kv_stride + 8 * e;
-    const size_t o3 = size_t(min(r + 3, kv_len - 1)) * kv_stride + 8 * e;
-    t.k0 = ld16(kb + o0);
-    t.k1 = ld16(kb + o1);
-    t.k2 = ld16(kb + o2);
-    t.k3 = ld16(kb + o3);
-    t.v0 = ld16(vb + o0);
-    t.v1 = ld16(vb + o1);
-    t.v2 = ld16(vb + o2);
-    t.v3 = ld16(vb + o3);
-}
-
-__device__ __forceinline__ void store_tile(char* ks, char* vs, int c, int e, const TileRegs& t) {
-    *reinterpret_cast<uint4*>(ks + k_off(4 * c + 0, e)) = t.k0;
-    *reinterpret_cast<uint4*>(ks + k_off(4 * c + 1, e)) = t.k1;
-    *reinterpret_cast<uint4*>(ks + k_off(4 * c + 2, e)) = t.k2;
-    *reinterpret_cast<uint4*>(ks + k_off(4 * c + 3, e)) = t.k3;
-    // Keys 4c..4c+3 sit in 16-key step j = c/4 at offsets 4a..4a+3 (a = c%4);
-    // with bits 2 and 3 of the offset swapped they become the four consecutive
-    // slots 4*sa .. 4*sa+3 of that step.
-    const int j = c >> 2, a = c & 3;
-    const int sa = ((a & 1) << 1) | (a >> 1);
-    const int chunk = 2 * j + (sa >> 1);
-    const uint32_t half_off = 8u * uint32_t(sa & 1);
-    // Lanes with odd e walk their eight d rows in the order i^1, which spreads a
-    // write instruction over both 128-byte halves of the bank space.
-    const uint32_t sel_even = (e & 1) ? 0x07060302u : 0x05040100u;
-    const uint32_t sel_odd = (e & 1) ? 0x05040100u : 0x07060302u;
+// Loads one 64-key K or V tile straight into LDS (global_load_lds_dwordx4: lane
+// l of a wave writes the 16 bytes at LDS base + 16*l). Wave w fills rows
+// 16w .. 16w+15, four rows per instruction; the lane at physical chunk p of row r
+// fetches logical chunk p ^ swz(r), which realises the swizzled layout. Rows past
+// kv_len load row kv_len-1: finite data whose scores are masked. base: the
+// head's first element in cache row 0, as bytes; 32-bit row offsets keep the
+// loads in the scalar-base + vector-offset form.
+template <bool IS_K>
+__device__ __forceinline__ void dma_tile(const char* base, uint32_t row_bytes, int key0,
+                                         int kv_len, int wave, int lane, char* lds_tile) {
+    const int pr = lane >> 4, pc = lane & 15;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int p = i >> 1;
-        const uint32_t sel = (i & 1) ? sel_odd : sel_even;
-        uint2 pk;
-        pk.x = __builtin_amdgcn_perm(word(t.v1, p), word(t.v0, p), sel);
-        pk.y = __builtin_amdgcn_perm(word(t.v3, p), word(t.v2, p), sel);
-        const int d = 8 * e + (i ^ (e & 1));
-        *reinterpret_cast<uint2*>(vs + vt_off(d, chunk) + half_off) = pk;
+    for (int i = 0; i < 4; ++i) {
+        const int r = 16 * wave + 4 * i + pr;  // tile row
+        const int chunk = IS_K ? (pc ^ (r & 15)) : (pc ^ (4 * (r & 3)));
+        const uint32_t off = __umul24(uint32_t(min(key0 + r, kv_len - 1)), row_bytes) + 16u * chunk;
+        __builtin_amdgcn_global_load_lds(
+            base + off, (__attribute__((address_space(3))) void*)(lds_tile + (16 * wave + 4 * i) * 256),
+            16, 0, 0);
     }
 }
 
 __device__ __forceinline__ half8 lds_half8(const char* p) {
     return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
+}
+
+// V^T operand of one (16-key step, 32-d block): two transposing reads of 4 keys.
+__device__ __forceinline__ half8 lds_vt(const char* p0, const char* p1) {
+    typedef short4_t __attribute__((address_space(3)))* lds_s4;
+    const short4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p0));
+    const short4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p1));
+    typedef short short8_t __attribute__((ext_vector_type(8)));
+    const short8_t r = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(half8, r);
 }
 
 // Max / sum over the two 32-lane halves (lane l and l^32).
@@ -164,141 +146,225 @@ __device__ __forceinline__ half8 to_half8(const float16v& s, int base) {
     return h;
 }
 
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const PrefillArgs a) {
-    __shared__ __align__(16) char s_k[2][kKTileBytes];
-    __shared__ __align__(16) char s_v[2][kVTileBytes];
+__device__ __forceinline__ float dot2_sum(const half8& h, float acc) {
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    const half2_t one = {f16(1.0f), f16(1.0f)};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const half2_t p = {h[2 * t], h[2 * t + 1]};
+        acc = __builtin_amdgcn_fdot2(p, one, acc, false);
+    }
+    return acc;
+}
+
+// LDS: K tiles at [0, 2*kTileBytes), V tiles after them.
+constexpr int kVBase = 2 * kTileBytes;
+
+template <int QB>
+__global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention_kernel(
+    const PrefillArgs a) {
+    constexpr int kQueries = 32 * QB * kPfWaves;  // per workgroup
+    __shared__ __align__(16) char s_lds[4 * kTileBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform branches below
     const int col = lane & 31, hi = lane >> 5;
-    const int tile = a.n_tiles - 1 - int(blockIdx.x) / a.n_q_heads;  // heaviest first
-    const int head = int(blockIdx.x) % a.n_q_heads;
-    const int kvh = head * a.n_kv_heads / a.n_q_heads;
-    const int t0 = tile * kPfQueries;
-    const int wq0 = t0 + 32 * wave;                // the wave's first query
+    // Block order: KV head fastest, then Q head of the group, then query tile
+    // heaviest first.
+    const int group = a.n_q_heads / a.n_kv_heads;
+    const int kvh = int(blockIdx.x) % a.n_kv_heads;
+    const int rest = int(blockIdx.x) / a.n_kv_heads;
+    const int head = kvh * group + rest % group;
+    const int tile = a.n_tiles - 1 - rest / group;
+    const int t0 = tile * kQueries;
+    const int wq0 = t0 + 32 * QB * wave;  // the wave's first query
     const bool wave_live = wq0 < a.n;
-    const int qi = min(wq0 + col, a.n - 1);        // this lane's query (clamped)
-    const int lim = min(a.p0 + qi + 1, a.kv_len);  // its keys: [0, lim)
 
-    const int wg_keys = min(a.p0 + min(t0 + kPfQueries, a.n), a.kv_len);
+    const int wg_keys = min(a.p0 + min(t0 + kQueries, a.n), a.kv_len);
     const int n_kt = (wg_keys + kPfKeys - 1) / kPfKeys;
-    // Keys the wave needs, and the first key hidden from some of its queries.
-    const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32, a.n), a.kv_len) : 0;
-    const int w_mask_from = min(a.p0 + wq0 + 1, a.kv_len);
+    // Keys the wave needs.
+    const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32 * QB, a.n), a.kv_len) : 0;
 
-    // Query operand first: the loop's first waits then cover it.
-    half8 qf[8];
-    {
+    // Query operands first: the loop's first waits then cover them.
+    half8 qf[QB][8];
+    int lim[QB];       // this lane's query of block b attends keys [0, lim[b])
+    int mask_from[QB]; // first key hidden from some query of block b
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+        const int qi = min(wq0 + 32 * b + col, a.n - 1);  // clamped
+        lim[b] = min(a.p0 + qi + 1, a.kv_len);
+        mask_from[b] = min(a.p0 + wq0 + 32 * b + 1, a.kv_len);
         const uint16_t* qrow = a.q + size_t(qi) * a.q_stride + size_t(head) * kPfHd + 8 * hi;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(half8, ld16(qrow + 16 * s));
+        for (int s = 0; s < 8; ++s) qf[b][s] = __builtin_bit_cast(half8, ld16(qrow + 16 * s));
     }
     // Keep the query loads ahead of the tile loads: the prologue's wait for the
     // tile then covers them, and the loop never waits on a query register.
     asm volatile("" ::: "memory");
-    const uint16_t* kb = a.k + size_t(kvh) * kPfHd;
-    const uint16_t* vb = a.v + size_t(kvh) * kPfHd;
-    const int c = tid >> 4, e = tid & 15;
-    TileRegs tr;
-    load_tile(kb, vb, a.kv_stride, 0, a.kv_len, c, e, tr);
-    store_tile(s_k[0], s_v[0], c, e, tr);
+    const char* kb = reinterpret_cast<const char*>(a.k + size_t(kvh) * kPfHd);
+    const char* vb = reinterpret_cast<const char*>(a.v + size_t(kvh) * kPfHd);
+    dma_tile<true>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds);
+    dma_tile<false>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase);
 
-    float16v o[4];
+    // Per-lane LDS operand offsets; the buffer, the key block and the key step
+    // are added as immediates.
+    //  K: row col (+32 for keys 32..63), chunk 2s+hi.
+    //  V^T: lane l of 16-lane group G reads row K0 + (l%16)/4 at d = 32db +
+    //  16(G%2) + 4(l%4), K0 = 16j + 8u + 4hi (u: first / second four slots).
+    uint32_t ka[8], va[4];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int s = 0; s < 8; ++s) ka[s] = k_off(col, 2 * s + hi);
+    {
+        const int jl = lane & 15, g1 = (lane >> 4) & 1;
+        const int rl = jl >> 2;  // row within the 4-key group (= row % 4)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
-    float m_run = kPfEmptyMax, l_run = 0.0f;
-    const float sc = a.scale_log2;
-
-    for (int kt = 0; kt < n_kt; ++kt) {
-        __syncthreads();
-        const int buf = kt & 1;
-        const bool more = kt + 1 < n_kt;
-        if (more) load_tile(kb, vb, a.kv_stride, (kt + 1) * kPfKeys, a.kv_len, c, e, tr);
-        const int key0 = kt * kPfKeys;
-        if (key0 < w_keys) {
-            const char* ks = s_k[buf];
-            float16v s0, s1;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const half8 k0 = lds_half8(ks + k_off(col, 2 * s + hi));
-                const half8 k1 = lds_half8(ks + k_off(32 + col, 2 * s + hi));
-                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qf[s], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qf[s], s1, 0, 0, 0);
-            }
-            // Register r of block b holds key key0 + 32b + 8(r/4) + 4hi + r%4.
-            if (key0 + kPfKeys > w_mask_from) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = key0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    s0[r] = key < lim ? s0[r] : -INFINITY;
-                    s1[r] = key + 32 < lim ? s1[r] : -INFINITY;
-                }
-            }
-            float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-            mx = halves_max(mx) * sc;
-            const bool need = mx > m_run + kPfLazyLog2;
-            if (__builtin_amdgcn_ballot_w64(need)) {
-                const float m_new = need ? mx : m_run;
-                const float alpha = fast_exp2(m_run - m_new);
-                m_run = m_new;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-            }
-            float ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s0[r] = fast_exp2(fmaf(s0[r], sc, -m_run));
-                s1[r] = fast_exp2(fmaf(s1[r], sc, -m_run));
-                ls += s0[r] + s1[r];
-            }
-            l_run += ls;
-            half8 pj[4];
-            pj[0] = to_half8(s0, 0);
-            pj[1] = to_half8(s0, 8);
-            pj[2] = to_half8(s1, 0);
-            pj[3] = to_half8(s1, 8);
-            const char* vs = s_v[buf];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const half8 vt = lds_half8(vs + vt_off(32 * db + col, 2 * j + hi));
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pj[j], o[db], 0, 0, 0);
-                }
+        for (int db = 0; db < 4; ++db) {
+            const int d = 32 * db + 16 * g1 + 4 * (jl & 3);
+            va[db] = kVBase + v_off(4 * hi + rl, d >> 3) + 2 * (d & 7);
         }
-        if (more) store_tile(s_k[buf ^ 1], s_v[buf ^ 1], c, e, tr);
     }
 
-    if (!wave_live || wq0 + col >= a.n) return;
-    const float inv = 1.0f / halves_sum(l_run);
-    uint16_t* orow = a.out + size_t(wq0 + col) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
+    float16v o[QB][4];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int b = 0; b < QB; ++b)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint2 w;
-            w.x = uint32_t(f2h(o[db][4 * g] * inv)) | (uint32_t(f2h(o[db][4 * g + 1] * inv)) << 16);
-            w.y = uint32_t(f2h(o[db][4 * g + 2] * inv)) |
-                  (uint32_t(f2h(o[db][4 * g + 3] * inv)) << 16);
-            *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) = w;
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[b][db][r] = 0.0f;
+    float m_run[QB], l_run[QB];
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+        m_run[b] = kPfEmptyMax;
+        l_run[b] = 0.0f;
+    }
+    const float sc = a.scale_log2;
+
+    auto step = [&](int kt, auto buf_c) {
+        constexpr int BUF = decltype(buf_c)::value;
+        // This wave's tile loads have landed in LDS; the barrier covers the others'
+        // and frees the other buffer (read in the previous step) for the next tile.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 1 < n_kt) {
+            dma_tile<true>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
+                           s_lds + (BUF ^ 1) * kTileBytes);
+            dma_tile<false>(vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
+                            s_lds + kVBase + (BUF ^ 1) * kTileBytes);
         }
+        const int key0 = kt * kPfKeys;
+        const char* ks = s_lds + BUF * kTileBytes;
+        const char* vs = s_lds + BUF * kTileBytes;  // va[] carries the V region's base
+        // Two halves of 32 keys: QK^T, softmax, then P.V for each.
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int keyh = key0 + 32 * kb;
+            if (keyh >= w_keys) break;  // wave-uniform
+            float16v sacc[QB];
+#pragma unroll
+            for (int b = 0; b < QB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[b][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const half8 kf = lds_half8(ks + ka[s] + kb * 32 * 256);
+#pragma unroll
+                for (int b = 0; b < QB; ++b)
+                    sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[b][s], sacc[b], 0, 0, 0);
+            }
+            half8 pj[QB][2];
+#pragma unroll
+            for (int b = 0; b < QB; ++b) {
+                // Register r holds key keyh + 8(r/4) + 4hi + r%4.
+                if (keyh + 32 > mask_from[b]) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = keyh + 8 * (r >> 2) + 4 * hi + (r & 3);
+                        sacc[b][r] = key < lim[b] ? sacc[b][r] : -INFINITY;
+                    }
+                }
+                // Probabilities against the running max m_run, rounded to fp16,
+                // and their row sum. While each lane's sum stays <= 2^8, every p
+                // is <= 2^8 and m_run is kept (it may trail the true max by up to
+                // 8 in log2 units; fp16 holds p to 2^15). Otherwise (the first
+                // keys, or scores that grew) the exact running max is taken and
+                // O^T, l rescaled: the max is computed only on this path.
+                float ls;
+                auto probs = [&]() {
+                    float16v pv;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(sacc[b][r], sc, -m_run[b]));
+                    pj[b][0] = to_half8(pv, 0);
+                    pj[b][1] = to_half8(pv, 8);
+                    ls = dot2_sum(pj[b][1], dot2_sum(pj[b][0], 0.0f));
+                };
+                probs();
+                if (__builtin_amdgcn_ballot_w64(!(ls <= kPfSumLimit))) {
+                    float mx = sacc[b][0];
+#pragma unroll
+                    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[b][r]);
+                    const float m_new = fmaxf(m_run[b], halves_max(mx) * sc);
+                    const float alpha = fast_exp2(m_run[b] - m_new);
+                    m_run[b] = m_new;
+                    l_run[b] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 4; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[b][db][r] *= alpha;
+                    probs();
+                }
+                l_run[b] += ls;
+            }
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const char* p = vs + va[db] + 16 * (2 * kb + jj) * 256;
+                    const half8 vt = lds_vt(p, p + 8 * 256);
+#pragma unroll
+                    for (int b = 0; b < QB; ++b)
+                        o[b][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pj[b][jj], o[b][db],
+                                                                          0, 0, 0);
+                }
+        }
+    };
+    int kt = 0;
+    for (; kt + 2 <= n_kt; kt += 2) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt < n_kt) step(kt, std::integral_constant<int, 0>{});
+
+    if (!wave_live) return;
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+        const int qi = wq0 + 32 * b + col;
+        const float inv = 1.0f / halves_sum(l_run[b]);
+        if (qi >= a.n) continue;
+        uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint2 w;
+                w.x = uint32_t(f2h(o[b][db][4 * g] * inv)) |
+                      (uint32_t(f2h(o[b][db][4 * g + 1] * inv)) << 16);
+                w.y = uint32_t(f2h(o[b][db][4 * g + 2] * inv)) |
+                      (uint32_t(f2h(o[b][db][4 * g + 3] * inv)) << 16);
+                *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) = w;
+            }
+    }
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-    const int grid = a.n_tiles * a.n_q_heads;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(kPfThreads), 0, stream, a);
+// One query block per wave: two workgroups per CU keep the matrix cores fed
+// across each other's softmax. (Two blocks per wave halve the LDS bytes per
+// MFMA but leave one wave per SIMD with its softmax exposed; measured slower.)
+int launch_prefill(PrefillArgs a, hipStream_t stream) {
+    a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
+    hipLaunchKernelGGL(prefill_attention_kernel<1>, dim3(a.n_tiles * a.n_q_heads),
+                       dim3(kPfThreads), 0, stream, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -330,6 +396,9 @@ extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_c
     a.k = static_cast<const uint16_t*>(k_cache);
     a.v = static_cast<const uint16_t*>(v_cache);
     a.kv_stride = int64_t(n_kv_heads) * head_dim;
+    // 32-bit row offsets in the kernel: the cache must span less than 4 GiB.
+    if (int64_t(max_seq) * a.kv_stride * 2 >= (int64_t(1) << 32)) return AF_ERR_UNSUPPORTED;
+    a.kv_row_bytes = uint32_t(a.kv_stride * 2);
     a.out = static_cast<uint16_t*>(out);
     a.out_stride = out_stride;
     a.p0 = p0;
@@ -337,7 +406,6 @@ extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_c
     a.kv_len = kv_len;
     a.n_q_heads = n_q_heads;
     a.n_kv_heads = n_kv_heads;
-    a.n_tiles = ceil_div(n, kPfQueries);
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(head_dim)));
     return launch_prefill(a, static_cast<hipStream_t>(stream));
 }

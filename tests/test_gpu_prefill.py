@@ -124,6 +124,23 @@ def test_prefill_attention_long_chunk_sampled_rows(gpu):
         assert_attn_close(got[i], ref, what=f"row {i}")
 
 
+@pytest.mark.parametrize("p0,n,kv_len", [(0, 6000, 6000), (3000, 5500, 8500), (0, 5600, 4100)])
+def test_prefill_attention_long_chunks(gpu, p0, n, kv_len):
+    """Long chunks (thousands of workgroups, many LDS tiles per workgroup); sampled
+    rows against the float64 decode oracle over min(p0+i+1, kv_len) rows."""
+    say(f"prefill_attention p0={p0} n={n} kv_len={kv_len} (sampled rows)")
+    max_seq = max(kv_len, p0 + n)
+    q = randn_f16((n, Q_DIM), 0xA70F58 + n)
+    k, v = caches(max_seq, kv_len, 0xA70F59 + p0)
+    got = run_prefill(q, k, v, p0, n, kv_len, Q_DIM)
+    edge = {0, 31, 32, 63, 64, 255, 256, 257, n - 257, n - 256, n - 1, max(0, kv_len - p0 - 1)}
+    rows = sorted(set(rng(p0 + n).choice(n, 20, replace=False).tolist()) | {i for i in edge if 0 <= i < n})
+    for i in rows:
+        L = min(p0 + i + 1, kv_len)
+        ref = oracle.cached_attention_f64(q[i], k, v, L, NQ, NKV, HD)
+        assert_attn_close(got[i], ref, what=f"row {i} (L={L})")
+
+
 def test_prefill_attention_large_scores(gpu):
     say("prefill_attention: scaled inputs (scores up to ~100), lazy rescale path")
     p0, n, kv_len = 0, 160, 160
