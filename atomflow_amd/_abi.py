@@ -59,6 +59,7 @@ PROTOTYPES = {
     "af_prefill_rope_append": (I, [P, I, P, P, P, P, I, P, I, I, I, I, P, P]),
     "af_prefill_attention": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, P]),
     "af_tiled_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "af_paged_prefill_attention": (I, [P, I, P, I, P, I, I, I, I, P, I, I, P]),
     "af_bm_create": (I, [I, I, I, I, I, I, I, ctypes.POINTER(P)]),
     "af_bm_destroy": (I, [P]),
     "af_bm_attach_pool": (I, [P, P, P]),

@@ -114,6 +114,15 @@ void launch_prefill_attention(const __half* q, int q_stride, const View& k_cache
           "launch_prefill_attention");
 }
 
+void launch_paged_prefill_attention(const __half* q, int q_stride, const af_kv_pool& pool,
+                                    int layer, const int32_t* d_block_table, int max_blocks,
+                                    int p0, int n, int kv_len, __half* out, int out_stride,
+                                    int n_q_heads, hipStream_t stream) {
+    check(af_paged_prefill_attention(q, q_stride, &pool, layer, d_block_table, max_blocks, p0, n,
+                                     kv_len, out, out_stride, n_q_heads, stream),
+          "launch_paged_prefill_attention");
+}
+
 void launch_cached_attention_ws(const __half* q, const __half* k_cache, const __half* v_cache,
                                 __half* out, int seq_len, const int32_t* d_seq_len,
                                 int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,

@@ -35,6 +35,8 @@
 //    moves only when a tile's probabilities sum past 2^8 in some lane, so most
 //    tiles skip both the tile max and the O^T rescale. The row sum is taken over
 //    the fp16 probabilities the P.V product uses.
+//  * Paged pools (PAGED): tile rows map through the sequence's block table; the
+//    entries for tile kt+1 are fetched during tile kt-1.
 //  * Workgroups are ordered KV head fastest (consecutive workgroups alternate
 //    XCDs, so each XCD's L2 serves one KV head when n_kv_heads divides 8), then
 //    Q head, then query tile heaviest first; waves skip key tiles that lie wholly
@@ -76,6 +78,10 @@ struct PrefillArgs {
     int32_t n_kv_heads;
     int32_t n_tiles;     // ceil(n / queries per workgroup)
     float scale_log2;    // log2(e) / sqrt(head_dim)
+    // Paged pool: k / v are the layer's K / V slabs (rows of kv_stride elements),
+    // logical row t lives in slot table[t >> bs_log2] * block_size + t % block_size.
+    const int32_t* table;
+    int32_t bs_log2;
 };
 
 // Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
@@ -96,20 +102,39 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
 // 16w .. 16w+15, four rows per instruction; the lane at physical chunk p of row r
 // fetches logical chunk p ^ swz(r), which realises the swizzled layout. Rows past
 // kv_len load row kv_len-1: finite data whose scores are masked. base: the
-// head's first element in cache row 0, as bytes; 32-bit row offsets keep the
-// loads in the scalar-base + vector-offset form.
-template <bool IS_K>
+// head's first element in cache row (slot) 0, as bytes. Contiguous caches use
+// 32-bit row offsets (scalar base + vector offset); paged pools map the row
+// through blk[i], the physical block of the lane's row in instruction i.
+template <bool IS_K, bool PAGED>
 __device__ __forceinline__ void dma_tile(const char* base, uint32_t row_bytes, int key0,
-                                         int kv_len, int wave, int lane, char* lds_tile) {
+                                         int kv_len, int wave, int lane, char* lds_tile,
+                                         const int (&blk)[4], int bs_log2) {
     const int pr = lane >> 4, pc = lane & 15;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = 16 * wave + 4 * i + pr;  // tile row
         const int chunk = IS_K ? (pc ^ (r & 15)) : (pc ^ (4 * (r & 3)));
-        const uint32_t off = __umul24(uint32_t(min(key0 + r, kv_len - 1)), row_bytes) + 16u * chunk;
+        const int key = min(key0 + r, kv_len - 1);
+        const char* src;
+        if constexpr (PAGED) {
+            const int64_t slot = (int64_t(blk[i]) << bs_log2) | (key & ((1 << bs_log2) - 1));
+            src = base + slot * row_bytes + 16 * chunk;
+        } else {
+            src = base + (__umul24(uint32_t(key), row_bytes) + 16u * chunk);
+        }
         __builtin_amdgcn_global_load_lds(
-            base + off, (__attribute__((address_space(3))) void*)(lds_tile + (16 * wave + 4 * i) * 256),
+            src, (__attribute__((address_space(3))) void*)(lds_tile + (16 * wave + 4 * i) * 256),
             16, 0, 0);
+    }
+}
+
+// Physical blocks of the rows this lane fetches for tile `kt` (paged pools).
+__device__ __forceinline__ void tile_blocks(const int32_t* table, int bs_log2, int kt, int kv_len,
+                                            int wave, int lane, int (&blk)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int key = min(kt * kPfKeys + 16 * wave + 4 * i + (lane >> 4), kv_len - 1);
+        blk[i] = table[key >> bs_log2];
     }
 }
 
@@ -160,7 +185,7 @@ __device__ __forceinline__ float dot2_sum(const half8& h, float acc) {
 // LDS: K tiles at [0, 2*kTileBytes), V tiles after them.
 constexpr int kVBase = 2 * kTileBytes;
 
-template <int QB>
+template <int QB, bool PAGED>
 __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention_kernel(
     const PrefillArgs a) {
     constexpr int kQueries = 32 * QB * kPfWaves;  // per workgroup
@@ -204,8 +229,15 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
     asm volatile("" ::: "memory");
     const char* kb = reinterpret_cast<const char*>(a.k + size_t(kvh) * kPfHd);
     const char* vb = reinterpret_cast<const char*>(a.v + size_t(kvh) * kPfHd);
-    dma_tile<true>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds);
-    dma_tile<false>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase);
+    // Paged: the block-table entries of tile kt+1 are loaded one step ahead, so
+    // the wait for tile kt's data also covers them.
+    int blk[4] = {0, 0, 0, 0};
+    if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, 0, a.kv_len, wave, lane, blk);
+    dma_tile<true, PAGED>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds, blk, a.bs_log2);
+    dma_tile<false, PAGED>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase, blk,
+                           a.bs_log2);
+    if constexpr (PAGED)
+        if (n_kt > 1) tile_blocks(a.table, a.bs_log2, 1, a.kv_len, wave, lane, blk);
 
     // Per-lane LDS operand offsets; the buffer, the key block and the key step
     // are added as immediates.
@@ -247,10 +279,12 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (kt + 1 < n_kt) {
-            dma_tile<true>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
-                           s_lds + (BUF ^ 1) * kTileBytes);
-            dma_tile<false>(vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
-                            s_lds + kVBase + (BUF ^ 1) * kTileBytes);
+            dma_tile<true, PAGED>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
+                                  s_lds + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
+            dma_tile<false, PAGED>(vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
+                                   s_lds + kVBase + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
+            if constexpr (PAGED)
+                if (kt + 2 < n_kt) tile_blocks(a.table, a.bs_log2, kt + 2, a.kv_len, wave, lane, blk);
         }
         const int key0 = kt * kPfKeys;
         const char* ks = s_lds + BUF * kTileBytes;
@@ -363,8 +397,12 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // MFMA but leave one wave per SIMD with its softmax exposed; measured slower.)
 int launch_prefill(PrefillArgs a, hipStream_t stream) {
     a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
-    hipLaunchKernelGGL(prefill_attention_kernel<1>, dim3(a.n_tiles * a.n_q_heads),
-                       dim3(kPfThreads), 0, stream, a);
+    if (a.table)
+        hipLaunchKernelGGL((prefill_attention_kernel<1, true>), dim3(a.n_tiles * a.n_q_heads),
+                           dim3(kPfThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((prefill_attention_kernel<1, false>), dim3(a.n_tiles * a.n_q_heads),
+                           dim3(kPfThreads), 0, stream, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -407,6 +445,48 @@ extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_c
     a.n_q_heads = n_q_heads;
     a.n_kv_heads = n_kv_heads;
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(head_dim)));
+    return launch_prefill(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* pool,
+                                          int layer, const int32_t* d_block_table,
+                                          int max_blocks, int p0, int n, int kv_len, void* out,
+                                          int out_stride, int n_q_heads, af_stream_t stream) {
+    if (!q || !pool || !pool->base || !d_block_table || !out || n < 0 || p0 < 0 ||
+        n_q_heads <= 0 || max_blocks <= 0)
+        return AF_ERR_INVALID_ARG;
+    if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
+        n_q_heads % pool->n_kv_heads)
+        return AF_ERR_INVALID_ARG;
+    if (pool->dtype != AF_KV_FP16 || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
+    const int bs = pool->block_size;
+    if (bs < 8 || (bs & (bs - 1))) return AF_ERR_INVALID_ARG;
+    const int q_dim = n_q_heads * kPfHd;
+    if (q_stride < q_dim || out_stride < q_dim || q_stride % 8 || out_stride % 8)
+        return AF_ERR_INVALID_ARG;
+    if (!aligned16(q) || !aligned16(out) || !aligned16(pool->base)) return AF_ERR_INVALID_ARG;
+    if (n == 0) return AF_OK;
+    if (kv_len <= 0 || int64_t(kv_len) > int64_t(max_blocks) * bs) return AF_ERR_OUT_OF_RANGE;
+    const int64_t kv_stride = int64_t(pool->n_kv_heads) * kPfHd;
+    const size_t slab = size_t(pool->total_blocks) * bs * kv_stride;  // elements
+    const uint16_t* base = static_cast<const uint16_t*>(pool->base);
+    PrefillArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.q_stride = q_stride;
+    a.k = base + size_t(2 * layer) * slab;
+    a.v = a.k + slab;
+    a.kv_stride = kv_stride;
+    a.kv_row_bytes = uint32_t(kv_stride * 2);
+    a.out = static_cast<uint16_t*>(out);
+    a.out_stride = out_stride;
+    a.p0 = p0;
+    a.n = n;
+    a.kv_len = kv_len;
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = pool->n_kv_heads;
+    a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
+    a.table = d_block_table;
+    a.bs_log2 = __builtin_ctz(unsigned(bs));
     return launch_prefill(a, static_cast<hipStream_t>(stream));
 }
 

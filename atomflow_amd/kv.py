@@ -90,6 +90,15 @@ def launch_prefill_attention(q, q_stride, k_cache, v_cache, out, out_stride, p0,
                                      head_dim, _s(stream)), "launch_prefill_attention")
 
 
+def launch_paged_prefill_attention(q, q_stride, pool, layer, d_block_table, max_blocks, p0, n,
+                                   kv_len, out, out_stride, n_q_heads, stream=None):
+    """Causal chunk attention over one sequence's rows of a paged pool."""
+    check(lib().af_paged_prefill_attention(_p(q), q_stride, ctypes.byref(pool), layer,
+                                           _p(d_block_table), max_blocks, p0, n, kv_len, _p(out),
+                                           out_stride, n_q_heads, _s(stream)),
+          "launch_paged_prefill_attention")
+
+
 def launch_tiled_attention_kernel(q, k, v, out, seq_q, seq_kv, head_dim, n_q_heads, n_kv_heads,
                                   stream=None):
     """tiled_attention.cu launch_tiled_attention_kernel<half>: query i attends keys s <= i."""
@@ -336,7 +345,7 @@ __all__ = [
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
     "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
     "launch_w8a16_gemv", "launch_prefill_rope_append", "launch_prefill_attention",
-    "launch_tiled_attention_kernel",
+    "launch_tiled_attention_kernel", "launch_paged_prefill_attention",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

@@ -267,6 +267,17 @@ int af_prefill_attention(const void* q, int q_stride, const void* k_cache, const
                          void* out, int out_stride, int p0, int n, int kv_len, int max_seq,
                          int n_q_heads, int n_kv_heads, int head_dim, af_stream_t stream);
 
+/* af_prefill_attention over one sequence's rows of a paged pool: logical row t of
+ * `layer` is read through d_block_table (device int32 [max_blocks]), slot
+ * d_block_table[t / block_size] * block_size + t % block_size. Chunked prefill
+ * (src/experimental/server_arch roadmap, README.md:269): append the chunk with
+ * af_paged_rope_append (one slot per token), then this. FP16 pools with
+ * head_dim 128 (else AF_ERR_UNSUPPORTED); kv_len <= max_blocks * block_size. */
+int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                               const int32_t* d_block_table, int max_blocks, int p0, int n,
+                               int kv_len, void* out, int out_stride, int n_q_heads,
+                               af_stream_t stream);
+
 /* launch_tiled_attention_kernel<half> (include/ops/kernel.h:73-85,
  * src/kernel/tiled_attention.cu:136-161): q [seq_q, n_q_heads*head_dim],
  * k/v [seq_kv, n_kv_heads*head_dim], out [seq_q, n_q_heads*head_dim]; query i

@@ -55,6 +55,13 @@ void launch_prefill_rope_append(View& qkv_out, int n, View& k_cache, View& v_cac
                                 const float* cos_table, const float* sin_table, int p0,
                                 int n_q_heads, int n_kv_heads, int head_dim, hipStream_t stream);
 
+// Causal attention of a chunk over one sequence's rows of a paged pool (block table
+// d_block_table, device int32 [max_blocks]).
+void launch_paged_prefill_attention(const __half* q, int q_stride, const af_kv_pool& pool,
+                                    int layer, const int32_t* d_block_table, int max_blocks,
+                                    int p0, int n, int kv_len, __half* out, int out_stride,
+                                    int n_q_heads, hipStream_t stream);
+
 // Causal attention of the chunk's n queries (row stride q_stride) over cache rows
 // [0, min(p0 + i + 1, kv_len)) into out (row stride out_stride). head_dim 128.
 void launch_prefill_attention(const __half* q, int q_stride, const View& k_cache,

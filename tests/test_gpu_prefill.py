@@ -243,3 +243,83 @@ def test_paged_chunk_append_whole_blocks(gpu):
     assert np.array_equal(bits(d_qkv.download(np.float16, qkv.shape)), bits(ref))
     assert np.array_equal(bits(slab[0]), bits(ks))
     assert np.array_equal(bits(slab[1]), bits(vs))
+
+
+# ---- paged pool: causal chunk attention through a block table -----------------
+def _paged_pool(bs, nblocks, layers, seed):
+    host = randn_f16((layers, 2, nblocks * bs, KV_DIM), seed)
+    buf = up(host)
+    pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP16, bs, layers, NKV, HD, nblocks)
+    return host, buf, pool
+
+
+@pytest.mark.parametrize("bs,p0,n,kv_len", [(16, 0, 200, 200), (16, 300, 129, 429),
+                                             (32, 1000, 300, 1300), (64, 0, 50, 37)])
+def test_paged_prefill_attention_vs_oracle(gpu, bs, p0, n, kv_len):
+    say(f"paged prefill bs={bs} p0={p0} n={n} kv_len={kv_len}")
+    layers, layer = 2, 1
+    max_blocks = (kv_len + bs - 1) // bs + 1
+    nblocks = max_blocks + 7
+    host, buf, pool = _paged_pool(bs, nblocks, layers, 0xA70F70 + bs + p0)
+    table = rng(bs + n).permutation(nblocks)[:max_blocks].astype(np.int32)
+    q = randn_f16((n, QKV), 0xA70F71 + n)
+    d_o = up(np.full((n, Q_DIM), np.float16(3.0)))
+    kv.launch_paged_prefill_attention(up(q), QKV, pool, layer, up(table), max_blocks, p0, n, kv_len,
+                                      d_o, Q_DIM, NQ)
+    got = d_o.download(np.float16, (n, Q_DIM))
+    kc = oracle.paged_gather(host[layer, 0], table, kv_len, bs, KV_DIM)
+    vc = oracle.paged_gather(host[layer, 1], table, kv_len, bs, KV_DIM)
+    assert_attn_close(got, oracle.prefill_attention_f64(q, kc, vc, p0, n, kv_len, NQ, NKV, HD),
+                      what="vs fp64")
+    assert_attn_close(got, oracle.prefill_attention(q, kc, vc, p0, n, kv_len, NQ, NKV, HD,
+                                                    threads=8), what="vs fp32 oracle")
+
+
+def test_paged_prefill_rejects_bad_arguments(gpu):
+    say("paged prefill argument checks")
+    lib = atomflow_amd.lib()
+    host, buf, pool = _paged_pool(16, 8, 1, 0xA70F72)
+    b = up(np.zeros((8, QKV), np.float16))
+    t = up(np.arange(4, dtype=np.int32))
+    import ctypes
+    args = lambda kv_len, max_blocks=4: (b.ptr, QKV, ctypes.byref(pool), 0, t.ptr, max_blocks, 0,
+                                         4, kv_len, b.ptr, Q_DIM, NQ, None)
+    assert lib.af_paged_prefill_attention(*args(65)) == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    assert lib.af_paged_prefill_attention(*args(0)) == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    assert lib.af_paged_prefill_attention(*args(64)) == atomflow_amd.AF_OK
+    fp8 = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, 16, 1, NKV, HD, 8, up(np.ones(16, np.float32)))
+    assert lib.af_paged_prefill_attention(b.ptr, QKV, ctypes.byref(fp8), 0, t.ptr, 4, 0, 4, 10,
+                                          b.ptr, Q_DIM, NQ, None) == atomflow_amd.AF_ERR_UNSUPPORTED
+
+
+def test_chunked_prefill_into_paged_pool_with_block_manager(gpu):
+    say("BlockManager: two prefill chunks (300, 213 tokens) appended + attended through the pool")
+    bs, nblocks = 16, 64
+    bm = kv.BlockManager(nblocks, bs, 1, NKV, HD, atomflow_amd.AF_KV_FP16, allocate_pool=True)
+    pool = bm.pool()
+    max_seq = 1024
+    c, s, d_c, d_s = rope_tables(max_seq)
+    filler = [bm.seq_create() for _ in range(3)]  # interleave other sequences' blocks
+    seq = bm.seq_create()
+    k_ref = np.zeros((max_seq, KV_DIM), np.float16)
+    v_ref = np.zeros((max_seq, KV_DIM), np.float16)
+    for p0, n in [(0, 300), (300, 213)]:
+        for f in filler:
+            bm.seq_extend(f, 20)
+        r = bm.seq_extend(seq, n)
+        assert not isinstance(r, int), r
+        pos = np.arange(p0, p0 + n, dtype=np.int32)
+        slots = np.array([bm.seq_slot(seq, int(p)) for p in pos], np.int64)
+        qkv = randn_f16((n, QKV), 0xA70F73 + p0)
+        d_qkv = up(qkv)
+        kv.launch_paged_rope_append(d_qkv, n, pool, 0, up(slots), up(pos), d_c, d_s, max_seq, NQ)
+        tables, lens = bm.export_tables([seq], 64)
+        assert lens[0] == p0 + n
+        d_o = up(np.zeros((n, Q_DIM), np.float16))
+        kv.launch_paged_prefill_attention(d_qkv, QKV, pool, 0, up(tables[0]), 64, p0, n, p0 + n,
+                                          d_o, Q_DIM, NQ)
+        ref_qkv = oracle.prefill_rope_append(qkv, k_ref, v_ref, c, s, p0, NQ, NKV, HD)
+        assert np.array_equal(bits(d_qkv.download(np.float16, qkv.shape)), bits(ref_qkv))
+        ref = oracle.prefill_attention_f64(ref_qkv, k_ref, v_ref, p0, n, p0 + n, NQ, NKV, HD)
+        assert_attn_close(d_o.download(np.float16, (n, Q_DIM)), ref, what=f"chunk p0={p0}")
+    bm.close()
