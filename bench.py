@@ -41,6 +41,7 @@ QKV = Q_DIM + 2 * KV_DIM
 HIDDEN = 3072                              # model width: the QKV projection's input
 THETA = 500000.0
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx8k_pmc.txt")
 METRIC = "decode-attn KV-read GB/s (% of 8 TB/s HBM) + us/layer-step at ctx 8k"
 
@@ -59,6 +60,7 @@ def parse():
     ap.add_argument("--ctx", type=int, default=8192, choices=[1024, 8192, 32768])
     ap.add_argument("--splits", type=int, default=0, help="attention split count (0 = library default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
     return ap.parse_args()
@@ -235,9 +237,90 @@ def bench_contiguous(args, dev, kv, lib, info):
                      "traffic": read_traffic() if ctx == 8192 else None},
         "cpu_baseline": None,
     }
+    if not args.no_prefill:
+        log("prefill (one layer) ...")
+        result["prefill"] = bench_prefill(dev, kv, lib, stream, 3, 10)
     if args.calibrate_copy:
         calibrate_copy(dev, kv, stream)
     return result
+
+
+def prefill_flops(p0, n, kv_len):
+    """Algorithmic FLOPs of causal chunk attention: 2 (QK) + 2 (PV) per head_dim
+    element per attended (query, key) pair, over all Q heads."""
+    keys = sum(min(p0 + i + 1, kv_len) for i in range(n))
+    return 4.0 * HD * NQ * keys
+
+
+def bench_prefill(dev, kv, lib, stream, warmup, reps):
+    """One layer of prefill: the ctx-8k prompt as one causal chunk, a 2048-token
+    chunk at p0 = 6144 (contiguous cache and a bs-16 paged pool with a permuted
+    block table), and the 2048-row RoPE + append."""
+    import atomflow_amd
+    e0, e1 = dev.Event(), dev.Event()
+
+    def time_us(fn):
+        for _ in range(warmup):
+            fn()
+        dev.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        e1.sync()
+        return e0.elapsed_ms(e1) * 1e3 / reps
+
+    L = 8192
+    k = dev.DeviceBuffer(L * KV_DIM * 2)
+    v = dev.DeviceBuffer(L * KV_DIM * 2)
+    qkv = dev.DeviceBuffer(L * QKV * 2)
+    out = dev.DeviceBuffer(L * Q_DIM * 2)
+    def randn(b, seed):
+        atomflow_amd.check(lib.af_rt_fill_randn_f16(b.ptr, b.nbytes // 2, seed, 1.0, stream.handle))
+
+    for i, b in enumerate((k, v, qkv)):
+        randn(b, 0xA70F90 + i)
+    full = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, 0, L, L, L, NQ, NKV,
+                                               HD, stream=stream)
+    p0, n = 6144, 2048
+    chunk = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, p0, n, p0 + n, L, NQ,
+                                                NKV, HD, stream=stream)
+    bs = 16
+    nblocks = L // bs
+    pool_buf = dev.DeviceBuffer(2 * nblocks * bs * KV_DIM * 2)
+    randn(pool_buf, 0xA70F93)
+    pool = kv.make_pool(pool_buf, atomflow_amd.AF_KV_FP16, bs, 1, NKV, HD, nblocks)
+    table = dev.DeviceBuffer.from_array(
+        np.random.default_rng(0xA70F94).permutation(nblocks).astype(np.int32))
+    paged = lambda: kv.launch_paged_prefill_attention(qkv, QKV, pool, 0, table, nblocks, p0, n,
+                                                      p0 + n, out, Q_DIM, NQ, stream=stream)
+    cos = dev.DeviceBuffer(L * (HD // 2) * 4)
+    sin = dev.DeviceBuffer(L * (HD // 2) * 4)
+    kv.build_rope_cache(cos, sin, L, HD, THETA)
+    append = lambda: kv.launch_prefill_rope_append(qkv, n, k, v, cos, sin, p0, L, NQ, NKV, HD,
+                                                   stream=stream)
+    us_full, us_chunk, us_paged, us_app = (time_us(f) for f in (full, chunk, paged, append))
+    tf = lambda fl, us: fl / (us * 1e-6) / 1e12
+    f_full, f_chunk = prefill_flops(0, L, L), prefill_flops(p0, n, p0 + n)
+    app_bytes = n * (QKV * 2 * 2 + 2 * KV_DIM * 2)  # qkv rows read + written, K/V rows written
+    res = {
+        "workload": "one layer, 24 Q / 8 KV heads x 128, fp16: 8192-token prompt as one causal "
+                    "chunk; 2048-token chunk at p0 6144 (contiguous, and paged bs 16 with a "
+                    "permuted block table); 2048-row RoPE + append",
+        "attn_8k_us": round(us_full, 1), "attn_8k_tflops": round(tf(f_full, us_full), 1),
+        "chunk_2k_at_6k_us": round(us_chunk, 1),
+        "chunk_2k_at_6k_tflops": round(tf(f_chunk, us_chunk), 1),
+        "paged_chunk_2k_at_6k_us": round(us_paged, 1),
+        "paged_chunk_2k_at_6k_tflops": round(tf(f_chunk, us_paged), 1),
+        "rope_append_2k_us": round(us_app, 2),
+        "rope_append_2k_gbs": round(app_bytes / (us_app * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tf(f_full, us_full), 1),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf(f_full, us_full) / MFMA_F16_PEAK_TFLOPS, 4)},
+    }
+    for b in (k, v, qkv, out, pool_buf, table, cos, sin):
+        b.free()
+    return res
 
 
 def bench_paged(args, dev, kv, lib, info):
