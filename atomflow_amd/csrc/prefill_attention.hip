@@ -36,7 +36,9 @@
 //    tiles skip both the tile max and the O^T rescale. The row sum is taken over
 //    the fp16 probabilities the P.V product uses.
 //  * Paged pools (PAGED): tile rows map through the sequence's block table; the
-//    entries for tile kt+1 are fetched during tile kt-1.
+//    entries for tile kt+1 are fetched during tile kt-1. FP8 pools (FP8) stage
+//    tiles through registers and convert E4M3 -> fp16 exactly on the way into
+//    LDS; the K scale joins the score scale and the V scale the output.
 //  * Workgroups are ordered KV head fastest (consecutive workgroups alternate
 //    XCDs, so each XCD's L2 serves one KV head when n_kv_heads divides 8), then
 //    Q head, then query tile heaviest first; waves skip key tiles that lie wholly
@@ -82,6 +84,9 @@ struct PrefillArgs {
     // logical row t lives in slot table[t >> bs_log2] * block_size + t % block_size.
     const int32_t* table;
     int32_t bs_log2;
+    // FP8 pools: this layer's fp32 scales [2][n_kv_heads] (K, V); the slabs hold
+    // E4M3 codes (one byte per element).
+    const float* scales;
 };
 
 // Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
@@ -138,6 +143,53 @@ __device__ __forceinline__ void tile_blocks(const int32_t* table, int bs_log2, i
     }
 }
 
+// FP8 pools: tile rows go through registers, 32 codes of K and of V per thread
+// (row tid/4, elements 32*(tid%4) ..), converted to fp16 exactly (E4M3 -> fp16,
+// unit scale) after the current tile's matrix work and stored in the same
+// swizzled layout as the DMA path. The K/V scales are applied to the scores and
+// the output instead.
+struct Fp8Tile {
+    uint4 k0, k1, v0, v1;
+};
+
+template <bool PAGED>
+__device__ __forceinline__ void fp8_load(const char* kb, const char* vb, uint32_t row_bytes,
+                                         int key0, int kv_len, int tid, int blk, int bs_log2,
+                                         Fp8Tile& t) {
+    const int key = min(key0 + (tid >> 2), kv_len - 1);
+    const int64_t slot =
+        PAGED ? ((int64_t(blk) << bs_log2) | (key & ((1 << bs_log2) - 1))) : int64_t(key);
+    const size_t off = size_t(slot) * row_bytes + 32 * (tid & 3);
+    t.k0 = *reinterpret_cast<const uint4*>(kb + off);
+    t.k1 = *reinterpret_cast<const uint4*>(kb + off + 16);
+    t.v0 = *reinterpret_cast<const uint4*>(vb + off);
+    t.v1 = *reinterpret_cast<const uint4*>(vb + off + 16);
+}
+
+// Eight E4M3 codes (two words) -> eight fp16 values.
+__device__ __forceinline__ uint4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    uint4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w0), 1.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w0), 1.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w1), 1.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w1), 1.0f, true));
+    return r;
+}
+
+__device__ __forceinline__ void fp8_store(char* ks, char* vs, int tid, const Fp8Tile& t) {
+    const int row = tid >> 2, q = tid & 3;
+    // chunk 4q + c holds elements 32q + 8c .. +7
+    *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 0)) = e4m3x8_to_f16(t.k0.x, t.k0.y);
+    *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 1)) = e4m3x8_to_f16(t.k0.z, t.k0.w);
+    *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 2)) = e4m3x8_to_f16(t.k1.x, t.k1.y);
+    *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 3)) = e4m3x8_to_f16(t.k1.z, t.k1.w);
+    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 0)) = e4m3x8_to_f16(t.v0.x, t.v0.y);
+    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 1)) = e4m3x8_to_f16(t.v0.z, t.v0.w);
+    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 2)) = e4m3x8_to_f16(t.v1.x, t.v1.y);
+    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 3)) = e4m3x8_to_f16(t.v1.z, t.v1.w);
+}
+
 __device__ __forceinline__ half8 lds_half8(const char* p) {
     return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
 }
@@ -185,7 +237,7 @@ __device__ __forceinline__ float dot2_sum(const half8& h, float acc) {
 // LDS: K tiles at [0, 2*kTileBytes), V tiles after them.
 constexpr int kVBase = 2 * kTileBytes;
 
-template <int QB, bool PAGED>
+template <int QB, bool PAGED, bool FP8>
 __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention_kernel(
     const PrefillArgs a) {
     constexpr int kQueries = 32 * QB * kPfWaves;  // per workgroup
@@ -227,17 +279,28 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
     // Keep the query loads ahead of the tile loads: the prologue's wait for the
     // tile then covers them, and the loop never waits on a query register.
     asm volatile("" ::: "memory");
-    const char* kb = reinterpret_cast<const char*>(a.k + size_t(kvh) * kPfHd);
-    const char* vb = reinterpret_cast<const char*>(a.v + size_t(kvh) * kPfHd);
+    constexpr int kElem = FP8 ? 1 : 2;
+    const char* kb = reinterpret_cast<const char*>(a.k) + size_t(kvh) * kPfHd * kElem;
+    const char* vb = reinterpret_cast<const char*>(a.v) + size_t(kvh) * kPfHd * kElem;
     // Paged: the block-table entries of tile kt+1 are loaded one step ahead, so
     // the wait for tile kt's data also covers them.
     int blk[4] = {0, 0, 0, 0};
-    if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, 0, a.kv_len, wave, lane, blk);
-    dma_tile<true, PAGED>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds, blk, a.bs_log2);
-    dma_tile<false, PAGED>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase, blk,
-                           a.bs_log2);
-    if constexpr (PAGED)
-        if (n_kt > 1) tile_blocks(a.table, a.bs_log2, 1, a.kv_len, wave, lane, blk);
+    int blk8 = 0;  // FP8: this thread's row's block for the next tile
+    Fp8Tile f8;
+    if constexpr (FP8) {
+        if constexpr (PAGED) blk8 = a.table[min(tid >> 2, a.kv_len - 1) >> a.bs_log2];
+        fp8_load<PAGED>(kb, vb, a.kv_row_bytes, 0, a.kv_len, tid, blk8, a.bs_log2, f8);
+        fp8_store(s_lds, s_lds + kVBase, tid, f8);
+        if constexpr (PAGED)
+            if (n_kt > 1) blk8 = a.table[min(kPfKeys + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
+    } else {
+        if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, 0, a.kv_len, wave, lane, blk);
+        dma_tile<true, PAGED>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds, blk, a.bs_log2);
+        dma_tile<false, PAGED>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase, blk,
+                               a.bs_log2);
+        if constexpr (PAGED)
+            if (n_kt > 1) tile_blocks(a.table, a.bs_log2, 1, a.kv_len, wave, lane, blk);
+    }
 
     // Per-lane LDS operand offsets; the buffer, the key block and the key step
     // are added as immediates.
@@ -270,7 +333,9 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         m_run[b] = kPfEmptyMax;
         l_run[b] = 0.0f;
     }
-    const float sc = a.scale_log2;
+    // FP8: scores carry the K scale, the output the V scale.
+    const float sc = FP8 ? a.scale_log2 * a.scales[kvh] : a.scale_log2;
+    const float v_scale = FP8 ? a.scales[a.n_kv_heads + kvh] : 1.0f;
 
     auto step = [&](int kt, auto buf_c) {
         constexpr int BUF = decltype(buf_c)::value;
@@ -279,12 +344,23 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (kt + 1 < n_kt) {
-            dma_tile<true, PAGED>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
-                                  s_lds + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
-            dma_tile<false, PAGED>(vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
-                                   s_lds + kVBase + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
-            if constexpr (PAGED)
-                if (kt + 2 < n_kt) tile_blocks(a.table, a.bs_log2, kt + 2, a.kv_len, wave, lane, blk);
+            if constexpr (FP8) {
+                fp8_load<PAGED>(kb, vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, tid, blk8,
+                                a.bs_log2, f8);
+                if constexpr (PAGED)
+                    if (kt + 2 < n_kt)
+                        blk8 = a.table[min((kt + 2) * kPfKeys + (tid >> 2), a.kv_len - 1) >>
+                                       a.bs_log2];
+            } else {
+                dma_tile<true, PAGED>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
+                                      s_lds + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
+                dma_tile<false, PAGED>(vb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave,
+                                       lane, s_lds + kVBase + (BUF ^ 1) * kTileBytes, blk,
+                                       a.bs_log2);
+                if constexpr (PAGED)
+                    if (kt + 2 < n_kt)
+                        tile_blocks(a.table, a.bs_log2, kt + 2, a.kv_len, wave, lane, blk);
+            }
         }
         const int key0 = kt * kPfKeys;
         const char* ks = s_lds + BUF * kTileBytes;
@@ -361,6 +437,10 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
                                                                           0, 0, 0);
                 }
         }
+        if constexpr (FP8)
+            if (kt + 1 < n_kt)
+                fp8_store(s_lds + (BUF ^ 1) * kTileBytes, s_lds + kVBase + (BUF ^ 1) * kTileBytes,
+                          tid, f8);
     };
     int kt = 0;
     for (; kt + 2 <= n_kt; kt += 2) {
@@ -373,7 +453,7 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
 #pragma unroll
     for (int b = 0; b < QB; ++b) {
         const int qi = wq0 + 32 * b + col;
-        const float inv = 1.0f / halves_sum(l_run[b]);
+        const float inv = v_scale / halves_sum(l_run[b]);
         if (qi >= a.n) continue;
         uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
 #pragma unroll
@@ -397,12 +477,13 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // MFMA but leave one wave per SIMD with its softmax exposed; measured slower.)
 int launch_prefill(PrefillArgs a, hipStream_t stream) {
     a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
-    if (a.table)
-        hipLaunchKernelGGL((prefill_attention_kernel<1, true>), dim3(a.n_tiles * a.n_q_heads),
-                           dim3(kPfThreads), 0, stream, a);
+    const dim3 grid(a.n_tiles * a.n_q_heads), block(kPfThreads);
+    if (a.scales)
+        hipLaunchKernelGGL((prefill_attention_kernel<1, true, true>), grid, block, 0, stream, a);
+    else if (a.table)
+        hipLaunchKernelGGL((prefill_attention_kernel<1, true, false>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((prefill_attention_kernel<1, false>), dim3(a.n_tiles * a.n_q_heads),
-                           dim3(kPfThreads), 0, stream, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<1, false, false>), grid, block, 0, stream, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -458,7 +539,9 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
         n_q_heads % pool->n_kv_heads)
         return AF_ERR_INVALID_ARG;
-    if (pool->dtype != AF_KV_FP16 || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
+    const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
+    if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
+    if (fp8 && !pool->scales) return AF_ERR_INVALID_ARG;
     const int bs = pool->block_size;
     if (bs < 8 || (bs & (bs - 1))) return AF_ERR_INVALID_ARG;
     const int q_dim = n_q_heads * kPfHd;
@@ -468,15 +551,17 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
     if (n == 0) return AF_OK;
     if (kv_len <= 0 || int64_t(kv_len) > int64_t(max_blocks) * bs) return AF_ERR_OUT_OF_RANGE;
     const int64_t kv_stride = int64_t(pool->n_kv_heads) * kPfHd;
-    const size_t slab = size_t(pool->total_blocks) * bs * kv_stride;  // elements
-    const uint16_t* base = static_cast<const uint16_t*>(pool->base);
+    const size_t esz = fp8 ? 1 : 2;
+    const size_t slab = size_t(pool->total_blocks) * bs * kv_stride * esz;  // bytes
+    const char* base = static_cast<const char*>(pool->base);
     PrefillArgs a{};
     a.q = static_cast<const uint16_t*>(q);
     a.q_stride = q_stride;
-    a.k = base + size_t(2 * layer) * slab;
-    a.v = a.k + slab;
+    a.k = reinterpret_cast<const uint16_t*>(base + size_t(2 * layer) * slab);
+    a.v = reinterpret_cast<const uint16_t*>(base + size_t(2 * layer + 1) * slab);
     a.kv_stride = kv_stride;
-    a.kv_row_bytes = uint32_t(kv_stride * 2);
+    a.kv_row_bytes = uint32_t(kv_stride * esz);
+    a.scales = fp8 ? pool->scales + size_t(layer) * 2 * pool->n_kv_heads : nullptr;
     a.out = static_cast<uint16_t*>(out);
     a.out_stride = out_stride;
     a.p0 = p0;

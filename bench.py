@@ -294,31 +294,41 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
         np.random.default_rng(0xA70F94).permutation(nblocks).astype(np.int32))
     paged = lambda: kv.launch_paged_prefill_attention(qkv, QKV, pool, 0, table, nblocks, p0, n,
                                                       p0 + n, out, Q_DIM, NQ, stream=stream)
+    pool8_buf = dev.DeviceBuffer(2 * nblocks * bs * KV_DIM)
+    atomflow_amd.check(lib.af_rt_fill_randn_fp8(pool8_buf.ptr, pool8_buf.nbytes, 0xA70F95, 20.0,
+                                                stream.handle))
+    scales8 = dev.DeviceBuffer.from_array(np.full(2 * NKV, 0.05, np.float32))
+    pool8 = kv.make_pool(pool8_buf, atomflow_amd.AF_KV_FP8_E4M3, bs, 1, NKV, HD, nblocks, scales8)
+    paged8 = lambda: kv.launch_paged_prefill_attention(qkv, QKV, pool8, 0, table, nblocks, p0, n,
+                                                       p0 + n, out, Q_DIM, NQ, stream=stream)
     cos = dev.DeviceBuffer(L * (HD // 2) * 4)
     sin = dev.DeviceBuffer(L * (HD // 2) * 4)
     kv.build_rope_cache(cos, sin, L, HD, THETA)
     append = lambda: kv.launch_prefill_rope_append(qkv, n, k, v, cos, sin, p0, L, NQ, NKV, HD,
                                                    stream=stream)
-    us_full, us_chunk, us_paged, us_app = (time_us(f) for f in (full, chunk, paged, append))
+    us_full, us_chunk, us_paged, us_paged8, us_app = (
+        time_us(f) for f in (full, chunk, paged, paged8, append))
     tf = lambda fl, us: fl / (us * 1e-6) / 1e12
     f_full, f_chunk = prefill_flops(0, L, L), prefill_flops(p0, n, p0 + n)
     app_bytes = n * (QKV * 2 * 2 + 2 * KV_DIM * 2)  # qkv rows read + written, K/V rows written
     res = {
         "workload": "one layer, 24 Q / 8 KV heads x 128, fp16: 8192-token prompt as one causal "
-                    "chunk; 2048-token chunk at p0 6144 (contiguous, and paged bs 16 with a "
-                    "permuted block table); 2048-row RoPE + append",
+                    "chunk; 2048-token chunk at p0 6144 (contiguous, paged bs 16 with a "
+                    "permuted block table, fp16 and FP8-E4M3 pools); 2048-row RoPE + append",
         "attn_8k_us": round(us_full, 1), "attn_8k_tflops": round(tf(f_full, us_full), 1),
         "chunk_2k_at_6k_us": round(us_chunk, 1),
         "chunk_2k_at_6k_tflops": round(tf(f_chunk, us_chunk), 1),
         "paged_chunk_2k_at_6k_us": round(us_paged, 1),
         "paged_chunk_2k_at_6k_tflops": round(tf(f_chunk, us_paged), 1),
+        "paged_fp8_chunk_2k_at_6k_us": round(us_paged8, 1),
+        "paged_fp8_chunk_2k_at_6k_tflops": round(tf(f_chunk, us_paged8), 1),
         "rope_append_2k_us": round(us_app, 2),
         "rope_append_2k_gbs": round(app_bytes / (us_app * 1e-6) / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(tf(f_full, us_full), 1),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf(f_full, us_full) / MFMA_F16_PEAK_TFLOPS, 4)},
     }
-    for b in (k, v, qkv, out, pool_buf, table, cos, sin):
+    for b in (k, v, qkv, out, pool_buf, pool8_buf, scales8, table, cos, sin):
         b.free()
     return res
 

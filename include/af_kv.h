@@ -271,8 +271,10 @@ int af_prefill_attention(const void* q, int q_stride, const void* k_cache, const
  * `layer` is read through d_block_table (device int32 [max_blocks]), slot
  * d_block_table[t / block_size] * block_size + t % block_size. Chunked prefill
  * (src/experimental/server_arch roadmap, README.md:269): append the chunk with
- * af_paged_rope_append (one slot per token), then this. FP16 pools with
- * head_dim 128 (else AF_ERR_UNSUPPORTED); kv_len <= max_blocks * block_size. */
+ * af_paged_rope_append (one slot per token), then this. FP16 or FP8-E4M3 pools
+ * (FP8: codes convert to fp16 exactly, the layer's K scale multiplies the scores
+ * and its V scale the output), head_dim 128 (else AF_ERR_UNSUPPORTED);
+ * kv_len <= max_blocks * block_size. */
 int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
                                const int32_t* d_block_table, int max_blocks, int p0, int n,
                                int kv_len, void* out, int out_stride, int n_q_heads,

@@ -287,8 +287,11 @@ def test_paged_prefill_rejects_bad_arguments(gpu):
     assert lib.af_paged_prefill_attention(*args(65)) == atomflow_amd.AF_ERR_OUT_OF_RANGE
     assert lib.af_paged_prefill_attention(*args(0)) == atomflow_amd.AF_ERR_OUT_OF_RANGE
     assert lib.af_paged_prefill_attention(*args(64)) == atomflow_amd.AF_OK
-    fp8 = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, 16, 1, NKV, HD, 8, up(np.ones(16, np.float32)))
+    fp8 = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, 16, 1, NKV, HD, 8)  # no scales
     assert lib.af_paged_prefill_attention(b.ptr, QKV, ctypes.byref(fp8), 0, t.ptr, 4, 0, 4, 10,
+                                          b.ptr, Q_DIM, NQ, None) == atomflow_amd.AF_ERR_INVALID_ARG
+    hd64 = kv.make_pool(buf, atomflow_amd.AF_KV_FP16, 16, 1, NKV, 64, 8)
+    assert lib.af_paged_prefill_attention(b.ptr, QKV, ctypes.byref(hd64), 0, t.ptr, 4, 0, 4, 10,
                                           b.ptr, Q_DIM, NQ, None) == atomflow_amd.AF_ERR_UNSUPPORTED
 
 
@@ -323,3 +326,48 @@ def test_chunked_prefill_into_paged_pool_with_block_manager(gpu):
         ref = oracle.prefill_attention_f64(ref_qkv, k_ref, v_ref, p0, n, p0 + n, NQ, NKV, HD)
         assert_attn_close(d_o.download(np.float16, (n, Q_DIM)), ref, what=f"chunk p0={p0}")
     bm.close()
+
+
+@pytest.mark.parametrize("bs,p0,n,kv_len", [(32, 0, 150, 150), (16, 700, 200, 900)])
+def test_paged_prefill_attention_fp8_pool(gpu, bs, p0, n, kv_len):
+    """FP8-E4M3 pool with per-(layer, K/V, KV-head) fp32 scales: every row against the
+    FP8 decode oracle over min(p0+i+1, kv_len) rows (ok_paged_attention_fp8), and
+    sampled rows against a float64 numpy dequantise + softmax."""
+    say(f"paged prefill fp8 bs={bs} p0={p0} n={n} kv_len={kv_len}")
+    from inputs import ATOL_FP8, RTOL_FP8
+    layers, layer = 2, 1
+    max_blocks = (kv_len + bs - 1) // bs
+    nblocks = max_blocks + 5
+    r = rng(0xA70F75 + bs)
+    host = r.integers(0, 256, (layers, 2, nblocks * bs, KV_DIM), dtype=np.uint8)
+    host[(host & 0x7F) == 0x7F] = 0  # no NaN codes
+    scales = r.uniform(0.004, 0.02, (layers, 2, NKV)).astype(np.float32)
+    buf = up(host)
+    pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, up(scales))
+    table = r.permutation(nblocks)[:max_blocks].astype(np.int32)
+    q = randn_f16((n, QKV), 0xA70F76 + n)
+    d_o = up(np.zeros((n, Q_DIM), np.float16))
+    kv.launch_paged_prefill_attention(up(q), QKV, pool, layer, up(table), max_blocks, p0, n,
+                                      kv_len, d_o, Q_DIM, NQ)
+    got = d_o.download(np.float16, (n, Q_DIM))
+    ks, vs = scales[layer, 0], scales[layer, 1]
+    for i in range(n):
+        L = min(p0 + i + 1, kv_len)
+        ref = oracle.paged_attention_fp8(q[i, :Q_DIM], host[layer, 0], host[layer, 1], ks, vs,
+                                         table, L, bs, NQ, NKV, HD)
+        assert_attn_close(got[i], ref, ATOL_FP8, RTOL_FP8, what=f"row {i}")
+    lut = oracle.e4m3_decode_table().astype(np.float64)
+    kc = oracle.paged_gather(host[layer, 0], table, kv_len, bs, KV_DIM)
+    vc = oracle.paged_gather(host[layer, 1], table, kv_len, bs, KV_DIM)
+    kf = lut[kc].reshape(kv_len, NKV, HD) * ks[None, :, None]
+    vf = lut[vc].reshape(kv_len, NKV, HD) * vs[None, :, None]
+    for i in sorted({0, n // 2, n - 1}):
+        L = min(p0 + i + 1, kv_len)
+        qi = q[i, :Q_DIM].astype(np.float64).reshape(NQ, HD)
+        out = np.empty((NQ, HD))
+        for h in range(NQ):
+            g = h * NKV // NQ
+            sc = kf[:L, g] @ qi[h] / np.sqrt(HD)
+            p = np.exp(sc - sc.max())
+            out[h] = p @ vf[:L, g] / p.sum()
+        assert_attn_close(got[i], out.ravel(), ATOL_FP8, RTOL_FP8, what=f"row {i} vs float64")
