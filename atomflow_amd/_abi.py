@@ -60,6 +60,14 @@ PROTOTYPES = {
     "af_prefill_attention": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, P]),
     "af_tiled_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
     "af_paged_prefill_attention": (I, [P, I, P, I, P, I, I, I, I, P, I, I, P]),
+    "af_sched_create": (I, [P, I, I, I, I, P]),
+    "af_sched_destroy": (I, [P]),
+    "af_sched_add_request": (I, [P, I64, I, I]),
+    "af_sched_step": (I, [P, P]),
+    "af_sched_plan_decode": (I, [P, P, P, P, P]),
+    "af_sched_plan_prefill": (I, [P, P, P, P, P]),
+    "af_sched_plan_copies": (I, [P, P]),
+    "af_sched_plan_events": (I, [P, P, P]),
     "af_bm_create": (I, [I, I, I, I, I, I, I, ctypes.POINTER(P)]),
     "af_bm_destroy": (I, [P]),
     "af_bm_attach_pool": (I, [P, P, P]),

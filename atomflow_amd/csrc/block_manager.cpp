@@ -284,6 +284,10 @@ struct af_block_manager {
     BlockManager bm;
 };
 
+namespace atomflow::server {
+BlockManager* block_manager_of(af_block_manager* h) { return h ? &h->bm : nullptr; }
+}  // namespace atomflow::server
+
 extern "C" int af_bm_create(int total_blocks, int block_size, int n_layers, int n_kv_heads,
                             int head_dim, int dtype, int allocate_pool, af_block_manager** out) {
     if (!out) return AF_ERR_INVALID_ARG;

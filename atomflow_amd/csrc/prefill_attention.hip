@@ -168,7 +168,6 @@ __device__ __forceinline__ void fp8_load(const char* kb, const char* vb, uint32_
 
 // Eight E4M3 codes (two words) -> eight fp16 values.
 __device__ __forceinline__ uint4 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
-    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     uint4 r;
     r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w0), 1.0f, false));
     r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(w0), 1.0f, true));

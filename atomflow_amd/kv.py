@@ -333,6 +333,66 @@ class BlockManager:
         return tables, lens
 
 
+class Scheduler:
+    """Continuous-batching scheduler (af_sched_*) over a BlockManager.
+
+    ``step()`` returns the plan as a dict: finished / preempted request ids,
+    decode [(request, seq, slot, position)], copies [(src, dst, rows)], prefill
+    [(request, seq, p0, n, last, slots)], and the running / waiting counts.
+    """
+
+    def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0):
+        h = ctypes.c_void_p()
+        check(lib().af_sched_create(bm.h, max_running, max_step_tokens, prefill_chunk, watermark,
+                                    ctypes.byref(h)), "af_sched_create")
+        self.h = h.value
+        self.bm = bm  # keeps the manager alive
+
+    def close(self):
+        if self.h:
+            lib().af_sched_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def add_request(self, rid, prompt_len, max_new_tokens):
+        return lib().af_sched_add_request(self.h, rid, prompt_len, max_new_tokens) == 0
+
+    def step(self):
+        c = np.zeros(8, np.int32)
+        check(lib().af_sched_step(self.h, c.ctypes.data), "af_sched_step")
+        nd, nc, nt, ncp, nf, npre, nrun, nwait = (int(x) for x in c)
+        dreq, dseq = np.zeros(nd, np.int64), np.zeros(nd, np.int32)
+        dslot, dpos = np.zeros(nd, np.int64), np.zeros(nd, np.int32)
+        lib().af_sched_plan_decode(self.h, dreq.ctypes.data, dseq.ctypes.data, dslot.ctypes.data,
+                                   dpos.ctypes.data)
+        preq, chunks = np.zeros(nc, np.int64), np.zeros((nc, 5), np.int32)
+        pslot, ppos = np.zeros(nt, np.int64), np.zeros(nt, np.int32)
+        lib().af_sched_plan_prefill(self.h, preq.ctypes.data, chunks.ctypes.data,
+                                    pslot.ctypes.data, ppos.ctypes.data)
+        copies = np.zeros((ncp, 3), np.int32)
+        lib().af_sched_plan_copies(self.h, copies.ctypes.data)
+        fin, pre = np.zeros(nf, np.int64), np.zeros(npre, np.int64)
+        lib().af_sched_plan_events(self.h, fin.ctypes.data, pre.ctypes.data)
+        prefill = []
+        for i in range(nc):
+            seq, p0, n, off, last = (int(x) for x in chunks[i])
+            prefill.append((int(preq[i]), seq, p0, n, bool(last), [int(x) for x in pslot[off:off + n]]))
+        return {
+            "finished": [int(x) for x in fin], "preempted": [int(x) for x in pre],
+            "decode": [(int(dreq[i]), int(dseq[i]), int(dslot[i]), int(dpos[i])) for i in range(nd)],
+            "copies": [tuple(int(x) for x in row) for row in copies],
+            "prefill": prefill, "running": nrun, "waiting": nwait,
+            "arrays": {"decode_seqs": dseq, "decode_slots": dslot, "decode_positions": dpos,
+                       "prefill_slots": pslot, "prefill_positions": ppos, "copies": copies,
+                       "chunks": chunks},
+        }
+
+
 def _nonneg(r, what):
     if r < 0:
         raise AfError(r, what)
@@ -345,7 +405,7 @@ __all__ = [
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
     "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
     "launch_w8a16_gemv", "launch_prefill_rope_append", "launch_prefill_attention",
-    "launch_tiled_attention_kernel", "launch_paged_prefill_attention",
+    "launch_tiled_attention_kernel", "launch_paged_prefill_attention", "Scheduler",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

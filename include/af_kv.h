@@ -350,6 +350,38 @@ int af_bm_plan_decode(af_block_manager* bm, const int32_t* seqs, int n, int64_t*
 int af_bm_export_tables(const af_block_manager* bm, const int32_t* seqs, int n, int32_t* tables,
                         int max_blocks, int32_t* seq_lens);
 
+/* ======================================================================== */
+/* b3. Continuous-batching scheduler (ServerEngine::step)                    */
+/* ======================================================================== */
+/* Fills in the stub ServerEngine::step (src/experimental/server_arch/
+ * server_engine.cu:55-68, server_engine.h:46-50: dequeue requests, build a
+ * micro-batch, resolve PageTables for the batched attention, advance and retire)
+ * over an af_block_manager; rules in include/server/scheduler.h. A step's plan is
+ * read back with the af_sched_plan_* calls until the next af_sched_step. */
+typedef struct af_scheduler af_scheduler;
+
+/* max_step_tokens >= max_running >= 1, prefill_chunk >= 1, watermark >= 0. */
+int af_sched_create(af_block_manager* bm, int max_running, int max_step_tokens,
+                    int prefill_chunk, int watermark_blocks, af_scheduler** out);
+int af_sched_destroy(af_scheduler* s);
+/* FIFO; AF_ERR_INVALID_ARG if the request could never fit the pool alone. */
+int af_sched_add_request(af_scheduler* s, int64_t id, int prompt_len, int max_new_tokens);
+/* Plans one step. counts (optional, int32[8]): decode sequences, prefill chunks,
+ * prefill tokens, CoW copies, finished, preempted, running, waiting. */
+int af_sched_step(af_scheduler* s, int32_t* counts);
+/* Decode batch: request ids, sequence ids, slots, positions (the new token's
+ * position; it attends position + 1 rows). Any pointer may be NULL. */
+int af_sched_plan_decode(const af_scheduler* s, int64_t* requests, int32_t* seqs, int64_t* slots,
+                         int32_t* positions);
+/* Prefill chunks: requests[i], chunks[5i..5i+4] = (seq, p0, n, offset, last);
+ * slots / positions of every chunk token, chunk i at [offset, offset + n). */
+int af_sched_plan_prefill(const af_scheduler* s, int64_t* requests, int32_t* chunks,
+                          int64_t* slots, int32_t* positions);
+/* CoW copies (src, dst, rows) to run (af_kv_copy_blocks) before the step's appends. */
+int af_sched_plan_copies(const af_scheduler* s, int32_t* copies);
+/* Requests retired at the start of the step, and requests preempted by it. */
+int af_sched_plan_events(const af_scheduler* s, int64_t* finished, int64_t* preempted);
+
 #ifdef __cplusplus
 }
 #endif

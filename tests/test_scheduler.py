@@ -1,0 +1,121 @@
+"""Continuous-batching scheduler (af_sched_*): the C++ Scheduler against the
+Python model of its rules (oracle/sched_model.py) decision for decision on
+random request traces, plus the invariants the rules promise."""
+import numpy as np
+import pytest
+
+import atomflow_amd
+from atomflow_amd import kv
+from oracle.block_model import BlockModel
+from oracle.sched_model import SchedModel
+
+
+def _same(a, b, step):
+    for key in ("finished", "preempted", "decode", "copies"):
+        assert [tuple(x) if isinstance(x, (list, tuple)) else x for x in a[key]] == \
+               [tuple(x) if isinstance(x, (list, tuple)) else x for x in b[key]], (step, key)
+    assert len(a["prefill"]) == len(b["prefill"]), step
+    for x, y in zip(a["prefill"], b["prefill"]):
+        assert tuple(x[:5]) == tuple(y[:5]) and list(x[5]) == list(y[5]), (step, x[:5], y[:5])
+
+
+def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, watermark, n_req,
+              max_prompt, max_new, arrivals_per_step):
+    r = np.random.default_rng(seed)
+    bm = kv.BlockManager(total_blocks, bs, 1, 8, 128)
+    sched = kv.Scheduler(bm, max_running, max_step_tokens, chunk, watermark)
+    model = SchedModel(BlockModel(total_blocks, bs), max_running, max_step_tokens, chunk,
+                       watermark)
+    reqs = [(i, int(r.integers(1, max_prompt + 1)), int(r.integers(1, max_new + 1)))
+            for i in range(n_req)]
+    generated = {rid: 0 for rid, _, _ in reqs}
+    finished = []
+    pending = list(reqs)
+    steps = 0
+    while pending or not model.idle():
+        for _ in range(int(r.integers(0, arrivals_per_step + 1))):
+            if pending:
+                rid, pl, mn = pending.pop(0)
+                assert sched.add_request(rid, pl, mn) == model.add_request(rid, pl, mn)
+        a = sched.step()
+        b = model.step()
+        _same(a, b, steps)
+        # invariants
+        toks = len(a["decode"]) + sum(c[3] for c in a["prefill"])
+        assert toks <= max_step_tokens
+        assert a["running"] <= max_running
+        for rid, seq, slot, pos in a["decode"]:
+            generated[rid] += 1
+        for rid, seq, p0, n, last, slots in a["prefill"]:
+            assert len(slots) == n
+            if last:
+                generated[rid] += 1
+        finished += a["finished"]
+        steps += 1
+        assert steps < 20000, "no progress"
+    assert sorted(finished) == sorted(rid for rid, _, _ in reqs)
+    for rid, pl, mn in reqs:
+        assert generated[rid] == mn, (rid, generated[rid], mn)
+    assert bm.num_free_blocks() == total_blocks
+    sched.close()
+    bm.close()
+    return steps
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_scheduler_matches_model_roomy_pool(seed):
+    run_trace(seed, total_blocks=400, bs=16, max_running=16, max_step_tokens=256, chunk=64,
+              watermark=4, n_req=40, max_prompt=300, max_new=40, arrivals_per_step=3)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_scheduler_matches_model_tight_pool_with_preemption(seed):
+    """A pool far smaller than the offered load: decode preemption (recompute),
+    prefill stalls and the liveness rule all fire."""
+    run_trace(100 + seed, total_blocks=40, bs=16, max_running=8, max_step_tokens=64, chunk=32,
+              watermark=0, n_req=30, max_prompt=200, max_new=120, arrivals_per_step=4)
+
+
+def test_scheduler_preempts_in_tight_pool():
+    bm = kv.BlockManager(12, 16, 1, 8, 128)
+    s = kv.Scheduler(bm, 4, 64, 64, 0)
+    for i in range(3):
+        assert s.add_request(i, 60, 100)
+    preempted = 0
+    for _ in range(400):
+        p = s.step()
+        preempted += len(p["preempted"])
+        if p["running"] == 0 and p["waiting"] == 0:
+            break
+    assert preempted > 0 and bm.num_free_blocks() == 12
+
+
+def test_scheduler_rejects_requests_that_cannot_fit():
+    bm = kv.BlockManager(10, 16, 1, 8, 128)
+    s = kv.Scheduler(bm, 4, 64, 32)
+    assert not s.add_request(1, 150, 20)   # 170 tokens > 160 rows
+    assert s.add_request(2, 150, 10)
+    assert not s.add_request(3, 0, 5)
+    assert not s.add_request(4, 5, 0)
+    lib = atomflow_amd.lib()
+    import ctypes
+    h = ctypes.c_void_p()
+    assert lib.af_sched_create(bm.h, 8, 4, 32, 0, ctypes.byref(h)) == atomflow_amd.AF_ERR_INVALID_ARG
+
+
+def test_scheduler_chunking_budget_and_fifo():
+    """Prompts are split into prefill_chunk pieces, the step budget caps decode +
+    prefill tokens, and requests are admitted in arrival order."""
+    bm = kv.BlockManager(200, 16, 1, 8, 128)
+    s = kv.Scheduler(bm, 4, 48, 32)
+    for i, pl in enumerate([70, 10, 10]):
+        s.add_request(i, pl, 3)
+    p = s.step()  # 32 + 10 + the 6 tokens of budget left
+    assert [(c[0], c[2], c[3]) for c in p["prefill"]] == [(0, 0, 32), (1, 0, 10), (2, 0, 6)]
+    assert [c[4] for c in p["prefill"]] == [False, True, False]
+    p = s.step()  # request 1 decodes at position 10; 0 and 2 continue in admission order
+    assert [(d[0], d[3]) for d in p["decode"]] == [(1, 10)]
+    assert [(c[0], c[2], c[3]) for c in p["prefill"]] == [(0, 32, 32), (2, 6, 4)]
+    p = s.step()  # 1 and 2 decode; 0 gets its last 6 prompt tokens
+    assert [(d[0], d[3]) for d in p["decode"]] == [(1, 11), (2, 10)]
+    assert [(c[0], c[2], c[3], c[4]) for c in p["prefill"]] == [(0, 64, 6, True)]
