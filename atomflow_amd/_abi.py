@@ -60,6 +60,8 @@ PROTOTYPES = {
     "af_prefill_attention": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, P]),
     "af_tiled_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
     "af_paged_prefill_attention": (I, [P, I, P, I, P, I, I, I, I, P, I, I, P]),
+    "af_paged_prefill_attention_batched": (I, [P, I, P, I, P, I, P, P, I, P, I, I, P]),
+    "af_prefill_tile_map": (I, [P, I, P, I]),
     "af_sched_create": (I, [P, I, I, I, I, P]),
     "af_sched_destroy": (I, [P]),
     "af_sched_add_request": (I, [P, I64, I, I]),

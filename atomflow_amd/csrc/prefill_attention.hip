@@ -43,8 +43,10 @@
 //    XCDs, so each XCD's L2 serves one KV head when n_kv_heads divides 8), then
 //    Q head, then query tile heaviest first; waves skip key tiles that lie wholly
 //    above their queries' diagonal.
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <vector>
 
 #include "af_common.h"
 #include "af_device.h"
@@ -87,6 +89,12 @@ struct PrefillArgs {
     // FP8 pools: this layer's fp32 scales [2][n_kv_heads] (K, V); the slabs hold
     // E4M3 codes (one byte per element).
     const float* scales;
+    // Batched chunks: workgroup tile tt handles query tile tile_map[2tt+1] of chunk
+    // c = tile_map[2tt], chunks[4c..4c+3] = (p0, n, kv_len, first row in q / out),
+    // block table at table + c * max_blocks. NULL: one chunk described above.
+    const int32_t* tile_map;
+    const int32_t* chunks;
+    int32_t max_blocks;
 };
 
 // Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
@@ -238,7 +246,8 @@ constexpr int kVBase = 2 * kTileBytes;
 
 template <int QB, bool PAGED, bool FP8>
 __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention_kernel(
-    const PrefillArgs a) {
+    const PrefillArgs args) {
+    PrefillArgs a = args;
     constexpr int kQueries = 32 * QB * kPfWaves;  // per workgroup
     __shared__ __align__(16) char s_lds[4 * kTileBytes];
 
@@ -252,7 +261,22 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
     const int kvh = int(blockIdx.x) % a.n_kv_heads;
     const int rest = int(blockIdx.x) / a.n_kv_heads;
     const int head = kvh * group + rest % group;
-    const int tile = a.n_tiles - 1 - rest / group;
+    int tile;
+    if (a.tile_map) {  // batched chunks: the host orders the tiles heaviest first
+        const int tt = rest / group;
+        const int c = __builtin_amdgcn_readfirstlane(a.tile_map[2 * tt]);
+        tile = __builtin_amdgcn_readfirstlane(a.tile_map[2 * tt + 1]);
+        const int32_t* ci = a.chunks + 4 * c;
+        a.p0 = __builtin_amdgcn_readfirstlane(ci[0]);
+        a.n = __builtin_amdgcn_readfirstlane(ci[1]);
+        a.kv_len = __builtin_amdgcn_readfirstlane(ci[2]);
+        const int row0 = __builtin_amdgcn_readfirstlane(ci[3]);
+        a.q += size_t(row0) * a.q_stride;
+        a.out += size_t(row0) * a.out_stride;
+        a.table += size_t(c) * a.max_blocks;
+    } else {
+        tile = a.n_tiles - 1 - rest / group;
+    }
     const int t0 = tile * kQueries;
     const int wq0 = t0 + 32 * QB * wave;  // the wave's first query
     const bool wave_live = wq0 < a.n;
@@ -572,6 +596,85 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
     a.table = d_block_table;
     a.bs_log2 = __builtin_ctz(unsigned(bs));
     return launch_prefill(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_prefill_tile_map(const int32_t* h_chunks, int n_chunks, int32_t* h_tile_map,
+                                   int max_tiles) {
+    if (!h_chunks || !h_tile_map || n_chunks < 0 || max_tiles < 0) return AF_ERR_INVALID_ARG;
+    struct T {
+        int64_t work;
+        int c, t;
+    };
+    std::vector<T> tiles;
+    const int tq = 32 * kPfWaves;  // queries per tile of the launched kernel
+    for (int c = 0; c < n_chunks; ++c) {
+        const int p0 = h_chunks[4 * c], n = h_chunks[4 * c + 1], kv_len = h_chunks[4 * c + 2];
+        if (p0 < 0 || n < 0 || h_chunks[4 * c + 3] < 0) return AF_ERR_INVALID_ARG;
+        if (n > 0 && kv_len <= 0) return AF_ERR_OUT_OF_RANGE;
+        for (int t = 0; t * tq < n; ++t) {
+            const int64_t keys = std::min<int64_t>(int64_t(p0) + std::min((t + 1) * tq, n), kv_len);
+            tiles.push_back({keys, c, t});
+        }
+    }
+    if (int(tiles.size()) > max_tiles) return AF_ERR_WORKSPACE;
+    std::stable_sort(tiles.begin(), tiles.end(), [](const T& x, const T& y) { return x.work > y.work; });
+    for (size_t i = 0; i < tiles.size(); ++i) {
+        h_tile_map[2 * i] = tiles[i].c;
+        h_tile_map[2 * i + 1] = tiles[i].t;
+    }
+    return int(tiles.size());
+}
+
+extern "C" int af_paged_prefill_attention_batched(
+    const void* q, int q_stride, const af_kv_pool* pool, int layer, const int32_t* d_tables,
+    int max_blocks, const int32_t* d_chunks, const int32_t* d_tile_map, int n_tiles, void* out,
+    int out_stride, int n_q_heads, af_stream_t stream) {
+    if (!q || !pool || !pool->base || !d_tables || !d_chunks || !d_tile_map || !out ||
+        n_tiles < 0 || n_q_heads <= 0 || max_blocks <= 0)
+        return AF_ERR_INVALID_ARG;
+    if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
+        n_q_heads % pool->n_kv_heads)
+        return AF_ERR_INVALID_ARG;
+    const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
+    if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
+    if (fp8 && !pool->scales) return AF_ERR_INVALID_ARG;
+    const int bs = pool->block_size;
+    if (bs < 8 || (bs & (bs - 1))) return AF_ERR_INVALID_ARG;
+    const int q_dim = n_q_heads * kPfHd;
+    if (q_stride < q_dim || out_stride < q_dim || q_stride % 8 || out_stride % 8)
+        return AF_ERR_INVALID_ARG;
+    if (!aligned16(q) || !aligned16(out) || !aligned16(pool->base)) return AF_ERR_INVALID_ARG;
+    if (n_tiles == 0) return AF_OK;
+    const int64_t kv_stride = int64_t(pool->n_kv_heads) * kPfHd;
+    const size_t esz = fp8 ? 1 : 2;
+    const size_t slab = size_t(pool->total_blocks) * bs * kv_stride * esz;
+    const char* base = static_cast<const char*>(pool->base);
+    PrefillArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.q_stride = q_stride;
+    a.k = reinterpret_cast<const uint16_t*>(base + size_t(2 * layer) * slab);
+    a.v = reinterpret_cast<const uint16_t*>(base + size_t(2 * layer + 1) * slab);
+    a.kv_stride = kv_stride;
+    a.kv_row_bytes = uint32_t(kv_stride * esz);
+    a.scales = fp8 ? pool->scales + size_t(layer) * 2 * pool->n_kv_heads : nullptr;
+    a.out = static_cast<uint16_t*>(out);
+    a.out_stride = out_stride;
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = pool->n_kv_heads;
+    a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
+    a.table = d_tables;
+    a.bs_log2 = __builtin_ctz(unsigned(bs));
+    a.tile_map = d_tile_map;
+    a.chunks = d_chunks;
+    a.max_blocks = max_blocks;
+    const dim3 grid(n_tiles * n_q_heads), block(kPfThreads);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fp8)
+        hipLaunchKernelGGL((prefill_attention_kernel<1, true, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_attention_kernel<1, true, false>), grid, block, 0, s, a);
+    AF_TRY_LAUNCH();
+    return AF_OK;
 }
 
 extern "C" int af_tiled_attention(const void* q, const void* k, const void* v, void* out,

@@ -99,6 +99,27 @@ def launch_paged_prefill_attention(q, q_stride, pool, layer, d_block_table, max_
           "launch_paged_prefill_attention")
 
 
+def prefill_tile_map(chunks):
+    """(chunk, tile) pairs of the chunks [(p0, n, kv_len, row0), ...], heaviest first."""
+    ch = np.ascontiguousarray(chunks, np.int32).reshape(-1, 4)
+    max_tiles = int(sum((int(n) + 127) // 128 for n in ch[:, 1])) + 1
+    out = np.zeros((max_tiles, 2), np.int32)
+    n = lib().af_prefill_tile_map(ch.ctypes.data, len(ch), out.ctypes.data, max_tiles)
+    if n < 0:
+        raise AfError(n, "af_prefill_tile_map")
+    return out[:n].copy()
+
+
+def launch_paged_prefill_attention_batched(q, q_stride, pool, layer, d_tables, max_blocks,
+                                           d_chunks, d_tile_map, n_tiles, out, out_stride,
+                                           n_q_heads, stream=None):
+    """Chunked prefill of several sequences in one launch (see af_kv.h)."""
+    check(lib().af_paged_prefill_attention_batched(
+        _p(q), q_stride, ctypes.byref(pool), layer, _p(d_tables), max_blocks, _p(d_chunks),
+        _p(d_tile_map), n_tiles, _p(out), out_stride, n_q_heads, _s(stream)),
+        "launch_paged_prefill_attention_batched")
+
+
 def launch_tiled_attention_kernel(q, k, v, out, seq_q, seq_kv, head_dim, n_q_heads, n_kv_heads,
                                   stream=None):
     """tiled_attention.cu launch_tiled_attention_kernel<half>: query i attends keys s <= i."""
@@ -406,6 +427,7 @@ __all__ = [
     "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
     "launch_w8a16_gemv", "launch_prefill_rope_append", "launch_prefill_attention",
     "launch_tiled_attention_kernel", "launch_paged_prefill_attention", "Scheduler",
+    "launch_paged_prefill_attention_batched", "prefill_tile_map",
     "launch_rope", "launch_rope_append", "launch_write_kv_cache", "make_pool", "paged_gather",
     "pool_bytes", "rope_table_host",
 ]

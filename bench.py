@@ -61,6 +61,7 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="attention split count (0 = library default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
+    ap.add_argument("--no-serving", action="store_true", help="skip the continuous-batching step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
     return ap.parse_args()
@@ -240,6 +241,9 @@ def bench_contiguous(args, dev, kv, lib, info):
     if not args.no_prefill:
         log("prefill (one layer) ...")
         result["prefill"] = bench_prefill(dev, kv, lib, stream, 3, 10)
+    if not args.no_serving:
+        log("serving (scheduler-driven continuous batching) ...")
+        result["serving"] = bench_serving(dev, kv, lib)
     if args.calibrate_copy:
         calibrate_copy(dev, kv, stream)
     return result
@@ -330,6 +334,117 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     }
     for b in (k, v, qkv, out, pool_buf, pool8_buf, scales8, table, cos, sin):
         b.free()
+    return res
+
+
+def bench_serving(dev, kv, lib, steps=12, warmup=3):
+    """Continuous batching through the Scheduler: configs[2]'s
+    32 sequences (contexts uniform in [128, 8192]) decoding while a 2048-token prompt
+    arrives every step and is prefilled in 512-token chunks under a 2048-token step
+    budget. A step = the host plan (af_sched_step) + upload of slots / positions /
+    block tables / chunk descriptors + 28 layers of three launches: one paged append
+    for every new row (decode tokens and chunk tokens), decode attention for the
+    batch, and one batched prefill attention for all chunks."""
+    import atomflow_amd
+    r = np.random.Generator(np.random.PCG64(0xA70F10 + 6))
+    bs, chunk, budget, max_running = 16, 512, 2048, 64
+    ctx = r.integers(128, 8193, 32)
+    n_new, new_prompt, new_gen, old_gen = steps + warmup + 8, 2048, 64, 1000
+    total_blocks = (sum(-(-(int(c) + old_gen) // bs) for c in ctx)
+                    + n_new * -(-(new_prompt + new_gen) // bs) + 64)
+    bm = kv.BlockManager(total_blocks, bs, LAYERS, NKV, HD, atomflow_amd.AF_KV_FP16)
+    ids = [bm.allocate_block() for _ in range(total_blocks)]
+    for b in r.permutation(ids):
+        bm.free_block(int(b))
+    stream = dev.Stream()
+    nbytes = kv.pool_bytes(bm.pool())
+    pool_buf = dev.DeviceBuffer(nbytes)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(pool_buf.ptr, nbytes // 2, 7, 1.0, stream.handle))
+    bm.attach_pool(pool_buf.ptr)
+    pool = bm.pool()
+    sched = kv.Scheduler(bm, max_running, budget, chunk, 16)
+    for i, c in enumerate(ctx):
+        assert sched.add_request(i, int(c), old_gen)
+    while True:  # host-only steps until the 32 contexts are in the cache and decoding
+        p = sched.step()
+        if not p["prefill"] and len(p["decode"]) == len(ctx):
+            break
+    max_pos = 16384
+    max_blocks = max_pos // bs
+    d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    kv.build_rope_cache(d_cos, d_sin, max_pos, HD, THETA, stream)
+    rows = max_running + budget  # per layer: decode rows, then the chunks' rows
+    qkv = dev.DeviceBuffer(LAYERS * rows * QKV * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, qkv.nbytes // 2, 11, 1.0, stream.handle))
+    out = dev.DeviceBuffer(rows * Q_DIM * 2)
+    ws = kv.AttentionWorkspace(max_running, NQ, NKV, HD, 0, stream)
+    dev.synchronize()
+    e0, e1 = dev.Event(), dev.Event()
+    rec = []
+    for k in range(warmup + steps):
+        t0 = time.perf_counter()
+        sched.add_request(1000 + k, new_prompt, new_gen)
+        p = sched.step()
+        t1 = time.perf_counter()
+        a = p["arrays"]
+        nd = len(p["decode"])
+        # host -> device: slots / positions of every new row, block tables, chunk descriptors
+        slots = np.concatenate([a["decode_slots"], a["prefill_slots"]])
+        positions = np.concatenate([a["decode_positions"], a["prefill_positions"]])
+        bufs = [dev.DeviceBuffer.from_array(slots), dev.DeviceBuffer.from_array(positions)]
+        if nd:
+            tables, lens = bm.export_tables(a["decode_seqs"], max_blocks)
+            bufs += [dev.DeviceBuffer.from_array(tables), dev.DeviceBuffer.from_array(lens)]
+        nch = len(p["prefill"])
+        if nch:
+            ctab, _ = bm.export_tables([c[1] for c in p["prefill"]], max_blocks)
+            desc = np.array([(p0, n, p0 + n, nd + int(a["chunks"][i, 3]))
+                             for i, (_, _, p0, n, _, _) in enumerate(p["prefill"])], np.int32)
+            tmap = kv.prefill_tile_map(desc)
+            cb = [dev.DeviceBuffer.from_array(ctab), dev.DeviceBuffer.from_array(desc),
+                  dev.DeviceBuffer.from_array(tmap)]
+            bufs += cb
+        n_rows = len(slots)
+        e0.record(stream)
+        for l in range(LAYERS):
+            q = qkv.ptr + l * rows * QKV * 2
+            kv.launch_paged_rope_append(q, n_rows, pool, l, bufs[0], bufs[1], d_cos, d_sin,
+                                        max_pos, NQ, stream=stream)
+            if nd:
+                kv.launch_paged_attention(q, QKV, pool, l, bufs[2], max_blocks, bufs[3], nd,
+                                          int(lens.max()), out, Q_DIM, NQ, ws, stream=stream)
+            if nch:
+                kv.launch_paged_prefill_attention_batched(q, QKV, pool, l, cb[0], max_blocks,
+                                                          cb[1], cb[2], len(tmap), out, Q_DIM,
+                                                          NQ, stream=stream)
+        e1.record(stream)
+        e1.sync()
+        t2 = time.perf_counter()
+        for b in bufs:
+            b.free()
+        if k >= warmup:
+            rec.append((nd, sum(c[3] for c in p["prefill"]), nch, (t1 - t0) * 1e6,
+                        e0.elapsed_ms(e1), (t2 - t0) * 1e3))
+    rec = np.array(rec)
+    dec, pf, nch, plan_us, gpu_ms, wall_ms = rec.mean(axis=0)
+    res = {
+        "workload": "configs[2] pool (bs 16, permuted free list), 32 sequences with contexts in "
+                    "[128, 8192] decoding + one 2048-token prompt arriving per step, prefill chunk "
+                    "512, step budget 2048 tokens, 28 layers x (one paged append for all new rows, "
+                    "decode attention for the batch, one batched prefill attention for the "
+                    "chunks)",
+        "steps": steps, "decode_seqs_per_step": round(float(dec), 1),
+        "prefill_tokens_per_step": round(float(pf), 1), "chunks_per_step": round(float(nch), 1),
+        "host_plan_us": round(float(plan_us), 1), "gpu_ms_per_step": round(float(gpu_ms), 3),
+        "wall_ms_per_step": round(float(wall_ms), 3),
+        "tokens_per_s_gpu": round(float((dec + pf) / (gpu_ms * 1e-3)), 0),
+        "decode_tokens_per_s_gpu": round(float(dec / (gpu_ms * 1e-3)), 0),
+    }
+    for b in (pool_buf, d_cos, d_sin, qkv, out):
+        b.free()
+    sched.close()
+    bm.close()
     return res
 
 

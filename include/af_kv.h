@@ -280,6 +280,24 @@ int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* po
                                int kv_len, void* out, int out_stride, int n_q_heads,
                                af_stream_t stream);
 
+/* Several chunks (of different sequences) in one launch, the per-layer form of a
+ * serving step's chunked prefill. d_chunks: device int32 [n_chunks][4] =
+ * (p0, n, kv_len, row0): chunk c's queries are rows row0 .. row0+n-1 of q and out;
+ * d_tables: device int32 [n_chunks][max_blocks], chunk c's block table;
+ * d_tile_map: device int32 [n_tiles][2] from af_prefill_tile_map. Per-chunk
+ * semantics as af_paged_prefill_attention; outputs equal one launch per chunk
+ * bit for bit. The descriptors are device data and are not validated. */
+int af_paged_prefill_attention_batched(const void* q, int q_stride, const af_kv_pool* pool,
+                                       int layer, const int32_t* d_tables, int max_blocks,
+                                       const int32_t* d_chunks, const int32_t* d_tile_map,
+                                       int n_tiles, void* out, int out_stride, int n_q_heads,
+                                       af_stream_t stream);
+/* Host helper: the query tiles (128 queries each) of the chunks h_chunks (same
+ * layout as d_chunks), heaviest first, into h_tile_map [max_tiles][2] = (chunk,
+ * tile). Returns the tile count, or AF_ERR_WORKSPACE when it exceeds max_tiles. */
+int af_prefill_tile_map(const int32_t* h_chunks, int n_chunks, int32_t* h_tile_map,
+                        int max_tiles);
+
 /* launch_tiled_attention_kernel<half> (include/ops/kernel.h:73-85,
  * src/kernel/tiled_attention.cu:136-161): q [seq_q, n_q_heads*head_dim],
  * k/v [seq_kv, n_kv_heads*head_dim], out [seq_q, n_q_heads*head_dim]; query i

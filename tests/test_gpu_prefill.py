@@ -371,3 +371,55 @@ def test_paged_prefill_attention_fp8_pool(gpu, bs, p0, n, kv_len):
             p = np.exp(sc - sc.max())
             out[h] = p @ vf[:L, g] / p.sum()
         assert_attn_close(got[i], out.ravel(), ATOL_FP8, RTOL_FP8, what=f"row {i} vs float64")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_batched_paged_prefill_equals_per_chunk_launches(gpu, fp8):
+    """One launch over the chunks of several sequences == one launch per chunk,
+    bit for bit (each workgroup's arithmetic does not depend on the grid)."""
+    say(f"batched paged prefill fp8={fp8}")
+    bs, layers, layer = 16, 1, 0
+    chunks = [(0, 300, 300), (1000, 100, 1100), (0, 1, 1), (64, 200, 200), (500, 129, 629)]
+    max_blocks = max((kvl + bs - 1) // bs for _, _, kvl in chunks)
+    nblocks = sum((kvl + bs - 1) // bs for _, _, kvl in chunks) + 4
+    r = rng(0xA70F77 + fp8)
+    if fp8:
+        host = r.integers(0, 256, (layers, 2, nblocks * bs, KV_DIM), dtype=np.uint8)
+        host[(host & 0x7F) == 0x7F] = 0
+        scales = up(r.uniform(0.004, 0.02, (layers, 2, NKV)).astype(np.float32))
+        buf = up(host)
+        pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, scales)
+    else:
+        host, buf, pool = _paged_pool(bs, nblocks, layers, 0xA70F78)
+    perm = r.permutation(nblocks).astype(np.int32)
+    tables = np.zeros((len(chunks), max_blocks), np.int32)
+    at = 0
+    for c, (_, _, kvl) in enumerate(chunks):
+        nb = (kvl + bs - 1) // bs
+        tables[c, :nb] = perm[at:at + nb]
+        at += nb
+    rows = sum(n for _, n, _ in chunks)
+    q = randn_f16((rows, QKV), 0xA70F79)
+    desc, row0 = [], 0
+    for p0, n, kvl in chunks:
+        desc.append((p0, n, kvl, row0))
+        row0 += n
+    tmap = kv.prefill_tile_map(desc)
+    d_q = up(q)
+    d_o = up(np.zeros((rows, Q_DIM), np.float16))
+    kv.launch_paged_prefill_attention_batched(d_q, QKV, pool, layer, up(tables), max_blocks,
+                                              up(np.array(desc, np.int32)), up(tmap), len(tmap),
+                                              d_o, Q_DIM, NQ)
+    got = d_o.download(np.float16, (rows, Q_DIM))
+    for c, (p0, n, kvl, r0) in enumerate(desc):
+        one = up(np.zeros((n, Q_DIM), np.float16))
+        kv.launch_paged_prefill_attention(d_q.ptr + r0 * QKV * 2, QKV, pool, layer,
+                                          up(tables[c]), max_blocks, p0, n, kvl, one, Q_DIM, NQ)
+        assert np.array_equal(bits(got[r0:r0 + n]), bits(one.download(np.float16, (n, Q_DIM)))), c
+    if not fp8:
+        for c, (p0, n, kvl, r0) in enumerate(desc):
+            kc = oracle.paged_gather(host[layer, 0], tables[c], kvl, bs, KV_DIM)
+            vc = oracle.paged_gather(host[layer, 1], tables[c], kvl, bs, KV_DIM)
+            assert_attn_close(got[r0:r0 + n],
+                              oracle.prefill_attention_f64(q[r0:r0 + n], kc, vc, p0, n, kvl, NQ,
+                                                           NKV, HD), what=f"chunk {c}")

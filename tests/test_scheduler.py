@@ -119,3 +119,15 @@ def test_scheduler_chunking_budget_and_fifo():
     p = s.step()  # 1 and 2 decode; 0 gets its last 6 prompt tokens
     assert [(d[0], d[3]) for d in p["decode"]] == [(1, 11), (2, 10)]
     assert [(c[0], c[2], c[3], c[4]) for c in p["prefill"]] == [(0, 64, 6, True)]
+
+
+def test_prefill_tile_map_orders_heaviest_first():
+    chunks = [(0, 300, 300, 0), (1000, 100, 1100, 300), (0, 1, 1, 400), (64, 200, 200, 401)]
+    m = kv.prefill_tile_map(chunks)
+    # tiles of 128 queries: chunk 0 -> 3, chunk 1 -> 1, chunk 2 -> 1, chunk 3 -> 2 (kv_len caps)
+    assert sorted(map(tuple, m)) == sorted([(0, 0), (0, 1), (0, 2), (1, 0), (2, 0), (3, 0), (3, 1)])
+    work = {(0, 0): 128, (0, 1): 256, (0, 2): 300, (1, 0): 1100, (2, 0): 1, (3, 0): 192,
+            (3, 1): 200}
+    w = [work[tuple(x)] for x in m]
+    assert w == sorted(w, reverse=True)
+    assert kv.prefill_tile_map([]).shape == (0, 2)
