@@ -62,6 +62,13 @@ PROTOTYPES = {
     "af_paged_prefill_attention": (I, [P, I, P, I, P, I, I, I, I, P, I, I, P]),
     "af_paged_prefill_attention_batched": (I, [P, I, P, I, P, I, P, P, I, P, I, I, P]),
     "af_prefill_tile_map": (I, [P, I, P, I]),
+    "af_weights_open": (I, [ctypes.c_char_p, P]),
+    "af_weights_close": (I, [P]),
+    "af_weights_layout_bytes": (SZ, [P]),
+    "af_weights_header": (I, [P, P]),
+    "af_weights_payload_bytes": (SZ, [P]),
+    "af_weights_tensor": (I, [P, I, I, P, P, P]),
+    "af_weights_upload": (I, [P, P, SZ, P]),
     "af_sched_create": (I, [P, I, I, I, I, P]),
     "af_sched_destroy": (I, [P]),
     "af_sched_add_request": (I, [P, I64, I, I]),

@@ -62,6 +62,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--no-serving", action="store_true", help="skip the continuous-batching step")
+    ap.add_argument("--no-weights", action="store_true", help="skip the .bin load measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
     return ap.parse_args()
@@ -244,6 +245,9 @@ def bench_contiguous(args, dev, kv, lib, info):
     if not args.no_serving:
         log("serving (scheduler-driven continuous batching) ...")
         result["serving"] = bench_serving(dev, kv, lib)
+    if not args.no_weights:
+        log("weights (.bin load) ...")
+        result["weights"] = bench_weights(dev)
     if args.calibrate_copy:
         calibrate_copy(dev, kv, stream)
     return result
@@ -446,6 +450,60 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3):
     sched.close()
     bm.close()
     return res
+
+
+def bench_weights(dev, path_dir="/tmp"):
+    """Loading the reference's .bin format: a
+    Llama-3.2-3B-shaped file (header of the real model, random contents) is
+    uploaded by af_weights_upload (one streamed block through pinned double
+    buffers) and, for comparison, the way the reference engine does it
+    (engine.cu:97-148): one pageable copy per tensor from the mapped file."""
+    from atomflow_amd import weights as W
+    cfg = dict(dim=3072, hidden_dim=8192, n_layers=28, n_heads=24, n_kv_heads=8,
+               vocab_size=128256, max_seq_len=131072)
+    total = W.layout_bytes(cfg)
+    path = os.path.join(path_dir, f"af_bench_{os.getpid()}.bin")
+    block = np.random.default_rng(0xA70F96).integers(0, 256, 64 << 20, dtype=np.uint8).tobytes()
+    try:
+        with open(path, "wb") as f:
+            f.write(W.header_bytes(cfg))
+            left = total - 256
+            while left > 0:
+                n = min(left, len(block))
+                f.write(block[:n])
+                left -= n
+        wf = W.WeightFile(path)
+        dst = dev.DeviceBuffer(wf.payload_bytes)
+        wf.upload(dst)  # warm the page cache and the pinned-allocation path
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            wf.upload(dst)
+        t_stream = (time.perf_counter() - t0) / reps
+        mm = np.memmap(path, np.uint8, "r")
+        kinds = [(W.EMBED, -1)] + [(k, l) for l in range(cfg["n_layers"])
+                                   for k in range(W.INPUT_NORM, W.DOWN_SCALES + 1)]
+        kinds += [(W.FINAL_NORM, -1), (W.LM_HEAD, -1)]
+        specs = [wf.tensor(k, l) for k, l in kinds]
+        t0 = time.perf_counter()
+        for off, nb, _ in specs:
+            dst.upload(mm[256 + off:256 + off + nb], offset=off)
+        dev.synchronize()
+        t_ref = time.perf_counter() - t0
+        del mm
+        gb = wf.payload_bytes / 1e9
+        res = {"workload": "Llama-3.2-3B-shaped .bin (dim 3072, ffn 8192, 28 layers, vocab 128256): "
+                           f"{wf.payload_bytes / 2**30:.2f} GiB payload, file in the page cache",
+               "tensors": len(specs),
+               "upload_s": round(t_stream, 3), "upload_gbs": round(gb / t_stream, 1),
+               "per_tensor_pageable_s": round(t_ref, 3),
+               "per_tensor_pageable_gbs": round(gb / t_ref, 1)}
+        dst.free()
+        wf.close()
+        return res
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
 
 
 def bench_paged(args, dev, kv, lib, info):

@@ -42,6 +42,7 @@ extern "C" {
 #define AF_ERR_WORKSPACE (-6)       /* workspace missing or too small                 */
 #define AF_ERR_BAD_SEQUENCE (-7)    /* unknown sequence id                            */
 #define AF_ERR_NOT_BUILT (-8)       /* library built without a device code object     */
+#define AF_ERR_BAD_FILE (-9)        /* weight file missing, not AtomFlow, or truncated */
 
 typedef void* af_stream_t; /* hipStream_t; NULL = the default stream */
 
@@ -399,6 +400,38 @@ int af_sched_plan_prefill(const af_scheduler* s, int64_t* requests, int32_t* chu
 int af_sched_plan_copies(const af_scheduler* s, int32_t* copies);
 /* Requests retired at the start of the step, and requests preempted by it. */
 int af_sched_plan_events(const af_scheduler* s, int64_t* finished, int64_t* preempted);
+
+/* ======================================================================== */
+/* b4. AtomFlow .bin weights (WeightLoader)                                 */
+/* ======================================================================== */
+/* The format of tools/quantize_weights.py:320-427 read by WeightLoader
+ * (include/memory/weight_loader.h:23-130, src/core/engine.cu:97-148); layout in
+ * include/memory/weight_loader.h. The file is mapped read-only; its payload (the
+ * bytes after the 256-byte header) is uploaded as one block, so a tensor's
+ * device address is dst + its payload offset. */
+typedef struct af_weights af_weights;
+
+/* AF_ERR_BAD_FILE when the file is missing, has no ATOM magic, an inconsistent
+ * header, or fewer bytes than its layout needs. */
+int af_weights_open(const char* path, af_weights** out);
+int af_weights_close(af_weights* w);
+/* Bytes of a file with header fields[9] (order of af_weights_header); 0 if the
+ * header is inconsistent. */
+size_t af_weights_layout_bytes(const int32_t* fields);
+/* fields[9] = version, group_size, dim, hidden_dim, n_layers, n_heads,
+ * n_kv_heads, vocab_size, max_seq_len. */
+int af_weights_header(const af_weights* w, int32_t* fields);
+size_t af_weights_payload_bytes(const af_weights* w);
+/* Tensor kinds: 0 embed_tokens fp32 [V,D]; per layer 1 input_norm, 2 post_norm
+ * fp32 [D]; 3 qkv E4M3 [D+2KV, D], 4 its fp16 scales; 5 o_proj [D,D], 6 scales;
+ * 7 gate [F,D], 8 scales; 9 up [F,D], 10 scales; 11 down [D,F], 12 scales;
+ * 13 final norm fp32 [D]; 14 lm_head fp16 [V,D]. layer = -1 for kinds 0, 13, 14.
+ * offset: bytes from the payload start; dims[2] = rows, cols (cols 1 for vectors). */
+int af_weights_tensor(const af_weights* w, int kind, int layer, int64_t* offset, int64_t* bytes,
+                      int64_t* dims);
+/* Copies the payload to device memory d_dst (dst_bytes >= payload bytes) through
+ * pinned double buffers on `stream`; returns when the copy is complete. */
+int af_weights_upload(const af_weights* w, void* d_dst, size_t dst_bytes, af_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -45,7 +45,7 @@ def test_ctypes_prototypes_cover_the_headers():
 def test_library_loads_and_reports_status_strings():
     lib = atomflow_amd.lib()
     assert lib.af_version() > 0
-    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
         assert lib.af_status_string(code)
     assert lib.af_status_string(-1).decode() == "block pool exhausted"
 
