@@ -343,7 +343,8 @@ def test_paged_prefill_attention_fp8_pool(gpu, bs, p0, n, kv_len):
     host[(host & 0x7F) == 0x7F] = 0  # no NaN codes
     scales = r.uniform(0.004, 0.02, (layers, 2, NKV)).astype(np.float32)
     buf = up(host)
-    pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, up(scales))
+    d_scales = up(scales)  # the pool descriptor holds its address: keep it alive
+    pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, d_scales)
     table = r.permutation(nblocks)[:max_blocks].astype(np.int32)
     q = randn_f16((n, QKV), 0xA70F76 + n)
     d_o = up(np.zeros((n, Q_DIM), np.float16))
