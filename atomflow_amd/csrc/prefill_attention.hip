@@ -10,13 +10,12 @@
 // p0 + i and attends rows [0, min(p0 + i + 1, kv_len)). p0 = 0 with
 // kv_len = seq_kv is the reference's form (af_tiled_attention).
 //
-// Design: a workgroup is 4 waves of one Q head; each wave owns QB blocks of 32
-// queries (the launch uses QB = 1: 128 queries per workgroup, two workgroups
-// per CU).
+// Design: a workgroup is 4 waves of one Q head; each wave owns a block of 32
+// queries (128 queries per workgroup, two workgroups per CU, so each SIMD has a
+// second wave to issue matrix work during the other's softmax).
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: the A operand is a K fragment read
-//    from LDS, the B operand a query block held in registers for the whole
-//    launch. Each K fragment feeds the QB query blocks, so LDS bytes per MFMA fall
-//    with QB (LDS delivers about 64 B/clk per CU, one 1 KB fragment per 16 clk;
+//    from LDS, the B operand the query block held in registers for the whole
+//    launch (LDS delivers about 64 B/clk per CU, one 1 KB fragment per 16 clk;
 //    an MFMA takes 32).
 //  * Each lane owns 16 of the 32 scores of one query (lane l^32 the other 16):
 //    the softmax is in-lane work plus one v_permlane32_swap.
@@ -244,11 +243,10 @@ __device__ __forceinline__ float dot2_sum(const half8& h, float acc) {
 // LDS: K tiles at [0, 2*kTileBytes), V tiles after them.
 constexpr int kVBase = 2 * kTileBytes;
 
-template <int QB, bool PAGED, bool FP8>
-__global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention_kernel(
-    const PrefillArgs args) {
+template <bool PAGED, bool FP8>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const PrefillArgs args) {
     PrefillArgs a = args;
-    constexpr int kQueries = 32 * QB * kPfWaves;  // per workgroup
+    constexpr int kQueries = 32 * kPfWaves;  // per workgroup
     __shared__ __align__(16) char s_lds[4 * kTileBytes];
 
     const int tid = threadIdx.x;
@@ -278,26 +276,24 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         tile = a.n_tiles - 1 - rest / group;
     }
     const int t0 = tile * kQueries;
-    const int wq0 = t0 + 32 * QB * wave;  // the wave's first query
+    const int wq0 = t0 + 32 * wave;  // the wave's first query
     const bool wave_live = wq0 < a.n;
 
     const int wg_keys = min(a.p0 + min(t0 + kQueries, a.n), a.kv_len);
     const int n_kt = (wg_keys + kPfKeys - 1) / kPfKeys;
     // Keys the wave needs.
-    const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32 * QB, a.n), a.kv_len) : 0;
+    const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32, a.n), a.kv_len) : 0;
 
     // Query operands first: the loop's first waits then cover them.
-    half8 qf[QB][8];
-    int lim[QB];       // this lane's query of block b attends keys [0, lim[b])
-    int mask_from[QB]; // first key hidden from some query of block b
+    half8 qf[8];
+    const int qi_lane = min(wq0 + col, a.n - 1);  // clamped
+    const int lim = min(a.p0 + qi_lane + 1, a.kv_len);     // this lane's query attends [0, lim)
+    const int mask_from = min(a.p0 + wq0 + 1, a.kv_len);  // first key hidden from some query
+    {
+        const uint16_t* qrow =
+            a.q + size_t(qi_lane) * a.q_stride + size_t(head) * kPfHd + 8 * hi;
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        const int qi = min(wq0 + 32 * b + col, a.n - 1);  // clamped
-        lim[b] = min(a.p0 + qi + 1, a.kv_len);
-        mask_from[b] = min(a.p0 + wq0 + 32 * b + 1, a.kv_len);
-        const uint16_t* qrow = a.q + size_t(qi) * a.q_stride + size_t(head) * kPfHd + 8 * hi;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) qf[b][s] = __builtin_bit_cast(half8, ld16(qrow + 16 * s));
+        for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(half8, ld16(qrow + 16 * s));
     }
     // Keep the query loads ahead of the tile loads: the prologue's wait for the
     // tile then covers them, and the loop never waits on a query register.
@@ -343,19 +339,12 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         }
     }
 
-    float16v o[QB][4];
+    float16v o[4];
 #pragma unroll
-    for (int b = 0; b < QB; ++b)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[b][db][r] = 0.0f;
-    float m_run[QB], l_run[QB];
-#pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        m_run[b] = kPfEmptyMax;
-        l_run[b] = 0.0f;
-    }
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    float m_run = kPfEmptyMax, l_run = 0.0f;
     // FP8: scores carry the K scale, the output the V scale.
     const float sc = FP8 ? a.scale_log2 * a.scales[kvh] : a.scale_log2;
     const float v_scale = FP8 ? a.scales[a.n_kv_heads + kvh] : 1.0f;
@@ -393,71 +382,61 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
         for (int kb = 0; kb < 2; ++kb) {
             const int keyh = key0 + 32 * kb;
             if (keyh >= w_keys) break;  // wave-uniform
-            float16v sacc[QB];
+            float16v sacc;
 #pragma unroll
-            for (int b = 0; b < QB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[b][r] = 0.0f;
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const half8 kf = lds_half8(ks + ka[s] + kb * 32 * 256);
-#pragma unroll
-                for (int b = 0; b < QB; ++b)
-                    sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[b][s], sacc[b], 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc, 0, 0, 0);
             }
-            half8 pj[QB][2];
+            // Register r holds key keyh + 8(r/4) + 4hi + r%4.
+            if (keyh + 32 > mask_from) {
 #pragma unroll
-            for (int b = 0; b < QB; ++b) {
-                // Register r holds key keyh + 8(r/4) + 4hi + r%4.
-                if (keyh + 32 > mask_from[b]) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = keyh + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        sacc[b][r] = key < lim[b] ? sacc[b][r] : -INFINITY;
-                    }
+                for (int r = 0; r < 16; ++r) {
+                    const int key = keyh + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    sacc[r] = key < lim ? sacc[r] : -INFINITY;
                 }
-                // Probabilities against the running max m_run, rounded to fp16,
-                // and their row sum. While each lane's sum stays <= 2^8, every p
-                // is <= 2^8 and m_run is kept (it may trail the true max by up to
-                // 8 in log2 units; fp16 holds p to 2^15). Otherwise (the first
-                // keys, or scores that grew) the exact running max is taken and
-                // O^T, l rescaled: the max is computed only on this path.
-                float ls;
-                auto probs = [&]() {
-                    float16v pv;
+            }
+            // Probabilities against the running max m_run, rounded to fp16, and
+            // their row sum. While each lane's sum stays <= 2^8, every p is <= 2^8
+            // and m_run is kept (it may trail the true max by up to 8 in log2
+            // units; fp16 holds p to 2^15). Otherwise (the first keys, or scores
+            // that grew) the exact running max is taken and O^T, l rescaled: the
+            // max is computed only on this path.
+            half8 pj[2];
+            float ls;
+            auto probs = [&]() {
+                float16v pv;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(sacc[b][r], sc, -m_run[b]));
-                    pj[b][0] = to_half8(pv, 0);
-                    pj[b][1] = to_half8(pv, 8);
-                    ls = dot2_sum(pj[b][1], dot2_sum(pj[b][0], 0.0f));
-                };
+                for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(sacc[r], sc, -m_run));
+                pj[0] = to_half8(pv, 0);
+                pj[1] = to_half8(pv, 8);
+                ls = dot2_sum(pj[1], dot2_sum(pj[0], 0.0f));
+            };
+            probs();
+            if (__builtin_amdgcn_ballot_w64(!(ls <= kPfSumLimit))) {
+                float mx = sacc[0];
+#pragma unroll
+                for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+                const float m_new = fmaxf(m_run, halves_max(mx) * sc);
+                const float alpha = fast_exp2(m_run - m_new);
+                m_run = m_new;
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
                 probs();
-                if (__builtin_amdgcn_ballot_w64(!(ls <= kPfSumLimit))) {
-                    float mx = sacc[b][0];
-#pragma unroll
-                    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[b][r]);
-                    const float m_new = fmaxf(m_run[b], halves_max(mx) * sc);
-                    const float alpha = fast_exp2(m_run[b] - m_new);
-                    m_run[b] = m_new;
-                    l_run[b] *= alpha;
-#pragma unroll
-                    for (int db = 0; db < 4; ++db)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) o[b][db][r] *= alpha;
-                    probs();
-                }
-                l_run[b] += ls;
             }
+            l_run += ls;
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const char* p = vs + va[db] + 16 * (2 * kb + jj) * 256;
                     const half8 vt = lds_vt(p, p + 8 * 256);
-#pragma unroll
-                    for (int b = 0; b < QB; ++b)
-                        o[b][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pj[b][jj], o[b][db],
-                                                                          0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pj[jj], o[db], 0, 0, 0);
                 }
         }
         if constexpr (FP8)
@@ -473,40 +452,33 @@ __global__ __launch_bounds__(kPfThreads, QB == 1 ? 2 : 1) void prefill_attention
     if (kt < n_kt) step(kt, std::integral_constant<int, 0>{});
 
     if (!wave_live) return;
+    const int qi = wq0 + col;
+    const float inv = v_scale / halves_sum(l_run);
+    if (qi >= a.n) return;
+    uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        const int qi = wq0 + 32 * b + col;
-        const float inv = v_scale / halves_sum(l_run[b]);
-        if (qi >= a.n) continue;
-        uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                uint2 w;
-                w.x = uint32_t(f2h(o[b][db][4 * g] * inv)) |
-                      (uint32_t(f2h(o[b][db][4 * g + 1] * inv)) << 16);
-                w.y = uint32_t(f2h(o[b][db][4 * g + 2] * inv)) |
-                      (uint32_t(f2h(o[b][db][4 * g + 3] * inv)) << 16);
-                *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) = w;
-            }
-    }
+        for (int g = 0; g < 4; ++g) {
+            uint2 w;
+            w.x = uint32_t(f2h(o[db][4 * g] * inv)) | (uint32_t(f2h(o[db][4 * g + 1] * inv)) << 16);
+            w.y = uint32_t(f2h(o[db][4 * g + 2] * inv)) |
+                  (uint32_t(f2h(o[db][4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) = w;
+        }
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// One query block per wave: two workgroups per CU keep the matrix cores fed
-// across each other's softmax. (Two blocks per wave halve the LDS bytes per
-// MFMA but leave one wave per SIMD with its softmax exposed; measured slower.)
 int launch_prefill(PrefillArgs a, hipStream_t stream) {
     a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
     const dim3 grid(a.n_tiles * a.n_q_heads), block(kPfThreads);
     if (a.scales)
-        hipLaunchKernelGGL((prefill_attention_kernel<1, true, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<true, true>), grid, block, 0, stream, a);
     else if (a.table)
-        hipLaunchKernelGGL((prefill_attention_kernel<1, true, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<true, false>), grid, block, 0, stream, a);
     else
-        hipLaunchKernelGGL((prefill_attention_kernel<1, false, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<false, false>), grid, block, 0, stream, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -670,9 +642,9 @@ extern "C" int af_paged_prefill_attention_batched(
     const dim3 grid(n_tiles * n_q_heads), block(kPfThreads);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fp8)
-        hipLaunchKernelGGL((prefill_attention_kernel<1, true, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<true, true>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((prefill_attention_kernel<1, true, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((prefill_attention_kernel<true, false>), grid, block, 0, s, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
