@@ -633,6 +633,8 @@ def bench_paged(args, dev, kv, lib, info):
     }
     if cfg == 4:
         result["kernels"].update(cow_copy_timing(dev, kv, bm, prefix, B, stream, desc))
+    if args.calibrate_copy:
+        calibrate_copy(dev, kv, stream)
     return result
 
 
