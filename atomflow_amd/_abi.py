@@ -72,6 +72,10 @@ PROTOTYPES = {
     "af_sched_create": (I, [P, I, I, I, I, P]),
     "af_sched_destroy": (I, [P]),
     "af_sched_add_request": (I, [P, I64, I, I]),
+    "af_sched_add_request_prefix": (I, [P, I64, I, I, I64, I]),
+    "af_sched_set_prefix_cache": (I, [P, I]),
+    "af_sched_clear_prefix_cache": (I, [P]),
+    "af_sched_plan_prefix": (I, [P, P, P, P, P]),
     "af_sched_step": (I, [P, P]),
     "af_sched_plan_decode": (I, [P, P, P, P, P]),
     "af_sched_plan_prefill": (I, [P, P, P, P, P]),

@@ -17,12 +17,62 @@ void StepPlan::clear() {
     prefill.clear();
     prefill_slots.clear();
     prefill_positions.clear();
+    prefix_hits.clear();
+    cached.clear();
+    evicted.clear();
 }
 
 Scheduler::Scheduler(BlockManager& bm, const SchedulerConfig& cfg) : bm_(bm), cfg_(cfg) {}
 
+Scheduler::~Scheduler() { clear_prefix_cache(); }
+
+void Scheduler::clear_prefix_cache() {
+    for (const CachedPrefix& c : cache_) (void)bm_.free_sequence(c.seq);
+    cache_.clear();
+}
+
+void Scheduler::set_max_cached_prefixes(int n) {
+    cfg_.max_cached_prefixes = n < 0 ? 0 : n;
+    while (int(cache_.size()) > cfg_.max_cached_prefixes) {
+        (void)bm_.free_sequence(cache_.front().seq);
+        cache_.erase(cache_.begin());
+    }
+}
+
+int Scheduler::find_prefix(int64_t key, int len, bool ready_only) const {
+    for (int i = 0; i < int(cache_.size()); ++i) {
+        const CachedPrefix& c = cache_[size_t(i)];
+        if (c.key == key && c.len == len && (c.ready || !ready_only)) return i;
+    }
+    return -1;
+}
+
+bool Scheduler::evict_oldest(StepPlan* plan) {
+    if (cache_.empty()) return false;
+    (void)bm_.free_sequence(cache_.front().seq);
+    plan->evicted.push_back(cache_.front().key);
+    cache_.erase(cache_.begin());
+    return true;
+}
+
+// After a chunk: a request whose prefill just reached its prefix caches it
+// (a fork of its sequence, which holds exactly the prefix now).
+void Scheduler::maybe_cache(StepPlan* plan, const Entry& e) {
+    if (!caching(e) || e.prefilled != e.req.prefix_len) return;
+    if (find_prefix(e.req.prefix_key, e.req.prefix_len, false) >= 0) return;
+    if (int(cache_.size()) >= cfg_.max_cached_prefixes) (void)evict_oldest(plan);
+    CachedPrefix c;
+    c.key = e.req.prefix_key;
+    c.seq = bm_.fork_sequence(e.seq);
+    c.len = e.req.prefix_len;
+    cache_.push_back(c);
+    plan->cached.push_back(c.key);
+}
+
 int Scheduler::add_request(const Request& r) {
     if (r.prompt_len < 1 || r.max_new_tokens < 1) return AF_ERR_INVALID_ARG;
+    if (r.prefix_len < 0 || r.prefix_len >= r.prompt_len || (r.prefix_len > 0 && r.prefix_key < 0))
+        return AF_ERR_INVALID_ARG;
     const int64_t bs = bm_.config().block_size;
     const int64_t need = (int64_t(r.prompt_len) + r.max_new_tokens + bs - 1) / bs;
     if (need > bm_.config().total_blocks) return AF_ERR_INVALID_ARG;
@@ -64,6 +114,8 @@ void Scheduler::emit_chunk(StepPlan* plan, Entry& e, int first, int n) {
 int Scheduler::step(StepPlan* plan) {
     if (!plan) return AF_ERR_INVALID_ARG;
     plan->clear();
+    // 0. prefixes cached last step are complete in the pool now
+    for (CachedPrefix& c : cache_) c.ready = true;
     // 1. retire
     std::vector<Entry> keep;
     keep.reserve(running_.size());
@@ -89,7 +141,7 @@ int Scheduler::step(StepPlan* plan) {
         slots.assign(dec.size(), AppendSlot{});
         const int st = bm_.plan_decode(seqs.data(), int(seqs.size()), slots.data());
         if (st == AF_ERR_POOL_EXHAUSTED) {
-            preempt_youngest(plan);
+            if (!evict_oldest(plan)) preempt_youngest(plan);
             continue;
         }
         if (st) return st;
@@ -116,10 +168,13 @@ int Scheduler::step(StepPlan* plan) {
         int n = e.prompt_eff - e.prefilled;
         if (n > cfg_.prefill_chunk) n = cfg_.prefill_chunk;
         if (n > budget) n = budget;
+        if (caching(e) && e.prefilled < e.req.prefix_len && n > e.req.prefix_len - e.prefilled)
+            n = e.req.prefix_len - e.prefilled;  // a chunk ends at the prefix
         int first = 0;
         CowCopy cow;
         const int st = bm_.extend(e.seq, n, &first, &cow);
         if (st == AF_ERR_POOL_EXHAUSTED) {
+            if (evict_oldest(plan)) continue;
             if (plan->decode_seqs.empty() && i + 1 < running_.size()) {
                 preempt_youngest(plan);
                 continue;
@@ -130,6 +185,7 @@ int Scheduler::step(StepPlan* plan) {
         if (st) return st;
         if (cow.src >= 0) plan->copies.push_back(cow);
         emit_chunk(plan, e, first, n);
+        maybe_cache(plan, e);
         budget -= n;
         ++i;
     }
@@ -137,19 +193,37 @@ int Scheduler::step(StepPlan* plan) {
     while (!stalled && !waiting_.empty() && int(running_.size()) < cfg_.max_running &&
            budget > 0) {
         Entry& h = waiting_.front();
-        int n = h.prompt_eff;
+        const int bs = bm_.config().block_size;
+        const int hit = caching(h) ? find_prefix(h.req.prefix_key, h.req.prefix_len, true) : -1;
+        const int base = hit >= 0 ? h.req.prefix_len : 0;  // tokens taken from the cache
+        int n = h.prompt_eff - base;
         if (n > cfg_.prefill_chunk) n = cfg_.prefill_chunk;
         if (n > budget) n = budget;
-        const int need = (n + bm_.config().block_size - 1) / bm_.config().block_size;
+        if (hit < 0 && caching(h) && n > h.req.prefix_len) n = h.req.prefix_len;
+        // New blocks: those the chunk touches, the shared partial tail included
+        // (copy-on-write).
+        const int need = (base + n + bs - 1) / bs - base / bs;
         if (bm_.num_free_blocks() - need < cfg_.watermark_blocks) break;
         Entry e = h;
         waiting_.pop_front();
-        e.seq = bm_.create_sequence();
+        CowCopy cow;
+        if (hit >= 0) {
+            const CachedPrefix c = cache_[size_t(hit)];
+            cache_.erase(cache_.begin() + hit);
+            cache_.push_back(c);  // youngest
+            e.seq = bm_.fork_sequence(c.seq);
+            e.prefilled = base;
+            plan->prefix_hits.push_back(e.req.id);
+        } else {
+            e.seq = bm_.create_sequence();
+        }
         int first = 0;
-        const int st = bm_.extend(e.seq, n, &first, nullptr);
+        const int st = bm_.extend(e.seq, n, &first, &cow);
         if (st) return st;  // cannot happen: the blocks were counted above
+        if (cow.src >= 0) plan->copies.push_back(cow);
         running_.push_back(e);
         emit_chunk(plan, running_.back(), first, n);
+        maybe_cache(plan, running_.back());
         budget -= n;
     }
     return AF_OK;
@@ -205,6 +279,47 @@ extern "C" int af_sched_add_request(af_scheduler* s, int64_t id, int prompt_len,
     r.prompt_len = prompt_len;
     r.max_new_tokens = max_new_tokens;
     return s->sched.add_request(r);
+}
+
+extern "C" int af_sched_add_request_prefix(af_scheduler* s, int64_t id, int prompt_len,
+                                           int max_new_tokens, int64_t prefix_key,
+                                           int prefix_len) {
+    if (!s) return AF_ERR_INVALID_ARG;
+    Request r;
+    r.id = id;
+    r.prompt_len = prompt_len;
+    r.max_new_tokens = max_new_tokens;
+    r.prefix_key = prefix_key;
+    r.prefix_len = prefix_len;
+    return s->sched.add_request(r);
+}
+
+extern "C" int af_sched_set_prefix_cache(af_scheduler* s, int max_entries) {
+    if (!s || max_entries < 0) return AF_ERR_INVALID_ARG;
+    s->sched.set_max_cached_prefixes(max_entries);
+    return AF_OK;
+}
+
+extern "C" int af_sched_clear_prefix_cache(af_scheduler* s) {
+    if (!s) return AF_ERR_INVALID_ARG;
+    s->sched.clear_prefix_cache();
+    return AF_OK;
+}
+
+extern "C" int af_sched_plan_prefix(const af_scheduler* s, int32_t* counts, int64_t* hits,
+                                    int64_t* cached, int64_t* evicted) {
+    if (!s) return AF_ERR_INVALID_ARG;
+    const StepPlan& p = s->plan;
+    if (counts) {
+        counts[0] = int32_t(p.prefix_hits.size());
+        counts[1] = int32_t(p.cached.size());
+        counts[2] = int32_t(p.evicted.size());
+        counts[3] = s->sched.num_cached_prefixes();
+    }
+    for (size_t i = 0; hits && i < p.prefix_hits.size(); ++i) hits[i] = p.prefix_hits[i];
+    for (size_t i = 0; cached && i < p.cached.size(); ++i) cached[i] = p.cached[i];
+    for (size_t i = 0; evicted && i < p.evicted.size(); ++i) evicted[i] = p.evicted[i];
+    return AF_OK;
 }
 
 extern "C" int af_sched_step(af_scheduler* s, int32_t* counts) {

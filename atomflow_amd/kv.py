@@ -362,12 +362,21 @@ class Scheduler:
     [(request, seq, p0, n, last, slots)], and the running / waiting counts.
     """
 
-    def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0):
+    def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0,
+                 max_cached_prefixes=0):
         h = ctypes.c_void_p()
         check(lib().af_sched_create(bm.h, max_running, max_step_tokens, prefill_chunk, watermark,
                                     ctypes.byref(h)), "af_sched_create")
         self.h = h.value
         self.bm = bm  # keeps the manager alive
+        if max_cached_prefixes:
+            self.set_prefix_cache(max_cached_prefixes)
+
+    def set_prefix_cache(self, max_entries):
+        check(lib().af_sched_set_prefix_cache(self.h, max_entries), "af_sched_set_prefix_cache")
+
+    def clear_prefix_cache(self):
+        check(lib().af_sched_clear_prefix_cache(self.h), "af_sched_clear_prefix_cache")
 
     def close(self):
         if self.h:
@@ -380,7 +389,10 @@ class Scheduler:
         except Exception:
             pass
 
-    def add_request(self, rid, prompt_len, max_new_tokens):
+    def add_request(self, rid, prompt_len, max_new_tokens, prefix_key=-1, prefix_len=0):
+        if prefix_len:
+            return lib().af_sched_add_request_prefix(self.h, rid, prompt_len, max_new_tokens,
+                                                     prefix_key, prefix_len) == 0
         return lib().af_sched_add_request(self.h, rid, prompt_len, max_new_tokens) == 0
 
     def step(self):
@@ -403,11 +415,18 @@ class Scheduler:
         for i in range(nc):
             seq, p0, n, off, last = (int(x) for x in chunks[i])
             prefill.append((int(preq[i]), seq, p0, n, bool(last), [int(x) for x in pslot[off:off + n]]))
+        pc = np.zeros(4, np.int32)
+        lib().af_sched_plan_prefix(self.h, pc.ctypes.data, None, None, None)
+        hits, cached, evicted = (np.zeros(int(x), np.int64) for x in pc[:3])
+        lib().af_sched_plan_prefix(self.h, None, hits.ctypes.data, cached.ctypes.data,
+                                   evicted.ctypes.data)
         return {
             "finished": [int(x) for x in fin], "preempted": [int(x) for x in pre],
             "decode": [(int(dreq[i]), int(dseq[i]), int(dslot[i]), int(dpos[i])) for i in range(nd)],
             "copies": [tuple(int(x) for x in row) for row in copies],
             "prefill": prefill, "running": nrun, "waiting": nwait,
+            "prefix_hits": [int(x) for x in hits], "cached": [int(x) for x in cached],
+            "evicted": [int(x) for x in evicted], "cache_entries": int(pc[3]),
             "arrays": {"decode_seqs": dseq, "decode_slots": dslot, "decode_positions": dpos,
                        "prefill_slots": pslot, "prefill_positions": ppos, "copies": copies,
                        "chunks": chunks},

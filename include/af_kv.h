@@ -385,6 +385,25 @@ int af_sched_create(af_block_manager* bm, int max_running, int max_step_tokens,
 int af_sched_destroy(af_scheduler* s);
 /* FIFO; AF_ERR_INVALID_ARG if the request could never fit the pool alone. */
 int af_sched_add_request(af_scheduler* s, int64_t id, int prompt_len, int max_new_tokens);
+/* Prefix caching (no counterpart in the reference, whose server loop is a stub:
+ * server_engine.cu:55-68; the fork it builds on is PageTable's "fork, bump
+ * ref_counts", paged_kv_manager.h:61). A request whose first prefix_len
+ * (< prompt_len) prompt tokens equal those of every request with the same
+ * prefix_key: with the cache on, the first such request's prefill caches a fork
+ * of its sequence at prefix_len, and later ones fork it and prefill only the
+ * rest (their first append into a partial shared block is a CoW copy in the
+ * plan). af_sched_set_prefix_cache sets the entry limit (0 = off, the default:
+ * prefixes are then ignored); entries are evicted oldest-first when full and
+ * before any preemption when the pool runs out. */
+int af_sched_add_request_prefix(af_scheduler* s, int64_t id, int prompt_len, int max_new_tokens,
+                                int64_t prefix_key, int prefix_len);
+int af_sched_set_prefix_cache(af_scheduler* s, int max_entries);
+int af_sched_clear_prefix_cache(af_scheduler* s);
+/* This step's prefix events. counts (optional, int32[4]): requests admitted on
+ * a cached prefix, prefixes cached, prefixes evicted, entries in the cache. The
+ * arrays (optional) receive the request ids and the cached / evicted keys. */
+int af_sched_plan_prefix(const af_scheduler* s, int32_t* counts, int64_t* hits, int64_t* cached,
+                         int64_t* evicted);
 /* Plans one step. counts (optional, int32[8]): decode sequences, prefill chunks,
  * prefill tokens, CoW copies, finished, preempted, running, waiting. */
 int af_sched_step(af_scheduler* s, int32_t* counts);

@@ -18,7 +18,20 @@
 //    yields the first output token, each decode step one more, and the request
 //    retires once it has generated max_new_tokens (its last token is never
 //    appended to the cache);
-//  * step(): (1) retire finished entries; (2) decode every fully prefilled
+//  * prefix cache (off unless max_cached_prefixes > 0): a request may name a
+//    prompt prefix (prefix_key, prefix_len < prompt_len) whose tokens equal
+//    every other request's with that key. Its prefill is chunked so that one
+//    chunk ends exactly at prefix_len; when a request's prefill reaches it and
+//    the key is not cached, the scheduler forks the sequence into the cache
+//    (block tables and refcounts only; usable from the next step, after that
+//    step's KV writes). A request admitted while its key is cached forks the
+//    cached sequence instead of computing the prefix (the first append into a
+//    partial shared tail block is a copy-on-write) and prefills the rest.
+//    Cached sequences are evicted oldest-first when the cache is full and
+//    before any preemption when the pool runs out; a hit makes an entry the
+//    youngest;
+//  * step(): (0) prefixes cached last step become usable; (1) retire finished
+//    entries; (2) decode every fully prefilled
 //    entry (plan_decode, all or nothing); if the pool cannot hold the batch,
 //    preempt the most recently admitted entry to the front of the queue and
 //    plan again; (3) continue partial prefills in admission order with
@@ -40,12 +53,15 @@ struct SchedulerConfig {
     int max_step_tokens = 2048;  // decode + prefill tokens per step (>= max_running)
     int prefill_chunk = 512;     // prompt tokens of one request per step
     int watermark_blocks = 0;    // free blocks admission leaves untouched
+    int max_cached_prefixes = 0; // prefix-cache entries (0: prefixes are ignored)
 };
 
 struct Request {
     int64_t id = 0;
     int prompt_len = 0;
     int max_new_tokens = 0;
+    int64_t prefix_key = -1;  // >= 0 when prefix_len > 0
+    int prefix_len = 0;       // shared prompt prefix, < prompt_len
 };
 
 struct PrefillChunk {
@@ -68,6 +84,9 @@ struct StepPlan {
     std::vector<PrefillChunk> prefill;
     std::vector<int64_t> prefill_slots;
     std::vector<int32_t> prefill_positions;
+    std::vector<int64_t> prefix_hits;  // requests admitted onto a cached prefix
+    std::vector<int64_t> cached;       // prefix keys cached by this step
+    std::vector<int64_t> evicted;      // prefix keys evicted by this step
     int tokens() const { return int(decode_seqs.size() + prefill_slots.size()); }
     void clear();
 };
@@ -75,9 +94,19 @@ struct StepPlan {
 class Scheduler {
 public:
     Scheduler(BlockManager& bm, const SchedulerConfig& cfg);
+    ~Scheduler();  // frees the cached prefix sequences
+    Scheduler(const Scheduler&) = delete;
+    Scheduler& operator=(const Scheduler&) = delete;
     // AF_OK, or AF_ERR_INVALID_ARG when the request could never fit the pool alone
-    // (ceil((prompt_len + max_new_tokens) / block_size) > total blocks).
+    // (ceil((prompt_len + max_new_tokens) / block_size) > total blocks) or its
+    // prefix fields are inconsistent.
     int add_request(const Request& r);
+    // Frees every cached prefix sequence (blocks shared with running requests
+    // stay theirs).
+    void clear_prefix_cache();
+    // Resizes the prefix cache (0 turns it off), evicting oldest entries first.
+    void set_max_cached_prefixes(int n);
+    int num_cached_prefixes() const { return int(cache_.size()); }
     // Plans one step into *plan (cleared first). AF_OK or an AF_* error.
     int step(StepPlan* plan);
     int num_waiting() const { return int(waiting_.size()); }
@@ -93,13 +122,26 @@ private:
         int prefilled = 0;
         int generated = 0;
     };
+    struct CachedPrefix {
+        int64_t key = -1;
+        int seq = -1;
+        int len = 0;
+        bool ready = false;  // false during the step that cached it
+    };
     void preempt_youngest(StepPlan* plan);
     void emit_chunk(StepPlan* plan, Entry& e, int first, int n);
+    bool caching(const Entry& e) const {
+        return cfg_.max_cached_prefixes > 0 && e.req.prefix_len > 0;
+    }
+    int find_prefix(int64_t key, int len, bool ready_only) const;  // index in cache_ or -1
+    bool evict_oldest(StepPlan* plan);
+    void maybe_cache(StepPlan* plan, const Entry& e);
 
     BlockManager& bm_;
     SchedulerConfig cfg_;
     std::deque<Entry> waiting_;
-    std::vector<Entry> running_;  // admission order
+    std::vector<Entry> running_;       // admission order
+    std::vector<CachedPrefix> cache_;  // oldest first
 };
 
 }  // namespace atomflow::server

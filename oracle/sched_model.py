@@ -30,31 +30,87 @@ step():
     remains: the first chunk n = min(prompt_eff, prefill_chunk, budget) needs
     ceil(n / block_size) blocks and leaves at least `watermark` free blocks, or
     admission stops (the head of the queue is never skipped).
+
+Prefix cache (max_cached_prefixes > 0; otherwise prefix fields are ignored). A
+request may carry (prefix_key, prefix_len), 0 < prefix_len < prompt_len: its
+first prefix_len prompt tokens equal those of every request with that key.
+ 0. at the start of step(), entries cached by the previous step become ready;
+ * prefill chunks of such a request are cut to end exactly at prefix_len; when
+   a chunk (step 3 or 4) brings prefilled to prefix_len and no entry (ready or
+   not) has this (key, len), the cache evicts its oldest entry if full, then
+   appends (key, fork(seq), len, not ready), oldest first;
+ * admission of a request with a ready (key, len) entry: base = prefix_len,
+   n = min(prompt_eff - base, prefill_chunk, budget), need = ceil((base + n) /
+   bs) - floor(base / bs) (the partial shared tail is copied on write); the
+   entry moves to the youngest end, seq = fork(entry's seq), prefilled = base,
+   extend by n (its CoW copy joins the plan), and the request id is listed in
+   prefix_hits. Without a hit, n is also capped at prefix_len;
+ * when the decode plan (step 2) or a prefill extend (step 3) finds the pool
+   exhausted, the oldest cache entry is evicted (its sequence freed) and the
+   same plan is retried; only with an empty cache do the preemption / stall
+   rules apply.
 """
 from .block_model import POOL_EXHAUSTED
 
 
 class _Entry:
-    __slots__ = ("rid", "prompt_len", "max_new", "seq", "prompt_eff", "prefilled", "generated")
+    __slots__ = ("rid", "prompt_len", "max_new", "seq", "prompt_eff", "prefilled", "generated",
+                 "pkey", "plen")
 
-    def __init__(self, rid, prompt_len, max_new):
+    def __init__(self, rid, prompt_len, max_new, pkey=-1, plen=0):
         self.rid, self.prompt_len, self.max_new = rid, prompt_len, max_new
         self.seq, self.prompt_eff, self.prefilled, self.generated = -1, prompt_len, 0, 0
+        self.pkey, self.plen = pkey, plen
 
 
 class SchedModel:
-    def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0):
+    def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0,
+                 max_cached_prefixes=0):
         self.bm = bm
         self.max_running, self.max_step_tokens = max_running, max_step_tokens
         self.prefill_chunk, self.watermark = prefill_chunk, watermark
+        self.max_cached = max_cached_prefixes
         self.waiting, self.running = [], []
+        self.cache = []  # [key, seq, len, ready], oldest first
 
-    def add_request(self, rid, prompt_len, max_new):
+    def _caching(self, e):
+        return self.max_cached > 0 and e.plen > 0
+
+    def _find(self, key, length, ready_only):
+        for i, c in enumerate(self.cache):
+            if c[0] == key and c[2] == length and (c[3] or not ready_only):
+                return i
+        return -1
+
+    def _evict_oldest(self, plan):
+        if not self.cache:
+            return False
+        key, seq, _, _ = self.cache.pop(0)
+        self.bm.seq_free(seq)
+        plan["evicted"].append(key)
+        return True
+
+    def _maybe_cache(self, plan, e):
+        if not self._caching(e) or e.prefilled != e.plen or self._find(e.pkey, e.plen, False) >= 0:
+            return
+        if len(self.cache) >= self.max_cached:
+            self._evict_oldest(plan)
+        self.cache.append([e.pkey, self.bm.seq_fork(e.seq), e.plen, False])
+        plan["cached"].append(e.pkey)
+
+    def clear_prefix_cache(self):
+        for _, seq, _, _ in self.cache:
+            self.bm.seq_free(seq)
+        self.cache = []
+
+    def add_request(self, rid, prompt_len, max_new, prefix_key=-1, prefix_len=0):
         if prompt_len < 1 or max_new < 1:
+            return False
+        if prefix_len < 0 or prefix_len >= prompt_len or (prefix_len > 0 and prefix_key < 0):
             return False
         if -(-(prompt_len + max_new) // self.bm.bs) > self.bm.total:
             return False  # could never fit alone
-        self.waiting.append(_Entry(rid, prompt_len, max_new))
+        self.waiting.append(_Entry(rid, prompt_len, max_new, prefix_key, prefix_len))
         return True
 
     def _preempt_youngest(self, plan):
@@ -73,7 +129,10 @@ class SchedModel:
             e.generated += 1
 
     def step(self):
-        plan = {"finished": [], "preempted": [], "decode": [], "copies": [], "prefill": []}
+        plan = {"finished": [], "preempted": [], "decode": [], "copies": [], "prefill": [],
+                "prefix_hits": [], "cached": [], "evicted": []}
+        for c in self.cache:
+            c[3] = True
         keep = []
         for e in self.running:
             if e.generated >= e.max_new:
@@ -88,7 +147,8 @@ class SchedModel:
                 break
             r = self.bm.plan_decode([e.seq for e in dec])
             if r == POOL_EXHAUSTED:
-                self._preempt_youngest(plan)
+                if not self._evict_oldest(plan):
+                    self._preempt_youngest(plan)
                 continue
             slots, positions, copies = r
             for e, sl, p in zip(dec, slots, positions):
@@ -105,8 +165,12 @@ class SchedModel:
                 i += 1
                 continue
             n = min(e.prompt_eff - e.prefilled, self.prefill_chunk, budget)
+            if self._caching(e) and e.prefilled < e.plen:
+                n = min(n, e.plen - e.prefilled)
             r = self.bm.seq_extend(e.seq, n)
             if r == POOL_EXHAUSTED:
+                if self._evict_oldest(plan):
+                    continue
                 if not plan["decode"] and i < len(self.running) - 1:
                     self._preempt_youngest(plan)
                     continue
@@ -116,21 +180,38 @@ class SchedModel:
             if cow[0] >= 0:
                 plan["copies"].append(cow)
             self._chunk(plan, e, first, n)
+            self._maybe_cache(plan, e)
             budget -= n
             i += 1
         while (not stalled and self.waiting and len(self.running) < self.max_running
                and budget > 0):
             e = self.waiting[0]
-            n = min(e.prompt_eff, self.prefill_chunk, budget)
-            need = -(-n // self.bm.bs)
+            bs = self.bm.bs
+            hit = self._find(e.pkey, e.plen, True) if self._caching(e) else -1
+            base = e.plen if hit >= 0 else 0
+            n = min(e.prompt_eff - base, self.prefill_chunk, budget)
+            if hit < 0 and self._caching(e):
+                n = min(n, e.plen)
+            need = -(-(base + n) // bs) - base // bs
             if self.bm.num_free_blocks() - need < self.watermark:
                 break
             self.waiting.pop(0)
-            e.seq = self.bm.seq_create()
+            if hit >= 0:
+                c = self.cache.pop(hit)
+                self.cache.append(c)
+                e.seq = self.bm.seq_fork(c[1])
+                e.prefilled = base
+                plan["prefix_hits"].append(e.rid)
+            else:
+                e.seq = self.bm.seq_create()
             r = self.bm.seq_extend(e.seq, n)
             assert r != POOL_EXHAUSTED
+            first, cow = r
+            if cow[0] >= 0:
+                plan["copies"].append(cow)
             self.running.append(e)
-            self._chunk(plan, e, r[0], n)
+            self._chunk(plan, e, first, n)
+            self._maybe_cache(plan, e)
             budget -= n
         return plan
 

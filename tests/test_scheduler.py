@@ -11,7 +11,7 @@ from oracle.sched_model import SchedModel
 
 
 def _same(a, b, step):
-    for key in ("finished", "preempted", "decode", "copies"):
+    for key in ("finished", "preempted", "decode", "copies", "prefix_hits", "cached", "evicted"):
         assert [tuple(x) if isinstance(x, (list, tuple)) else x for x in a[key]] == \
                [tuple(x) if isinstance(x, (list, tuple)) else x for x in b[key]], (step, key)
     assert len(a["prefill"]) == len(b["prefill"]), step
@@ -20,23 +20,35 @@ def _same(a, b, step):
 
 
 def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, watermark, n_req,
-              max_prompt, max_new, arrivals_per_step):
+              max_prompt, max_new, arrivals_per_step, n_prefixes=0, max_cached=0):
+    """Random trace; with n_prefixes > 0 about half the requests share one of
+    n_prefixes prompt prefixes (lengths drawn per key) and the prefix cache holds
+    max_cached entries."""
     r = np.random.default_rng(seed)
     bm = kv.BlockManager(total_blocks, bs, 1, 8, 128)
-    sched = kv.Scheduler(bm, max_running, max_step_tokens, chunk, watermark)
+    sched = kv.Scheduler(bm, max_running, max_step_tokens, chunk, watermark, max_cached)
     model = SchedModel(BlockModel(total_blocks, bs), max_running, max_step_tokens, chunk,
-                       watermark)
-    reqs = [(i, int(r.integers(1, max_prompt + 1)), int(r.integers(1, max_new + 1)))
-            for i in range(n_req)]
-    generated = {rid: 0 for rid, _, _ in reqs}
+                       watermark, max_cached)
+    plens = [int(r.integers(1, max_prompt)) for _ in range(n_prefixes)]
+    reqs = []
+    for i in range(n_req):
+        pl, mn = int(r.integers(1, max_prompt + 1)), int(r.integers(1, max_new + 1))
+        key, plen = -1, 0
+        if n_prefixes and r.random() < 0.5:
+            key = int(r.integers(0, n_prefixes))
+            plen = plens[key]
+            pl = plen + int(r.integers(1, max(2, max_prompt - plen + 1)))
+        reqs.append((i, pl, mn, key, plen))
+    generated = {q[0]: 0 for q in reqs}
     finished = []
     pending = list(reqs)
-    steps = 0
+    steps = hits = 0
     while pending or not model.idle():
         for _ in range(int(r.integers(0, arrivals_per_step + 1))):
             if pending:
-                rid, pl, mn = pending.pop(0)
-                assert sched.add_request(rid, pl, mn) == model.add_request(rid, pl, mn)
+                rid, pl, mn, key, plen = pending.pop(0)
+                assert sched.add_request(rid, pl, mn, key, plen) == \
+                    model.add_request(rid, pl, mn, key, plen)
         a = sched.step()
         b = model.step()
         _same(a, b, steps)
@@ -50,16 +62,20 @@ def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, water
             assert len(slots) == n
             if last:
                 generated[rid] += 1
+        assert a["cache_entries"] == len(model.cache) <= max(max_cached, 0)
+        hits += len(a["prefix_hits"])
         finished += a["finished"]
         steps += 1
         assert steps < 20000, "no progress"
-    assert sorted(finished) == sorted(rid for rid, _, _ in reqs)
-    for rid, pl, mn in reqs:
+    assert sorted(finished) == sorted(q[0] for q in reqs)
+    for rid, pl, mn, _, _ in reqs:
         assert generated[rid] == mn, (rid, generated[rid], mn)
+    sched.clear_prefix_cache()
+    model.clear_prefix_cache()
     assert bm.num_free_blocks() == total_blocks
     sched.close()
     bm.close()
-    return steps
+    return steps, hits
 
 
 @pytest.mark.parametrize("seed", range(6))
@@ -74,6 +90,49 @@ def test_scheduler_matches_model_tight_pool_with_preemption(seed):
     prefill stalls and the liveness rule all fire."""
     run_trace(100 + seed, total_blocks=40, bs=16, max_running=8, max_step_tokens=64, chunk=32,
               watermark=0, n_req=30, max_prompt=200, max_new=120, arrivals_per_step=4)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_scheduler_prefix_cache_matches_model(seed):
+    """Shared prompt prefixes: forks from the cache, CoW copies of partial shared
+    tails, and eviction under pool pressure, decision for decision."""
+    steps, hits = run_trace(200 + seed, total_blocks=120, bs=16, max_running=8,
+                            max_step_tokens=128, chunk=48, watermark=2, n_req=40,
+                            max_prompt=150, max_new=30, arrivals_per_step=3, n_prefixes=3,
+                            max_cached=2)
+    assert hits > 0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_scheduler_prefix_cache_tight_pool(seed):
+    run_trace(300 + seed, total_blocks=40, bs=16, max_running=8, max_step_tokens=64, chunk=32,
+              watermark=0, n_req=30, max_prompt=200, max_new=60, arrivals_per_step=4,
+              n_prefixes=2, max_cached=4)
+
+
+def test_scheduler_prefix_hit_skips_the_prefix():
+    """The second request with a cached prefix starts its prefill at prefix_len on
+    a fork, and its first append into the shared partial block is a CoW copy."""
+    bm = kv.BlockManager(64, 16, 1, 8, 128)
+    s = kv.Scheduler(bm, 4, 256, 64, 0, max_cached_prefixes=2)
+    assert s.add_request(0, 60, 2, prefix_key=7, prefix_len=40)
+    p = s.step()  # request 0: chunk [0, 40) ends at the prefix and caches it
+    assert [(c[0], c[2], c[3]) for c in p["prefill"]] == [(0, 0, 40)] and p["cached"] == [7]
+    assert s.add_request(1, 50, 2, prefix_key=7, prefix_len=40)
+    p = s.step()  # request 0 continues; request 1 forks the (now ready) prefix
+    assert p["prefix_hits"] == [1]
+    chunks = {c[0]: (c[2], c[3]) for c in p["prefill"]}
+    assert chunks == {0: (40, 20), 1: (40, 10)}
+    # both append into block 2 of the prefix (rows 32..39 filled, shared by the
+    # cache entry, request 0 and request 1): each gets its own copy of 8 rows
+    assert sorted(c[2] for c in p["copies"]) == [8, 8]
+    assert not s.add_request(2, 40, 2, prefix_key=7, prefix_len=40)  # prefix must be shorter
+    assert not s.add_request(3, 50, 2, prefix_key=-1, prefix_len=10)
+    while p["running"] or p["waiting"]:
+        p = s.step()
+    assert p["cache_entries"] == 1
+    s.clear_prefix_cache()
+    assert bm.num_free_blocks() == 64
 
 
 def test_scheduler_preempts_in_tight_pool():
