@@ -245,6 +245,8 @@ def bench_contiguous(args, dev, kv, lib, info):
     if not args.no_serving:
         log("serving (scheduler-driven continuous batching) ...")
         result["serving"] = bench_serving(dev, kv, lib)
+        log("serving with a shared 1544-token prompt prefix and the prefix cache ...")
+        result["serving_shared_prefix"] = bench_serving(dev, kv, lib, shared_prefix=1544)
     if not args.no_weights:
         log("weights (.bin load) ...")
         result["weights"] = bench_weights(dev)
@@ -341,14 +343,16 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     return res
 
 
-def bench_serving(dev, kv, lib, steps=12, warmup=3):
+def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
     """Continuous batching through the Scheduler: configs[2]'s
     32 sequences (contexts uniform in [128, 8192]) decoding while a 2048-token prompt
     arrives every step and is prefilled in 512-token chunks under a 2048-token step
     budget. A step = the host plan (af_sched_step) + upload of slots / positions /
-    block tables / chunk descriptors + 28 layers of three launches: one paged append
-    for every new row (decode tokens and chunk tokens), decode attention for the
-    batch, and one batched prefill attention for all chunks."""
+    block tables / chunk descriptors / CoW copies + the copies + 28 layers of three
+    launches: one paged append for every new row (decode tokens and chunk tokens),
+    decode attention for the batch, and one batched prefill attention for all chunks.
+    With shared_prefix > 0 every arriving prompt starts with the same shared_prefix
+    tokens and the scheduler's prefix cache is on (4 entries)."""
     import atomflow_amd
     r = np.random.Generator(np.random.PCG64(0xA70F10 + 6))
     bs, chunk, budget, max_running = 16, 512, 2048, 64
@@ -366,7 +370,7 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3):
     atomflow_amd.check(lib.af_rt_fill_randn_f16(pool_buf.ptr, nbytes // 2, 7, 1.0, stream.handle))
     bm.attach_pool(pool_buf.ptr)
     pool = bm.pool()
-    sched = kv.Scheduler(bm, max_running, budget, chunk, 16)
+    sched = kv.Scheduler(bm, max_running, budget, chunk, 16, 4 if shared_prefix else 0)
     for i, c in enumerate(ctx):
         assert sched.add_request(i, int(c), old_gen)
     while True:  # host-only steps until the 32 contexts are in the cache and decoding
@@ -386,11 +390,19 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3):
     dev.synchronize()
     e0, e1 = dev.Event(), dev.Event()
     rec = []
+    arrived, ttft = {}, []  # steps from arrival to the first output token
     for k in range(warmup + steps):
         t0 = time.perf_counter()
-        sched.add_request(1000 + k, new_prompt, new_gen)
+        if shared_prefix:
+            sched.add_request(1000 + k, new_prompt, new_gen, 7, shared_prefix)
+        else:
+            sched.add_request(1000 + k, new_prompt, new_gen)
+        arrived[1000 + k] = k
         p = sched.step()
         t1 = time.perf_counter()
+        for c in p["prefill"]:
+            if c[4] and c[0] in arrived and arrived[c[0]] >= warmup:
+                ttft.append(k - arrived[c[0]] + 1)
         a = p["arrays"]
         nd = len(p["decode"])
         # host -> device: slots / positions of every new row, block tables, chunk descriptors
@@ -409,8 +421,15 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3):
             cb = [dev.DeviceBuffer.from_array(ctab), dev.DeviceBuffer.from_array(desc),
                   dev.DeviceBuffer.from_array(tmap)]
             bufs += cb
+        ncp = len(p["copies"])
+        if ncp:
+            cpb = [dev.DeviceBuffer.from_array(np.ascontiguousarray(a["copies"], np.int32)),
+                   dev.DeviceBuffer.from_array(np.array([ncp], np.int32))]
+            bufs += cpb
         n_rows = len(slots)
         e0.record(stream)
+        if ncp:  # copy-on-write of shared partial blocks, all layers, before the appends
+            kv.kv_copy_blocks(pool, cpb[0], cpb[1], ncp, stream)
         for l in range(LAYERS):
             q = qkv.ptr + l * rows * QKV * 2
             kv.launch_paged_rope_append(q, n_rows, pool, l, bufs[0], bufs[1], d_cos, d_sin,
@@ -429,22 +448,27 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3):
             b.free()
         if k >= warmup:
             rec.append((nd, sum(c[3] for c in p["prefill"]), nch, (t1 - t0) * 1e6,
-                        e0.elapsed_ms(e1), (t2 - t0) * 1e3))
+                        e0.elapsed_ms(e1), (t2 - t0) * 1e3, len(p["prefix_hits"]), ncp))
     rec = np.array(rec)
-    dec, pf, nch, plan_us, gpu_ms, wall_ms = rec.mean(axis=0)
+    dec, pf, nch, plan_us, gpu_ms, wall_ms, hits, ncopies = rec.mean(axis=0)
     res = {
         "workload": "configs[2] pool (bs 16, permuted free list), 32 sequences with contexts in "
                     "[128, 8192] decoding + one 2048-token prompt arriving per step, prefill chunk "
                     "512, step budget 2048 tokens, 28 layers x (one paged append for all new rows, "
                     "decode attention for the batch, one batched prefill attention for the "
-                    "chunks)",
+                    "chunks)" + (f"; every prompt shares its first {shared_prefix} tokens, prefix "
+                                 "cache of 4 entries" if shared_prefix else ""),
         "steps": steps, "decode_seqs_per_step": round(float(dec), 1),
         "prefill_tokens_per_step": round(float(pf), 1), "chunks_per_step": round(float(nch), 1),
         "host_plan_us": round(float(plan_us), 1), "gpu_ms_per_step": round(float(gpu_ms), 3),
         "wall_ms_per_step": round(float(wall_ms), 3),
         "tokens_per_s_gpu": round(float((dec + pf) / (gpu_ms * 1e-3)), 0),
         "decode_tokens_per_s_gpu": round(float(dec / (gpu_ms * 1e-3)), 0),
+        "steps_to_first_token": round(float(np.mean(ttft)), 2) if ttft else None,
     }
+    if shared_prefix:
+        res["prefix_hits_per_step"] = round(float(hits), 2)
+        res["cow_copies_per_step"] = round(float(ncopies), 2)
     for b in (pool_buf, d_cos, d_sin, qkv, out):
         b.free()
     sched.close()
