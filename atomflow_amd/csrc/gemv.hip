@@ -111,6 +111,40 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(
     }
 }
 
+// ---- two GEMVs of one activation in one launch (gate and up) -----------------
+// Blocks [0, blocks0) compute matrix 0, the rest matrix 1, with the plain
+// kernel's row mapping inside each: a row's arithmetic is the same as in
+// w8a16_gemv_kernel, so each output equals af_w8a16_gemv bit for bit.
+struct GemvPair {
+    const uint8_t* w[2];
+    const uint16_t* scales[2];
+    uint16_t* y[2];
+    int n[2];
+    int blocks0;
+};
+
+template <int RPW, int NCH>
+__global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_pair_kernel(
+    const GemvPair p, const uint16_t* __restrict__ x, int k, int group_size) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = int(blockIdx.x) >= p.blocks0 ? 1 : 0;
+    const int blk = int(blockIdx.x) - m * p.blocks0;
+    const int n = p.n[m];
+    const int row0 = (blk * kGemvWaves + wave) * RPW;
+    if (row0 >= n) return;
+    int rows[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rows[r] = min(row0 + r, n - 1);
+    float acc[RPW];
+    row_partials<RPW, NCH>(p.w[m], x, p.scales[m], rows, k, group_size, k / group_size, lane, acc);
+    uint16_t* y = p.y[m];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const float tot = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < n) y[row0 + r] = f2h(tot);
+    }
+}
+
 // ---- fused decode QKV projection + RoPE + KV append --------------------------
 // Output rows of qkv_out = [Q heads | K heads | V heads] x head_dim. Rotation
 // pairs are numbered p = head * HD/2 + d; wave w of block b takes pairs
@@ -209,20 +243,74 @@ void launch_gemv(int nch, hipStream_t s, const uint8_t* w, const uint16_t* x, co
                            sc, y, n, k, group_size);
 }
 
+// Rows per wave for n rows: the fewest whole rounds of one wave per SIMD with at
+// most 5 rows per wave, then rows spread evenly over those rounds (2..5).
+int rows_per_wave(int n) {
+    const int simds = 4 * device_compute_units();
+    const int rounds = std::max(1, (n + 5 * simds - 1) / (5 * simds));
+    return std::min(5, std::max(2, (n + simds * rounds - 1) / (simds * rounds)));
+}
+
+template <int RPW, int NCH>
+void launch_pair_nch(const GemvPair& p, const uint16_t* x, int k, int group_size, hipStream_t s) {
+    const int per_block = kGemvWaves * RPW;
+    GemvPair q = p;
+    q.blocks0 = (p.n[0] + per_block - 1) / per_block;
+    const int grid = q.blocks0 + (p.n[1] + per_block - 1) / per_block;
+    hipLaunchKernelGGL((w8a16_gemv_pair_kernel<RPW, NCH>), dim3(grid), dim3(kGemvThreads), 0, s,
+                       q, x, k, group_size);
+}
+
+template <int RPW>
+void launch_pair(int nch, const GemvPair& p, const uint16_t* x, int k, int group_size,
+                 hipStream_t s) {
+    if (nch == 3)
+        launch_pair_nch<RPW, 3>(p, x, k, group_size, s);
+    else if (nch == 8)
+        launch_pair_nch<RPW, 8>(p, x, k, group_size, s);
+    else
+        launch_pair_nch<RPW, 4>(p, x, k, group_size, s);
+}
+
 }  // namespace
 }  // namespace af
 
 using namespace af;
 
+extern "C" int af_w8a16_gemv_pair(const void* x, const uint8_t* weight0, const void* scales0,
+                                  void* y0, int n0, const uint8_t* weight1, const void* scales1,
+                                  void* y1, int n1, int k, int group_size, af_stream_t stream) {
+    if (int st = check_gemv_shape(x, weight0, scales0, n0, k, group_size)) return st;
+    if (int st = check_gemv_shape(x, weight1, scales1, n1, k, group_size)) return st;
+    if (!y0 || !y1) return AF_ERR_INVALID_ARG;
+    GemvPair p;
+    p.w[0] = weight0;
+    p.w[1] = weight1;
+    p.scales[0] = static_cast<const uint16_t*>(scales0);
+    p.scales[1] = static_cast<const uint16_t*>(scales1);
+    p.y[0] = static_cast<uint16_t*>(y0);
+    p.y[1] = static_cast<uint16_t*>(y1);
+    p.n[0] = n0;
+    p.n[1] = n1;
+    p.blocks0 = 0;
+    const int nch = chunks_per_pass(k);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* xw = static_cast<const uint16_t*>(x);
+    switch (rows_per_wave(n0 + n1)) {
+        case 2: launch_pair<2>(nch, p, xw, k, group_size, s); break;
+        case 3: launch_pair<3>(nch, p, xw, k, group_size, s); break;
+        case 4: launch_pair<4>(nch, p, xw, k, group_size, s); break;
+        default: launch_pair<5>(nch, p, xw, k, group_size, s); break;
+    }
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}
+
 extern "C" int af_w8a16_gemv(const void* x, const uint8_t* weight, const void* scales, void* y,
                              int n, int k, int group_size, af_stream_t stream) {
     if (int st = check_gemv_shape(x, weight, scales, n, k, group_size)) return st;
     if (!y) return AF_ERR_INVALID_ARG;
-    // Rows per wave: the fewest whole rounds of one wave per SIMD with at most
-    // 5 rows per wave, then rows spread evenly over those rounds (2..5).
-    const int simds = 4 * device_compute_units();
-    const int rounds = std::max(1, (n + 5 * simds - 1) / (5 * simds));
-    const int rpw = std::min(5, std::max(2, (n + simds * rounds - 1) / (simds * rounds)));
+    const int rpw = rows_per_wave(n);
     const int nch = chunks_per_pass(k);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto* xw = static_cast<const uint16_t*>(x);

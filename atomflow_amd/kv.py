@@ -61,6 +61,12 @@ def launch_w8a16_gemv(x, weight, scales, y, n, k, group_size=128, stream=None):
           "launch_w8a16_gemv")
 
 
+def launch_w8a16_gemv_pair(x, w0, s0, y0, n0, w1, s1, y1, n1, k, group_size=128, stream=None):
+    """y0 = W0 x and y1 = W1 x in one launch (gate and up), each as launch_w8a16_gemv."""
+    check(lib().af_w8a16_gemv_pair(_p(x), _p(w0), _p(s0), _p(y0), n0, _p(w1), _p(s1), _p(y1), n1,
+                                   k, group_size, _s(stream)), "launch_w8a16_gemv_pair")
+
+
 def launch_qkv_rope_append(x, w_qkv, scales, k, qkv_out, k_cache, v_cache, cos_table, sin_table,
                            pos, max_seq, n_q_heads, n_kv_heads, head_dim, group_size=128,
                            d_pos=None, d_status=None, stream=None):

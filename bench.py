@@ -247,6 +247,8 @@ def bench_contiguous(args, dev, kv, lib, info):
         result["serving"] = bench_serving(dev, kv, lib)
         log("serving with a shared 1544-token prompt prefix and the prefix cache ...")
         result["serving_shared_prefix"] = bench_serving(dev, kv, lib, shared_prefix=1544)
+    log("projection GEMVs ...")
+    result["gemv"] = bench_gemv(dev, kv, lib, args.steps, args.warmup)
     if not args.no_weights:
         log("weights (.bin load) ...")
         result["weights"] = bench_weights(dev)
@@ -280,21 +282,24 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
         e1.sync()
         return e0.elapsed_ms(e1) * 1e3 / reps
 
-    L = 8192
-    k = dev.DeviceBuffer(L * KV_DIM * 2)
-    v = dev.DeviceBuffer(L * KV_DIM * 2)
-    qkv = dev.DeviceBuffer(L * QKV * 2)
-    out = dev.DeviceBuffer(L * Q_DIM * 2)
+    L, LMAX = 8192, 16384
+    k = dev.DeviceBuffer(LMAX * KV_DIM * 2)
+    v = dev.DeviceBuffer(LMAX * KV_DIM * 2)
+    qkv = dev.DeviceBuffer(LMAX * QKV * 2)
+    out = dev.DeviceBuffer(LMAX * Q_DIM * 2)
     def randn(b, seed):
         atomflow_amd.check(lib.af_rt_fill_randn_f16(b.ptr, b.nbytes // 2, seed, 1.0, stream.handle))
 
     for i, b in enumerate((k, v, qkv)):
         randn(b, 0xA70F90 + i)
-    full = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, 0, L, L, L, NQ, NKV,
-                                               HD, stream=stream)
+
+    def prompt(lp):  # an lp-token prompt as one causal chunk
+        return lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, 0, lp, lp, LMAX,
+                                                   NQ, NKV, HD, stream=stream)
+    full = prompt(L)
     p0, n = 6144, 2048
-    chunk = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, p0, n, p0 + n, L, NQ,
-                                                NKV, HD, stream=stream)
+    chunk = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, p0, n, p0 + n, LMAX,
+                                                NQ, NKV, HD, stream=stream)
     bs = 16
     nblocks = L // bs
     pool_buf = dev.DeviceBuffer(2 * nblocks * bs * KV_DIM * 2)
@@ -316,16 +321,19 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     kv.build_rope_cache(cos, sin, L, HD, THETA)
     append = lambda: kv.launch_prefill_rope_append(qkv, n, k, v, cos, sin, p0, L, NQ, NKV, HD,
                                                    stream=stream)
-    us_full, us_chunk, us_paged, us_paged8, us_app = (
-        time_us(f) for f in (full, chunk, paged, paged8, append))
+    us_full, us_chunk, us_paged, us_paged8, us_app, us_2k, us_16k = (
+        time_us(f) for f in (full, chunk, paged, paged8, append, prompt(2048), prompt(LMAX)))
     tf = lambda fl, us: fl / (us * 1e-6) / 1e12
     f_full, f_chunk = prefill_flops(0, L, L), prefill_flops(p0, n, p0 + n)
+    f_2k, f_16k = prefill_flops(0, 2048, 2048), prefill_flops(0, LMAX, LMAX)
     app_bytes = n * (QKV * 2 * 2 + 2 * KV_DIM * 2)  # qkv rows read + written, K/V rows written
     res = {
-        "workload": "one layer, 24 Q / 8 KV heads x 128, fp16: 8192-token prompt as one causal "
-                    "chunk; 2048-token chunk at p0 6144 (contiguous, paged bs 16 with a "
+        "workload": "one layer, 24 Q / 8 KV heads x 128, fp16: 2048-, 8192- and 16384-token "
+                    "prompts, each as one causal chunk; 2048-token chunk at p0 6144 (contiguous, paged bs 16 with a "
                     "permuted block table, fp16 and FP8-E4M3 pools); 2048-row RoPE + append",
         "attn_8k_us": round(us_full, 1), "attn_8k_tflops": round(tf(f_full, us_full), 1),
+        "attn_2k_us": round(us_2k, 1), "attn_2k_tflops": round(tf(f_2k, us_2k), 1),
+        "attn_16k_us": round(us_16k, 1), "attn_16k_tflops": round(tf(f_16k, us_16k), 1),
         "chunk_2k_at_6k_us": round(us_chunk, 1),
         "chunk_2k_at_6k_tflops": round(tf(f_chunk, us_chunk), 1),
         "paged_chunk_2k_at_6k_us": round(us_paged, 1),
@@ -473,6 +481,79 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
         b.free()
     sched.close()
     bm.close()
+    return res
+
+
+def bench_gemv(dev, kv, lib, steps, warmup):
+    """The W8A16 projections either side of the path at the engine's shapes
+    (engine.cu:315-459), each timed as a graph of 28 launches over 28 layers'
+    weights: o_proj 3072 x 3072, gate and up 8192 x 3072 (two launches, and the
+    pair in one af_w8a16_gemv_pair launch), down 3072 x 8192. Algorithmic bytes
+    = E4M3 weights + fp16 group scales + activation in + output out."""
+    import atomflow_amd
+    FFN = 8192
+    stream = dev.Stream()
+    shapes = {"o_proj": (HIDDEN, HIDDEN), "gate": (FFN, HIDDEN), "up": (FFN, HIDDEN),
+              "down": (HIDDEN, FFN)}
+    bufs = {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        w = dev.DeviceBuffer(LAYERS * n * k)
+        sc = dev.DeviceBuffer(LAYERS * n * (k // 128) * 2)
+        atomflow_amd.check(lib.af_rt_fill_randn_fp8(w.ptr, w.nbytes, 0xA70FA0 + i, 20.0,
+                                                    stream.handle))
+        atomflow_amd.check(lib.af_rt_fill_randn_f16(sc.ptr, sc.nbytes // 2, 0xA70FB0 + i, 0.002,
+                                                    stream.handle))
+        bufs[name] = (w, sc)
+    x = dev.DeviceBuffer(LAYERS * FFN * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(x.ptr, x.nbytes // 2, 0xA70FC0, 1.0, stream.handle))
+    y = dev.DeviceBuffer(LAYERS * 2 * FFN * 2)
+    stream.sync()
+
+    def args(name, l):
+        n, k = shapes[name]
+        w, sc = bufs[name]
+        return (w.ptr + l * n * k, sc.ptr + l * n * (k // 128) * 2, n, k)
+
+    def single(name):
+        def run():
+            for l in range(LAYERS):
+                w, sc, n, k = args(name, l)
+                kv.launch_w8a16_gemv(x.ptr + l * FFN * 2, w, sc, y.ptr + l * 2 * FFN * 2, n, k,
+                                     stream=stream)
+        return run
+
+    def gate_up_two():
+        single("gate")()
+        single("up")()
+
+    def gate_up_pair():
+        for l in range(LAYERS):
+            wg, sg, n, k = args("gate", l)
+            wu, su, _, _ = args("up", l)
+            yl = y.ptr + l * 2 * FFN * 2
+            kv.launch_w8a16_gemv_pair(x.ptr + l * FFN * 2, wg, sg, yl, n, wu, su, yl + FFN * 2, n,
+                                      k, stream=stream)
+
+    fns = {"o_proj": single("o_proj"), "gate": single("gate"), "down": single("down"),
+           "gate_up_two_launches": gate_up_two, "gate_up_pair": gate_up_pair}
+    t = Timer(dev, stream, warmup)
+    res = {"workload": "W8A16 GEMV, E4M3 weights with fp16 scales per 128-group, fp16 in/out, "
+                       "28 layers' weights per graph (each launch reads its own layer's)"}
+    for name, fn in fns.items():
+        g = dev.Graph.capture(stream, fn)
+        us = t.graph_ms(g, steps) * 1e3 / LAYERS
+        g.destroy()
+        mats = {"gate_up_two_launches": ["gate", "up"], "gate_up_pair": ["gate", "up"]}.get(
+            name, [name])
+        nbytes = sum(shapes[m][0] * shapes[m][1] * (1 + 2 / 128) + shapes[m][1] * 2
+                     + shapes[m][0] * 2 for m in mats)
+        res[f"{name}_us"] = round(us, 3)
+        res[f"{name}_gbs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    for w, sc in bufs.values():
+        w.free()
+        sc.free()
+    x.free()
+    y.free()
     return res
 
 

@@ -224,6 +224,13 @@ int af_fp8_quantize(const void* src_f16, uint8_t* dst, size_t n, float scale, af
  * x and weight 16-byte aligned. */
 int af_w8a16_gemv(const void* x, const uint8_t* weight, const void* scales, void* y, int n, int k,
                   int group_size, af_stream_t stream);
+/* Two af_w8a16_gemv of the same activation in one launch: y0 = W0 x (n0 rows)
+ * and y1 = W1 x (n1 rows), each bit for bit the single call's output. For the
+ * MLP's gate and up projections, which the engine issues as two launches of
+ * launch_w8a16_gemv on the same input (src/core/engine.cu:418-436). */
+int af_w8a16_gemv_pair(const void* x, const uint8_t* weight0, const void* scales0, void* y0, int n0,
+                       const uint8_t* weight1, const void* scales1, void* y1, int n1, int k,
+                       int group_size, af_stream_t stream);
 
 /* Decode QKV projection, RoPE and KV append in one launch: af_w8a16_gemv of the
  * fused QKV weight into qkv_out ([Q | K | V] heads, the engine's layout,

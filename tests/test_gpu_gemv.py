@@ -47,6 +47,26 @@ def test_gemv_parity(gpu, n, k):
     assert np.all(np.abs(got - ref) <= fp16_ulp(y64) + 2 * bound)
 
 
+@pytest.mark.parametrize("n0,n1,k", [(8192, 8192, 3072), (37, 5120, 1040), (3072, 13, 8192)])
+def test_gemv_pair_equals_two_gemvs(gpu, n0, n1, k):
+    """af_w8a16_gemv_pair (gate and up in one launch): each output bit for bit the
+    single af_w8a16_gemv of its matrix, and within the oracle bound."""
+    say(f"gemv pair n0={n0} n1={n1} k={k}")
+    group = 128 if k % 128 == 0 else 16
+    w0, x, s0 = gemv_case(n0, k, 0xA70F20 + n0, group=group)
+    w1, _, s1 = gemv_case(n1, k, 0xA70F21 + n1, group=group)
+    y0, y1 = dev.DeviceBuffer(n0 * 2), dev.DeviceBuffer(n1 * 2)
+    kv.launch_w8a16_gemv_pair(up(x), up(w0), up(s0), y0, n0, up(w1), up(s1), y1, n1, k, group)
+    got0 = y0.download(np.float16, (n0,))
+    got1 = y1.download(np.float16, (n1,))
+    assert np.array_equal(got0.view(np.uint16), gemv_gpu(w0, x, s0, group).view(np.uint16))
+    assert np.array_equal(got1.view(np.uint16), gemv_gpu(w1, x, s1, group).view(np.uint16))
+    for w, s, got in ((w0, s0, got0), (w1, s1, got1)):
+        y64 = oracle.w8a16_gemv_f64(w, x, s, group)
+        bound = k * 2.0 ** -24 * gemv_abs_terms(w, x, s, group)
+        assert np.all(np.abs(got.astype(np.float64) - y64) <= 0.5 * fp16_ulp(y64) + bound)
+
+
 def test_gemv_identity_and_nan_codes(gpu):
     say("gemv identity weights, NaN code propagates to its row only")
     n = k = 1024
