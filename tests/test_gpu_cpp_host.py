@@ -1,0 +1,83 @@
+"""The C++ operator and memory API driven from a C++ host (tests/cpp/engine_step,
+built with the library): one contiguous decode step the way the reference
+engine issues it (launch_rope, launch_write_kv_cache, launch_cached_attention;
+src/core/engine.cu:326-370) and the sandbox's paged step (BlockManager fork +
+copy-on-write, launch_kv_copy_blocks, launch_paged_rope_append,
+launch_paged_attention). The program checks in itself that launch_rope_append
+equals the three-launch sequence bit for bit; here its outputs are checked
+against the oracle: append and copies bit-exact, attention within the
+north-star tolerance of the float64 oracle."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import HD, KV_DIM, NKV, NQ, Q_DIM, QKV, THETA, assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "tests", "cpp", "engine_step")
+MAX_SEQ, POS = 1024, 300
+
+
+def load(d, name, dtype, shape=None):
+    a = np.fromfile(os.path.join(d, name + ".bin"), dtype)
+    return a.reshape(shape) if shape is not None else a
+
+
+def test_cpp_host_decode_steps(gpu, tmp_path):
+    print("[case] C++ host: contiguous and paged decode step", flush=True)
+    assert os.path.exists(EXE), "tests/cpp/engine_step is built by the library's Makefile"
+    r = subprocess.run([EXE, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
+    d = str(tmp_path)
+
+    # contiguous: the engine's three launches at position POS
+    c, s = oracle.rope_table(MAX_SEQ, HD, THETA)
+    qkv = load(d, "c_qkv_in", np.float16)
+    k = load(d, "c_k_in", np.float16, (MAX_SEQ, KV_DIM)).copy()
+    v = load(d, "c_v_in", np.float16, (MAX_SEQ, KV_DIM)).copy()
+    roped = oracle.rope_append(qkv, k, v, c, s, POS, NQ, NKV, HD)
+    assert np.array_equal(load(d, "c_qkv_out", np.uint16), roped.view(np.uint16))
+    assert np.array_equal(load(d, "c_k_out", np.uint16, (MAX_SEQ, KV_DIM)), k.view(np.uint16))
+    assert np.array_equal(load(d, "c_v_out", np.uint16, (MAX_SEQ, KV_DIM)), v.view(np.uint16))
+    ref = oracle.cached_attention_f64(roped[:Q_DIM], k, v, POS + 1, NQ, NKV, HD)
+    assert_attn_close(load(d, "c_attn", np.float16), ref, what="C++ host contiguous step")
+
+    # paged: pool [K, V][blocks][16][kv_dim] for one layer
+    bs, total, max_pos = 16, 64, 512
+    pool = load(d, "p_pool_in", np.float16, (2, total * bs, KV_DIM)).copy()
+    copies = load(d, "p_copies", np.int32, (-1, 3))
+    assert len(copies) == 1
+    for src, dst, rows in copies:
+        pool[:, dst * bs:dst * bs + rows] = pool[:, src * bs:src * bs + rows]
+    tables = load(d, "p_tables", np.int32, (3, -1))
+    lens = load(d, "p_lens", np.int32)
+    slots = load(d, "p_slots", np.int64)
+    positions = load(d, "p_positions", np.int32)
+    qkv = load(d, "p_qkv_in", np.float16, (3, QKV))
+    c, s = oracle.rope_table(max_pos, HD, THETA)
+    got_attn = load(d, "p_attn", np.float16, (3, Q_DIM))
+    roped_rows = []
+    for b in range(3):
+        L, pos = int(lens[b]), int(positions[b])
+        assert L == pos + 1
+        rows = np.array([tables[b][t // bs] * bs + t % bs for t in range(L)])
+        assert rows[pos] == slots[b]
+        kseq = np.zeros((max_pos, KV_DIM), np.float16)
+        vseq = np.zeros((max_pos, KV_DIM), np.float16)
+        kseq[:pos] = pool[0, rows[:pos]]
+        vseq[:pos] = pool[1, rows[:pos]]
+        roped = oracle.rope_append(qkv[b], kseq, vseq, c, s, pos, NQ, NKV, HD)
+        roped_rows.append(roped)
+        ref = oracle.cached_attention_f64(roped[:Q_DIM], kseq, vseq, L, NQ, NKV, HD)
+        assert_attn_close(got_attn[b], ref, what=f"C++ host paged step, sequence {b}")
+        pool[0, slots[b]] = kseq[pos]
+        pool[1, slots[b]] = vseq[pos]
+    assert np.array_equal(load(d, "p_qkv_out", np.uint16, (3, QKV)),
+                          np.stack(roped_rows).view(np.uint16))
+    assert np.array_equal(load(d, "p_pool_out", np.uint16, (2, total * bs, KV_DIM)),
+                          pool.view(np.uint16))
