@@ -534,8 +534,45 @@ def bench_gemv(dev, kv, lib, steps, warmup):
             kv.launch_w8a16_gemv_pair(x.ptr + l * FFN * 2, wg, sg, yl, n, wu, su, yl + FFN * 2, n,
                                       k, stream=stream)
 
+    # batched QKV projection (one token per sequence of a serving step), weights 5120 x 3072
+    wq = dev.DeviceBuffer(LAYERS * QKV * HIDDEN)
+    sq = dev.DeviceBuffer(LAYERS * QKV * (HIDDEN // 128) * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_fp8(wq.ptr, wq.nbytes, 0xA70FD0, 20.0, stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(sq.ptr, sq.nbytes // 2, 0xA70FD1, 0.002,
+                                                stream.handle))
+    xb = dev.DeviceBuffer(LAYERS * 32 * HIDDEN * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(xb.ptr, xb.nbytes // 2, 0xA70FD2, 1.0,
+                                                stream.handle))
+    yb = dev.DeviceBuffer(LAYERS * 32 * QKV * 2)
+    gws = kv.GemmWorkspace(32, QKV, HIDDEN, stream=stream)
+    stream.sync()
+
+    def batched(m):
+        def run():
+            for l in range(LAYERS):
+                kv.launch_w8a16_gemm_batched(xb.ptr + l * 32 * HIDDEN * 2, HIDDEN, m,
+                                             wq.ptr + l * QKV * HIDDEN,
+                                             sq.ptr + l * QKV * (HIDDEN // 128) * 2,
+                                             yb.ptr + l * 32 * QKV * 2, QKV, QKV, HIDDEN, gws,
+                                             stream=stream)
+        return run
+
+    def per_token(m):  # the same projection as m single-token GEMVs
+        def run():
+            for l in range(LAYERS):
+                for i in range(m):
+                    kv.launch_w8a16_gemv(xb.ptr + (l * 32 + i) * HIDDEN * 2,
+                                         wq.ptr + l * QKV * HIDDEN,
+                                         sq.ptr + l * QKV * (HIDDEN // 128) * 2,
+                                         yb.ptr + (l * 32 + i) * QKV * 2, QKV, HIDDEN,
+                                         stream=stream)
+        return run
+
+    shapes["qkv"] = (QKV, HIDDEN)
     fns = {"o_proj": single("o_proj"), "gate": single("gate"), "down": single("down"),
-           "gate_up_two_launches": gate_up_two, "gate_up_pair": gate_up_pair}
+           "gate_up_two_launches": gate_up_two, "gate_up_pair": gate_up_pair,
+           "qkv_batched_m1": batched(1), "qkv_batched_m8": batched(8),
+           "qkv_batched_m32": batched(32), "qkv_per_token_gemv_m8": per_token(8)}
     t = Timer(dev, stream, warmup)
     res = {"workload": "W8A16 GEMV, E4M3 weights with fp16 scales per 128-group, fp16 in/out, "
                        "28 layers' weights per graph (each launch reads its own layer's)"}
@@ -544,16 +581,20 @@ def bench_gemv(dev, kv, lib, steps, warmup):
         us = t.graph_ms(g, steps) * 1e3 / LAYERS
         g.destroy()
         mats = {"gate_up_two_launches": ["gate", "up"], "gate_up_pair": ["gate", "up"]}.get(
-            name, [name])
-        nbytes = sum(shapes[m][0] * shapes[m][1] * (1 + 2 / 128) + shapes[m][1] * 2
-                     + shapes[m][0] * 2 for m in mats)
+            name, ["qkv"] if name.startswith("qkv") else [name])
+        tokens = int(name.rsplit("_m", 1)[1]) if name.startswith("qkv") else 1
+        nbytes = sum(shapes[m][0] * shapes[m][1] * (1 + 2 / 128)
+                     + tokens * (shapes[m][1] + shapes[m][0]) * 2 for m in mats)
         res[f"{name}_us"] = round(us, 3)
         res[f"{name}_gbs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    res["qkv_note"] = ("qkv_*: the 5120 x 3072 QKV projection of m tokens; batched = one "
+                       "af_w8a16_gemm_batched launch (weights read once), per_token = m "
+                       "af_w8a16_gemv launches; GB/s counts the weights once")
     for w, sc in bufs.values():
         w.free()
         sc.free()
-    x.free()
-    y.free()
+    for b in (x, y, wq, sq, xb, yb, gws.buf):
+        b.free()
     return res
 
 

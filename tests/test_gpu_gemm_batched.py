@@ -1,0 +1,119 @@
+"""GPU parity of the batched W8A16 projection (af_w8a16_gemm_batched) and the
+paged serving step's fused QKV projection + RoPE + paged append
+(af_paged_qkv_rope_append).
+
+Batched projection: every token row within half an fp16 ulp plus the fp32
+summation bound of the float64 oracle (the reference's per-token GEMV,
+qkv_gemm.cu:32-110), the same bar as af_w8a16_gemv. Fused kernel: bit for bit
+the batched projection followed by af_paged_rope_append, whole pool compared.
+"""
+import numpy as np
+import pytest
+
+import atomflow_amd
+import oracle
+from atomflow_amd import device as dev
+from atomflow_amd import kv
+from inputs import HD, KV_DIM, NKV, NQ, QKV, THETA, fp16_ulp, gemv_abs_terms, gemv_case
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def up(a):
+    return dev.DeviceBuffer.from_array(a)
+
+
+def batched_gpu(w, xs, s, group=128, x_stride=None):
+    n, k = w.shape
+    m = xs.shape[0]
+    stride = x_stride or k
+    xb = np.zeros((max(m, 1), stride), np.float16)
+    xb[:m, :k] = xs
+    y = dev.DeviceBuffer(max(m, 1) * n * 2)
+    ws = kv.GemmWorkspace(max(m, 1), n, k, group)
+    kv.launch_w8a16_gemm_batched(up(xb), stride, m, up(w), up(s), y, n, n, k, ws, group)
+    # twice: the first launch left the arrival counters re-armed
+    kv.launch_w8a16_gemm_batched(up(xb), stride, m, up(w), up(s), y, n, n, k, ws, group)
+    return y.download(np.float16, (max(m, 1), n))[:m]
+
+
+@pytest.mark.parametrize("n,k,m", [(QKV, 3072, 32), (QKV, 3072, 1), (3072, 3072, 7),
+                                   (8192, 3072, 45), (3072, 8192, 16), (100, 1024, 33)])
+def test_gemm_batched_parity(gpu, n, k, m):
+    say(f"batched gemm n={n} k={k} m={m}")
+    w, _, s = gemv_case(n, k, 0xA70F30 + n + k, group=128)
+    xs = np.random.default_rng(m + n).standard_normal((m, k)).astype(np.float16)
+    got = batched_gpu(w, xs, s, 128, x_stride=k + (8 if m % 2 else 0)).astype(np.float64)
+    assert np.all(np.isfinite(got))
+    for i in range(m):
+        y64 = oracle.w8a16_gemv_f64(w, xs[i], s, 128)
+        bound = k * 2.0 ** -24 * gemv_abs_terms(w, xs[i], s, 128)
+        err = np.abs(got[i] - y64)
+        assert np.all(err <= 0.5 * fp16_ulp(y64) + bound), f"token {i}: max err {err.max():.3e}"
+
+
+def test_gemm_batched_rejects_bad_shapes(gpu):
+    say("batched gemm argument checks")
+    w, x, s = gemv_case(64, 1024, 5)
+    lib = atomflow_amd.lib()
+    y = dev.DeviceBuffer(64 * 2)
+    dx, dw, ds = up(x), up(w), up(s)
+    ws = kv.GemmWorkspace(1, 64, 1024)
+    call = lib.af_w8a16_gemm_batched
+    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1000, 128, ws.ptr, ws.nbytes,
+                None) == atomflow_amd.AF_ERR_UNSUPPORTED
+    assert call(dx.ptr, 1000, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, ws.nbytes,
+                None) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, 1024,
+                None) == atomflow_amd.AF_ERR_WORKSPACE
+    assert call(dx.ptr, 1024, 0, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, ws.nbytes,
+                None) == 0
+    assert lib.af_gemm_batched_workspace_size(1, 64, 1000, 128) == 0
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
+    say(f"paged qkv rope append, fp8 {fp8}")
+    k_in, m, bs, total, max_pos = 3072, 19, 16, 96, 700
+    w, _, s = gemv_case(QKV, k_in, 0xA70F31, group=128)
+    xs = np.random.default_rng(3).standard_normal((m, k_in)).astype(np.float16)
+    r = np.random.default_rng(4)
+    slots = r.permutation(total * bs)[:m].astype(np.int64)
+    positions = r.integers(0, max_pos, m).astype(np.int32)
+    positions[5] = max_pos  # out of range: projection stays unrotated, nothing appended
+    esz = 1 if fp8 else 2
+    pool_bytes = 2 * 2 * total * bs * KV_DIM * esz  # two layers
+    init = r.integers(0, 256, pool_bytes, dtype=np.uint8)
+    scales = up(np.full((2, 2, NKV), 0.04, np.float32)) if fp8 else None
+    dtype = atomflow_amd.AF_KV_FP8_E4M3 if fp8 else atomflow_amd.AF_KV_FP16
+    pools = []
+    for _ in range(2):
+        buf = up(init)
+        pools.append((buf, kv.make_pool(buf, dtype, bs, 2, NKV, HD, total, scales)))
+    c, sn = oracle.rope_table(max_pos, HD, THETA)
+    d_c, d_s = up(c), up(sn)
+    dx, dw, ds = up(xs), up(w), up(s)
+    d_slots, d_pos = up(slots), up(positions)
+    # fused
+    q1 = dev.DeviceBuffer(m * QKV * 2)
+    st = up(np.zeros(1, np.int32))
+    ws = kv.GemmWorkspace(m, QKV, k_in)
+    kv.launch_paged_qkv_rope_append(dx, k_in, m, dw, ds, k_in, q1, pools[0][1], 1, d_slots,
+                                    d_pos, d_c, d_s, max_pos, NQ, ws, d_status=st)
+    # unfused: batched projection, then the paged append
+    q2 = dev.DeviceBuffer(m * QKV * 2)
+    kv.launch_w8a16_gemm_batched(dx, k_in, m, dw, ds, q2, QKV, QKV, k_in, ws)
+    kv.launch_paged_rope_append(q2, m, pools[1][1], 1, d_slots, d_pos, d_c, d_s, max_pos, NQ)
+    assert np.array_equal(q1.download(np.uint16, (m, QKV)), q2.download(np.uint16, (m, QKV)))
+    p1 = pools[0][0].download(np.uint8, (pool_bytes,))
+    p2 = pools[1][0].download(np.uint8, (pool_bytes,))
+    assert np.array_equal(p1, p2)
+    assert not np.array_equal(p1, init)  # something was appended
+    assert st.download(np.int32, (1,))[0] == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    # the out-of-range token's projection is unrotated: equal to the plain projection
+    plain = batched_gpu(w, xs, s)
+    assert np.array_equal(q1.download(np.uint16, (m, QKV))[5], plain[5].view(np.uint16))
