@@ -55,11 +55,8 @@ PROTOTYPES = {
     "af_kv_copy_blocks": (I, [PPOOL, P, P, I, P]),
     "af_fp8_quantize": (I, [P, P, SZ, F, P]),
     "af_w8a16_gemv": (I, [P, P, P, P, I, I, I, P]),
-    "af_gemm_batched_workspace_size": (SZ, [I, I, I, I]),
-    "af_gemm_batched_workspace_init": (I, [P, SZ, P]),
-    "af_w8a16_gemm_batched": (I, [P, I64, I, P, P, P, I64, I, I, I, P, SZ, P]),
-    "af_paged_qkv_rope_append": (I, [P, I64, I, P, P, I, I, P, P, I, P, P, P, P, I, I, P, P, SZ,
-                                     P]),
+    "af_w8a16_gemm_batched": (I, [P, I64, I, P, P, P, I64, I, I, I, P]),
+    "af_paged_qkv_rope_append": (I, [P, I64, I, P, P, I, I, P, P, I, P, P, P, P, I, I, P, P]),
     "af_w8a16_gemv_pair": (I, [P, P, P, P, I, P, P, P, I, I, I, P]),
     "af_qkv_rope_append": (I, [P, P, P, I, I, P, P, P, P, P, I, P, I, I, I, I, P, P]),
     "af_prefill_rope_append": (I, [P, I, P, P, P, P, I, P, I, I, I, I, P, P]),

@@ -12,24 +12,21 @@
 // af_paged_rope_append does on the projection's output.
 //
 // Design (HBM-bound: one weight byte per 2*M flops; M <= 32 per token tile):
-//  * D = X W^T on v_mfma_f32_32x32x16_f16. A = 32 tokens x 16 k of x, B = 16 k
-//    x 32 weight rows (E4M3 -> fp16 in registers with v_cvt_scalef32_pk_f16_fp8
-//    at scale 1, exact). Each lane loads 16 contiguous weight bytes per pair of
-//    MFMAs; the pair's k order is permuted identically on both operands.
+//  * D = X W^T on v_mfma_f32_32x32x16_f16. A = 32 tokens x 16 k of x (read
+//    from L2, tokens past m read as zero), B = 16 k x 32 weight rows (E4M3 ->
+//    fp16 in registers with v_cvt_scalef32_pk_f16_fp8 at scale 1, exact). A
+//    lane loads 16 contiguous weight bytes per pair of MFMAs; the pair's k
+//    order is permuted identically on both operands.
 //  * D's column is the lane's weight row, so a group scale is one value per
 //    lane: each group accumulates into a fresh fragment, then acc += scale * it.
-//  * A workgroup is 4 waves = 128 weight rows (one head of the fused QKV) x one
-//    of KS (<= 16) group-aligned slices of K of at most 512; the grid is row
-//    blocks x KS x token tiles,
-//    so every CU streams weights. The workgroup stages its x slice in LDS (rows
-//    padded by 16 B against bank conflicts) and keeps 8 weight loads in flight
-//    per wave.
-//  * Slices are combined by the last workgroup of a row block to arrive (the
-//    split-K protocol of the decode attention: agent-scope partial stores, one
-//    relaxed agent-scope counter increment, re-armed by the last arrival), in
-//    slice order, so results do not depend on timing. For the fused kernel the
-//    rotation partners (d, d + 64) of the head are exchanged through LDS and
-//    RoPE runs on the rounded fp16 projections.
+//  * A workgroup is 16 waves: two 32-row tiles x eight group-aligned parts of
+//    K. It owns its 64 rows' whole K, so no partial leaves the workgroup: the
+//    parts are summed through LDS in a fixed tree (results do not depend on
+//    timing) and the epilogue follows at once. Each wave keeps 8 weight loads
+//    (8 KB) in flight, 128 KB per workgroup.
+//  * For the fused kernel the two tiles are the rotation partners (d, d + 64)
+//    of one head, exchanged through LDS; RoPE runs on the rounded fp16
+//    projections.
 #include <algorithm>
 #include <cmath>
 
@@ -43,13 +40,12 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
 typedef float float16v_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBgWaves = 4;
-constexpr int kBgThreads = 64 * kBgWaves;
-constexpr int kBgTok = 32;          // tokens per token tile (one MFMA operand)
-constexpr int kBgRows = 64;         // weight rows per workgroup: two 32-row tiles
-constexpr int kBgDepth = 8;         // weight loads in flight per wave
-constexpr int kBgCounterBytes = 64 * 1024;
-constexpr int kBgMaxSliceK = 768;   // LDS: 32 x (768 + 8) fp16 + 10 KiB
+constexpr int kBgParts = 8;                 // K parts per workgroup
+constexpr int kBgWaves = 2 * kBgParts;       // two row tiles per part
+constexpr int kBgThreads = 64 * kBgWaves;    // 1024
+constexpr int kBgTok = 32;                   // tokens per token tile (one MFMA operand)
+constexpr int kBgRows = 64;                  // weight rows per workgroup
+constexpr int kBgDepth = 8;                  // weight loads in flight per wave
 
 struct BatchedArgs {
     const uint16_t* x;  // [m][x_stride] fp16
@@ -57,12 +53,9 @@ struct BatchedArgs {
     int m;
     const uint8_t* w;         // [n][k] E4M3
     const uint16_t* scales;   // [n][k / group_size] fp16
-    int n, k, group_size, groups, slices;
-    int slice_k;  // the widest slice's k extent
+    int n, k, group_size, groups;
     uint16_t* y;  // [m][y_stride] fp16 (fused: qkv_out)
     int64_t y_stride;
-    uint32_t* counters;  // [row blocks * token tiles]
-    float* part;         // [row blocks * token tiles][slices][4 waves][64 lanes][16]
     // fused paged QKV only
     int n_q_heads, n_kv_heads, head_dim;
     const float* cos_t;
@@ -102,59 +95,43 @@ __device__ __forceinline__ void rotate1(uint16_t x, uint16_t y, float c, float s
 
 template <bool FUSED, bool FP8>
 __global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const BatchedArgs a) {
-    // Dynamic LDS: the x slice [32 tokens][xs] fp16 (rows padded by 8 elements
-    // against bank conflicts).
-    extern __shared__ __align__(16) uint16_t s_x[];
-    __shared__ float s_red[2][16][64];   // the second k-half's fragments
-    __shared__ uint16_t s_y[16][64];     // fused: tile 1's rounded projections
-    __shared__ int s_last;
-    const int xs = a.slice_k + 8;
+    __shared__ float s_red[kBgParts][16][64];  // partial fragments, half the parts at a time
+    __shared__ uint16_t s_y[16][64];           // fused: tile 1's rounded projections
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int tile = wave & 1, khalf = wave >> 1;  // waves 0,1: first k-half; 2,3: second
+    const int tile = wave & 1, part = wave >> 1;
     const int col = lane & 31, hi = lane >> 5;
-    const int blk = int(blockIdx.x), slice = int(blockIdx.y), ttile = int(blockIdx.z);
-    const int t0 = ttile * kBgTok;
-    const int mt = min(kBgTok, a.m - t0);   // tokens of this tile
-    const int rmax = 4 * ((mt + 7) / 8);    // fragment registers holding them
+    const int blk = int(blockIdx.x), t0 = int(blockIdx.y) * kBgTok;
     // The workgroup's tiles: plain, rows [64 blk, +64); fused (head_dim 128),
     // rows d and d + 64 of one head for d in [32 j, 32 j + 32).
     const int c0 = FUSED ? (blk >> 1) * 128 + 32 * (blk & 1) : blk * kBgRows;
     const int c = c0 + tile * (FUSED ? 64 : 32);
     const int nrow = min(c + col, a.n - 1);  // clamped loads
+    const int tok = t0 + col;
+    const bool tok_live = tok < a.m;
 
-    const int g_lo = slice * a.groups / a.slices;
-    const int g_hi = (slice + 1) * a.groups / a.slices;
-    const int g_mid = g_lo + (g_hi - g_lo + 1) / 2;
-    const int k0 = g_lo * a.group_size;                       // the slice
-    const int kn = (g_hi - g_lo) * a.group_size;
-    const int wg_lo = khalf ? g_mid : g_lo, wg_hi = khalf ? g_hi : g_mid;  // this wave
-    const int iters = (wg_hi - wg_lo) * a.group_size / 32;
-    const uint8_t* wrow = a.w + size_t(nrow) * a.k + size_t(wg_lo) * a.group_size + 16 * hi;
+    const int g_lo = part * a.groups / kBgParts, g_hi = (part + 1) * a.groups / kBgParts;
+    const int iters = (g_hi - g_lo) * a.group_size / 32;
+    const int kbase = g_lo * a.group_size + 16 * hi;
+    const uint8_t* wrow = a.w + size_t(nrow) * a.k + kbase;
+    const uint16_t* xr = a.x + size_t(tok_live ? tok : 0) * a.x_stride + kbase;
 
-    // Weight loads first (they stream from HBM), then the x slice into LDS.
     uint4 wq[kBgDepth];
 #pragma unroll
     for (int i = 0; i < kBgDepth; ++i)
         if (i < iters) wq[i] = *reinterpret_cast<const uint4*>(wrow + 32 * i);
-    {
-        const int chunks = kn / 8;  // 16-byte chunks per token row
-        for (int e = tid; e < mt * chunks; e += kBgThreads) {
-            const int t = e / chunks, ch = e % chunks;
-            *reinterpret_cast<uint4*>(s_x + t * xs + 8 * ch) = *reinterpret_cast<const uint4*>(
-                a.x + size_t(t0 + t) * a.x_stride + k0 + 8 * ch);
-        }
+    const uint4 zero4 = {0u, 0u, 0u, 0u};
+    uint4 xa = zero4, xb = zero4;
+    if (tok_live && iters > 0) {
+        xa = *reinterpret_cast<const uint4*>(xr);
+        xb = *reinterpret_cast<const uint4*>(xr + 8);
     }
-    __syncthreads();
 
-    // Rows of s_x at or past mt are not written: their fragment rows are never
-    // used (a D row depends only on its own A row).
     float16v_t acc, f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = f[r] = 0.0f;
-    const uint16_t* xl = s_x + col * xs + (wg_lo - g_lo) * a.group_size + 16 * hi;
     const int per_group = a.group_size / 32;
     for (int it0 = 0; it0 < iters; it0 += kBgDepth) {
 #pragma unroll
@@ -162,15 +139,18 @@ __global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const Batched
             const int it = it0 + i;
             if (it < iters) {
                 const uint4 wv = wq[i];
+                const half8_t x0 = __builtin_bit_cast(half8_t, xa);
+                const half8_t x1 = __builtin_bit_cast(half8_t, xb);
                 if (it + kBgDepth < iters)  // refill the slot kBgDepth iterations ahead
                     wq[i] = *reinterpret_cast<const uint4*>(wrow + 32 * (it + kBgDepth));
-                const half8_t xa = *reinterpret_cast<const half8_t*>(xl + 32 * it);
-                const half8_t xb = *reinterpret_cast<const half8_t*>(xl + 32 * it + 8);
-                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa, e4m3x8(wv.x, wv.y), f, 0, 0, 0);
-                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(xb, e4m3x8(wv.z, wv.w), f, 0, 0, 0);
+                if (tok_live && it + 1 < iters) {  // the next iteration's activations
+                    xa = *reinterpret_cast<const uint4*>(xr + 32 * (it + 1));
+                    xb = *reinterpret_cast<const uint4*>(xr + 32 * (it + 1) + 8);
+                }
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, e4m3x8(wv.x, wv.y), f, 0, 0, 0);
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, e4m3x8(wv.z, wv.w), f, 0, 0, 0);
                 if ((it + 1) % per_group == 0) {  // group done: scale into the accumulator
-                    const int g = wg_lo + it / per_group;
-                    const float sc = h2f(a.scales[size_t(nrow) * a.groups + g]);
+                    const float sc = h2f(a.scales[size_t(nrow) * a.groups + g_lo + it / per_group]);
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         acc[r] = fmaf(sc, f[r], acc[r]);
@@ -180,73 +160,34 @@ __global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const Batched
             }
         }
     }
-    // The second k-half joins the first through LDS.
-    if (khalf) {
+
+    // Sum the parts: a fixed tree through LDS (parts p and p + h, h = 4, 2, 1).
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s_red[tile][r][lane] = acc[r];
-    }
-    __syncthreads();
-    if (!khalf) {
+    for (int h = kBgParts / 2; h >= 1; h >>= 1) {
+        if (part >= h && part < 2 * h) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += s_red[tile][r][lane];
+            for (int r = 0; r < 16; ++r) s_red[(part - h) * 2 + tile][r][lane] = acc[r];
+        }
+        __syncthreads();
+        if (part < h) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] += s_red[part * 2 + tile][r][lane];
+        }
+        __syncthreads();
     }
 
-    // ---- slices: the last workgroup of the row block to arrive sums them -----
-    const size_t rec = size_t(ttile) * gridDim.x + blk;
-    if (!khalf) {
-        float* my = a.part + ((rec * a.slices + slice) * 2 + tile) * 64 * 16 + lane * 16;
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-            if (r >= rmax) break;
-            // (built as a float2: composing the 64-bit value from the two vector
-            // elements with shifts compiled to one element stored twice)
-            const float2 pr = make_float2(acc[r], acc[r + 1]);
-            __hip_atomic_store(reinterpret_cast<uint64_t*>(my + r),
-                               __builtin_bit_cast(uint64_t, pr), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t* ctr = a.counters + rec;
-        const uint32_t prev =
-            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = prev == uint32_t(a.slices - 1);
-        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-
-    float v[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = 0.0f;
-    if (!khalf) {
-        for (int sl = 0; sl < a.slices; ++sl) {
-            const float* src = a.part + ((rec * a.slices + sl) * 2 + tile) * 64 * 16 + lane * 16;
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                if (r >= rmax) break;
-                const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(src + r),
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                v[r] += __builtin_bit_cast(float, uint32_t(u));
-                v[r + 1] += __builtin_bit_cast(float, uint32_t(u >> 32));
-            }
-        }
-    }
     // Register r of lane l: token t0 + 8(r/4) + 4(l/32) + r%4, weight row c + l%32.
     if constexpr (!FUSED) {
-        if (khalf) return;
+        if (part != 0) return;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if (t < a.m && c + col < a.n) a.y[size_t(t) * a.y_stride + c + col] = f2h(v[r]);
+            if (t < a.m && c + col < a.n) a.y[size_t(t) * a.y_stride + c + col] = f2h(acc[r]);
         }
     } else {
-        if (tile == 1 && !khalf) {
+        if (part == 0 && tile == 1) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s_y[r][lane] = f2h(v[r]);
+            for (int r = 0; r < 16; ++r) s_y[r][lane] = f2h(acc[r]);
         }
         __syncthreads();
         if (wave != 0) return;  // wave 0 finishes the pairs (d, d + 64)
@@ -260,7 +201,7 @@ __global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const Batched
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + 8 * (r >> 2) + 4 * hi + (r & 3);
             if (t >= a.m) continue;
-            const uint16_t y0 = f2h(v[r]), y1 = s_y[r][lane];
+            const uint16_t y0 = f2h(acc[r]), y1 = s_y[r][lane];
             uint16_t* yrow = a.y + size_t(t) * a.y_stride + size_t(head) * hd;
             const int pos = a.d_positions[t];
             const int64_t row = a.d_slots[t];
@@ -295,35 +236,18 @@ __global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const Batched
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Slices of K: the fewest whole-group slices of at most kBgMaxSliceK, at least
-// 4 when K allows (so the grid streams from every CU).
-int slices_for(int k, int group_size) {
-    const int groups = k / group_size;
-    const int per = std::max(1, kBgMaxSliceK / group_size);
-    return std::min(groups, std::max(4, (groups + per - 1) / per));
-}
-
-size_t part_bytes(int m, int n, int k, int group_size) {
-    const size_t recs = size_t((n + kBgRows - 1) / kBgRows) * ((m + kBgTok - 1) / kBgTok);
-    return recs * slices_for(k, group_size) * 2 * 64 * 16 * sizeof(float);
-}
-
 int check_batched(const void* x, int64_t x_stride, int m, const uint8_t* w, const void* scales,
-                  int n, int k, int group_size, const void* ws, size_t ws_bytes) {
-    if (!x || !w || !scales || !ws || m < 0 || n <= 0 || k <= 0 || group_size <= 0)
+                  int n, int k, int group_size) {
+    if (!x || !w || !scales || m < 0 || n <= 0 || k <= 0 || group_size <= 0)
         return AF_ERR_INVALID_ARG;
-    if (k % 32 || group_size % 32 || k % group_size || group_size > kBgMaxSliceK)
-        return AF_ERR_UNSUPPORTED;
+    if (k % 32 || group_size % 32 || k % group_size) return AF_ERR_UNSUPPORTED;
     if (x_stride < k || x_stride % 8) return AF_ERR_INVALID_ARG;
-    if (!aligned16(x) || !aligned16(w) || !aligned16(ws)) return AF_ERR_INVALID_ARG;
-    const size_t recs = size_t((n + kBgRows - 1) / kBgRows) * ((m + kBgTok - 1) / kBgTok);
-    if (recs * sizeof(uint32_t) > size_t(kBgCounterBytes)) return AF_ERR_UNSUPPORTED;
-    if (ws_bytes < kBgCounterBytes + part_bytes(m, n, k, group_size)) return AF_ERR_WORKSPACE;
+    if (!aligned16(x) || !aligned16(w)) return AF_ERR_INVALID_ARG;
     return AF_OK;
 }
 
 void fill_common(BatchedArgs& a, const void* x, int64_t x_stride, int m, const uint8_t* w,
-                 const void* scales, int n, int k, int group_size, void* ws) {
+                 const void* scales, int n, int k, int group_size) {
     a.x = static_cast<const uint16_t*>(x);
     a.x_stride = x_stride;
     a.m = m;
@@ -333,46 +257,26 @@ void fill_common(BatchedArgs& a, const void* x, int64_t x_stride, int m, const u
     a.k = k;
     a.group_size = group_size;
     a.groups = k / group_size;
-    a.slices = slices_for(k, group_size);
-    a.slice_k = (a.groups + a.slices - 1) / a.slices * group_size;
-    a.counters = static_cast<uint32_t*>(ws);
-    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kBgCounterBytes);
 }
-
-size_t lds_bytes(const BatchedArgs& a) { return size_t(kBgTok) * (a.slice_k + 8) * 2; }
 
 }  // namespace
 }  // namespace af
 
 using namespace af;
 
-extern "C" size_t af_gemm_batched_workspace_size(int m, int n, int k, int group_size) {
-    if (m <= 0 || n <= 0 || k <= 0 || group_size <= 0 || k % group_size) return 0;
-    return kBgCounterBytes + part_bytes(m, n, k, group_size);
-}
-
-extern "C" int af_gemm_batched_workspace_init(void* workspace, size_t workspace_bytes,
-                                              af_stream_t stream) {
-    if (!workspace || workspace_bytes < size_t(kBgCounterBytes)) return AF_ERR_INVALID_ARG;
-    return fill_u32(workspace, 0u, kBgCounterBytes / 4, static_cast<hipStream_t>(stream));
-}
-
 extern "C" int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, const uint8_t* weight,
                                      const void* scales, void* y, int64_t y_stride, int n, int k,
-                                     int group_size, void* workspace, size_t workspace_bytes,
-                                     af_stream_t stream) {
-    if (int st = check_batched(x, x_stride, m, weight, scales, n, k, group_size, workspace,
-                               workspace_bytes))
-        return st;
+                                     int group_size, af_stream_t stream) {
+    if (int st = check_batched(x, x_stride, m, weight, scales, n, k, group_size)) return st;
     if (!y || y_stride < n) return AF_ERR_INVALID_ARG;
     if (m == 0) return AF_OK;
     BatchedArgs a{};
-    fill_common(a, x, x_stride, m, weight, scales, n, k, group_size, workspace);
+    fill_common(a, x, x_stride, m, weight, scales, n, k, group_size);
     a.y = static_cast<uint16_t*>(y);
     a.y_stride = y_stride;
-    const dim3 grid((n + kBgRows - 1) / kBgRows, a.slices, (m + kBgTok - 1) / kBgTok);
-    hipLaunchKernelGGL((w8a16_batched_kernel<false, false>), grid, dim3(kBgThreads),
-                       lds_bytes(a), static_cast<hipStream_t>(stream), a);
+    const dim3 grid((n + kBgRows - 1) / kBgRows, (m + kBgTok - 1) / kBgTok);
+    hipLaunchKernelGGL((w8a16_batched_kernel<false, false>), grid, dim3(kBgThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -383,8 +287,7 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
                                         int layer, const int64_t* d_slots,
                                         const int32_t* d_positions, const float* cos_table,
                                         const float* sin_table, int max_pos, int n_q_heads,
-                                        int32_t* d_status, void* workspace,
-                                        size_t workspace_bytes, af_stream_t stream) {
+                                        int32_t* d_status, af_stream_t stream) {
     if (!pool || !pool->base || !qkv_out || !d_slots || !d_positions || !cos_table ||
         !sin_table || max_pos <= 0 || n_q_heads <= 0)
         return AF_ERR_INVALID_ARG;
@@ -396,16 +299,14 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
     const int hd = pool->head_dim;
     if (hd != 128) return AF_ERR_UNSUPPORTED;  // a workgroup's tiles are d and d + 64
     const int n = (n_q_heads + 2 * pool->n_kv_heads) * hd;
-    if (int st = check_batched(x, x_stride, m, w_qkv, scales, n, k, group_size, workspace,
-                               workspace_bytes))
-        return st;
+    if (int st = check_batched(x, x_stride, m, w_qkv, scales, n, k, group_size)) return st;
     if (m == 0) return AF_OK;
     const size_t esz = fp8 ? 1 : 2;
     const int kv_dim = pool->n_kv_heads * hd;
     const size_t slab = size_t(pool->total_blocks) * pool->block_size * kv_dim * esz;
     uint8_t* base = static_cast<uint8_t*>(pool->base);
     BatchedArgs a{};
-    fill_common(a, x, x_stride, m, w_qkv, scales, n, k, group_size, workspace);
+    fill_common(a, x, x_stride, m, w_qkv, scales, n, k, group_size);
     a.y = static_cast<uint16_t*>(qkv_out);
     a.y_stride = n;
     a.n_q_heads = n_q_heads;
@@ -424,13 +325,12 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
         a.v_scales = a.k_scales + pool->n_kv_heads;
     }
     a.d_status = d_status;
-    const dim3 grid(n / kBgRows, a.slices, (m + kBgTok - 1) / kBgTok);  // 2 per head
+    const dim3 grid(n / kBgRows, (m + kBgTok - 1) / kBgTok);  // two per head
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const size_t lds = lds_bytes(a);
     if (fp8)
-        hipLaunchKernelGGL((w8a16_batched_kernel<true, true>), grid, dim3(kBgThreads), lds, s, a);
+        hipLaunchKernelGGL((w8a16_batched_kernel<true, true>), grid, dim3(kBgThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((w8a16_batched_kernel<true, false>), grid, dim3(kBgThreads), lds, s, a);
+        hipLaunchKernelGGL((w8a16_batched_kernel<true, false>), grid, dim3(kBgThreads), 0, s, a);
     AF_TRY_LAUNCH();
     return AF_OK;
 }

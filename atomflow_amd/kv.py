@@ -67,39 +67,21 @@ def launch_w8a16_gemv_pair(x, w0, s0, y0, n0, w1, s1, y1, n1, k, group_size=128,
                                    k, group_size, _s(stream)), "launch_w8a16_gemv_pair")
 
 
-class GemmWorkspace:
-    """Caller-owned workspace of the batched projection (af_gemm_batched_workspace_*),
-    sized for m tokens of an n x k weight."""
-
-    def __init__(self, m, n, k, group_size=128, stream=None):
-        self.nbytes = int(lib().af_gemm_batched_workspace_size(m, n, k, group_size))
-        if not self.nbytes:
-            raise ValueError(f"bad batched-projection shape m={m} n={n} k={k} g={group_size}")
-        self.buf = DeviceBuffer(self.nbytes)
-        check(lib().af_gemm_batched_workspace_init(self.buf.ptr, self.nbytes, _s(stream)),
-              "af_gemm_batched_workspace_init")
-
-    @property
-    def ptr(self):
-        return self.buf.ptr
-
-
-def launch_w8a16_gemm_batched(x, x_stride, m, weight, scales, y, y_stride, n, k, ws,
-                              group_size=128, stream=None):
+def launch_w8a16_gemm_batched(x, x_stride, m, weight, scales, y, y_stride, n, k, group_size=128,
+                              stream=None):
     """y[i] = W x[i] for m tokens (rows x_stride / y_stride elements apart), one launch."""
     check(lib().af_w8a16_gemm_batched(_p(x), x_stride, m, _p(weight), _p(scales), _p(y), y_stride,
-                                      n, k, group_size, ws.ptr, ws.nbytes, _s(stream)),
-          "launch_w8a16_gemm_batched")
+                                      n, k, group_size, _s(stream)), "launch_w8a16_gemm_batched")
 
 
 def launch_paged_qkv_rope_append(x, x_stride, m, w_qkv, scales, k, qkv_out, pool, layer, d_slots,
-                                 d_positions, cos_table, sin_table, max_pos, n_q_heads, ws,
+                                 d_positions, cos_table, sin_table, max_pos, n_q_heads,
                                  group_size=128, d_status=None, stream=None):
     """Batched QKV projection + RoPE + paged append (af_paged_qkv_rope_append)."""
     check(lib().af_paged_qkv_rope_append(_p(x), x_stride, m, _p(w_qkv), _p(scales), k, group_size,
                                          _p(qkv_out), ctypes.byref(pool), layer, _p(d_slots),
                                          _p(d_positions), _p(cos_table), _p(sin_table), max_pos,
-                                         n_q_heads, _p(d_status), ws.ptr, ws.nbytes, _s(stream)),
+                                         n_q_heads, _p(d_status), _s(stream)),
           "launch_paged_qkv_rope_append")
 
 

@@ -544,7 +544,6 @@ def bench_gemv(dev, kv, lib, steps, warmup):
     atomflow_amd.check(lib.af_rt_fill_randn_f16(xb.ptr, xb.nbytes // 2, 0xA70FD2, 1.0,
                                                 stream.handle))
     yb = dev.DeviceBuffer(LAYERS * 32 * QKV * 2)
-    gws = kv.GemmWorkspace(32, QKV, HIDDEN, stream=stream)
     stream.sync()
 
     def batched(m):
@@ -553,7 +552,7 @@ def bench_gemv(dev, kv, lib, steps, warmup):
                 kv.launch_w8a16_gemm_batched(xb.ptr + l * 32 * HIDDEN * 2, HIDDEN, m,
                                              wq.ptr + l * QKV * HIDDEN,
                                              sq.ptr + l * QKV * (HIDDEN // 128) * 2,
-                                             yb.ptr + l * 32 * QKV * 2, QKV, QKV, HIDDEN, gws,
+                                             yb.ptr + l * 32 * QKV * 2, QKV, QKV, HIDDEN,
                                              stream=stream)
         return run
 
@@ -593,7 +592,7 @@ def bench_gemv(dev, kv, lib, steps, warmup):
     for w, sc in bufs.values():
         w.free()
         sc.free()
-    for b in (x, y, wq, sq, xb, yb, gws.buf):
+    for b in (x, y, wq, sq, xb, yb):
         b.free()
     return res
 

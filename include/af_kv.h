@@ -236,19 +236,12 @@ int af_w8a16_gemv_pair(const void* x, const uint8_t* weight0, const void* scales
  * launch: y[i] = af_w8a16_gemv(x[i]) for every token i, within the same fp32
  * summation bound (no counterpart in the reference, whose engine decodes one
  * token per step: launch_w8a16_gemv, qkv_gemm.cu:32-152; a serving step has one
- * token per sequence). k and group_size multiples of 32, group_size <= 1024;
- * x_stride >= k and a multiple of 8; x, weight and workspace 16-byte aligned.
- * Weights are read once per 32 tokens. The workspace (caller-owned,
- * af_gemm_batched_workspace_size(m, n, k, group_size) bytes, initialised once
- * with af_gemm_batched_workspace_init) holds the K-slice partials and arrival
- * counters; every launch leaves the counters at zero. Launches that may
- * overlap need different workspaces. */
-size_t af_gemm_batched_workspace_size(int m, int n, int k, int group_size);
-int af_gemm_batched_workspace_init(void* workspace, size_t workspace_bytes, af_stream_t stream);
+ * token per sequence). k and group_size multiples of 32; x_stride >= k and a
+ * multiple of 8; x and weight 16-byte aligned. Weights are read once per 32
+ * tokens. */
 int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, const uint8_t* weight,
                           const void* scales, void* y, int64_t y_stride, int n, int k,
-                          int group_size, void* workspace, size_t workspace_bytes,
-                          af_stream_t stream);
+                          int group_size, af_stream_t stream);
 
 /* The paged serving step's QKV projection + RoPE + KV append in one launch:
  * af_w8a16_gemm_batched of the fused QKV weight into qkv_out ([m][q_dim +
@@ -256,15 +249,13 @@ int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, const uint8_t*
  * d_positions, ...), the same outputs bit for bit (the paged form of
  * af_qkv_rope_append). A token whose position or slot is out of range gets its
  * unrotated projection in qkv_out, nothing in the pool, and AF_ERR_OUT_OF_RANGE
- * in *d_status (if given). head_dim 128; workspace as af_w8a16_gemm_batched's
- * for n = (n_q_heads + 2 n_kv_heads) * head_dim. */
+ * in *d_status (if given). head_dim 128. */
 int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m, const uint8_t* w_qkv,
                              const void* scales, int k, int group_size, void* qkv_out,
                              const af_kv_pool* pool, int layer, const int64_t* d_slots,
                              const int32_t* d_positions, const float* cos_table,
                              const float* sin_table, int max_pos, int n_q_heads,
-                             int32_t* d_status, void* workspace, size_t workspace_bytes,
-                             af_stream_t stream);
+                             int32_t* d_status, af_stream_t stream);
 
 /* Decode QKV projection, RoPE and KV append in one launch: af_w8a16_gemv of the
  * fused QKV weight into qkv_out ([Q | K | V] heads, the engine's layout,

@@ -34,10 +34,7 @@ def batched_gpu(w, xs, s, group=128, x_stride=None):
     xb = np.zeros((max(m, 1), stride), np.float16)
     xb[:m, :k] = xs
     y = dev.DeviceBuffer(max(m, 1) * n * 2)
-    ws = kv.GemmWorkspace(max(m, 1), n, k, group)
-    kv.launch_w8a16_gemm_batched(up(xb), stride, m, up(w), up(s), y, n, n, k, ws, group)
-    # twice: the first launch left the arrival counters re-armed
-    kv.launch_w8a16_gemm_batched(up(xb), stride, m, up(w), up(s), y, n, n, k, ws, group)
+    kv.launch_w8a16_gemm_batched(up(xb), stride, m, up(w), up(s), y, n, n, k, group)
     return y.download(np.float16, (max(m, 1), n))[:m]
 
 
@@ -62,17 +59,14 @@ def test_gemm_batched_rejects_bad_shapes(gpu):
     lib = atomflow_amd.lib()
     y = dev.DeviceBuffer(64 * 2)
     dx, dw, ds = up(x), up(w), up(s)
-    ws = kv.GemmWorkspace(1, 64, 1024)
     call = lib.af_w8a16_gemm_batched
-    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1000, 128, ws.ptr, ws.nbytes,
+    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1000, 128,
                 None) == atomflow_amd.AF_ERR_UNSUPPORTED
-    assert call(dx.ptr, 1000, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, ws.nbytes,
+    assert call(dx.ptr, 1000, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128,
                 None) == atomflow_amd.AF_ERR_INVALID_ARG
-    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, 1024,
-                None) == atomflow_amd.AF_ERR_WORKSPACE
-    assert call(dx.ptr, 1024, 0, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, ws.ptr, ws.nbytes,
-                None) == 0
-    assert lib.af_gemm_batched_workspace_size(1, 64, 1000, 128) == 0
+    assert call(dx.ptr, 1024, 1, dw.ptr, ds.ptr, y.ptr, 32, 64, 1024, 128,
+                None) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert call(dx.ptr, 1024, 0, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, None) == 0
 
 
 @pytest.mark.parametrize("fp8", [False, True])
@@ -101,12 +95,11 @@ def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
     # fused
     q1 = dev.DeviceBuffer(m * QKV * 2)
     st = up(np.zeros(1, np.int32))
-    ws = kv.GemmWorkspace(m, QKV, k_in)
     kv.launch_paged_qkv_rope_append(dx, k_in, m, dw, ds, k_in, q1, pools[0][1], 1, d_slots,
-                                    d_pos, d_c, d_s, max_pos, NQ, ws, d_status=st)
+                                    d_pos, d_c, d_s, max_pos, NQ, d_status=st)
     # unfused: batched projection, then the paged append
     q2 = dev.DeviceBuffer(m * QKV * 2)
-    kv.launch_w8a16_gemm_batched(dx, k_in, m, dw, ds, q2, QKV, QKV, k_in, ws)
+    kv.launch_w8a16_gemm_batched(dx, k_in, m, dw, ds, q2, QKV, QKV, k_in)
     kv.launch_paged_rope_append(q2, m, pools[1][1], 1, d_slots, d_pos, d_c, d_s, max_pos, NQ)
     assert np.array_equal(q1.download(np.uint16, (m, QKV)), q2.download(np.uint16, (m, QKV)))
     p1 = pools[0][0].download(np.uint8, (pool_bytes,))
