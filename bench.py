@@ -844,7 +844,7 @@ def main():
     if args.config == 2:
         result = bench_contiguous(args, dev, kv, lib, info)
         if not args.no_cpu:
-            log("cpu baseline (scalar oracle, 1 thread) ...")
+            log("cpu baseline (C++ oracle, threaded and 1 thread) ...")
             result["cpu_baseline"] = cpu_baseline(args.ctx)
     else:
         result = bench_paged(args, dev, kv, lib, info)
