@@ -110,3 +110,42 @@ def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
     # the out-of-range token's projection is unrotated: equal to the plain projection
     plain = batched_gpu(w, xs, s)
     assert np.array_equal(q1.download(np.uint16, (m, QKV))[5], plain[5].view(np.uint16))
+
+
+def test_paged_qkv_rope_append_graph_replays(gpu):
+    """Captured in a hipGraph and replayed three times (device positions advanced
+    between replays by the eager side): every replay equals the eager launch."""
+    say("paged qkv rope append under graph replay")
+    k_in, m, bs, total, max_pos = 3072, 8, 16, 64, 256
+    w, _, s = gemv_case(QKV, k_in, 0xA70F32, group=128)
+    xs = np.random.default_rng(6).standard_normal((m, k_in)).astype(np.float16)
+    slots = np.arange(m, dtype=np.int64) * 5
+    c, sn = oracle.rope_table(max_pos, HD, THETA)
+    d_c, d_s = up(c), up(sn)
+    dx, dw, ds = up(xs), up(w), up(s)
+    pool_bytes = 2 * total * bs * KV_DIM * 2
+    bufs = [dev.DeviceBuffer(pool_bytes) for _ in range(2)]
+    for b in bufs:
+        b.fill_u32(0, None)
+    dev.synchronize()
+    pools = [kv.make_pool(b, atomflow_amd.AF_KV_FP16, bs, 1, NKV, HD, total) for b in bufs]
+    outs = [dev.DeviceBuffer(m * QKV * 2) for _ in range(2)]
+    d_slots = up(slots)
+    d_pos = [up(np.zeros(m, np.int32)) for _ in range(2)]
+    stream = dev.Stream()
+    run = lambda i: kv.launch_paged_qkv_rope_append(dx, k_in, m, dw, ds, k_in, outs[i], pools[i],
+                                                    0, d_slots, d_pos[i], d_c, d_s, max_pos, NQ,
+                                                    stream=stream)
+    graph = dev.Graph.capture(stream, lambda: run(1))
+    for step in range(3):
+        pos = (np.arange(m) * 7 + 11 * step).astype(np.int32)
+        for dp in d_pos:
+            dp.upload(pos)
+        run(0)
+        graph.launch(stream)
+        stream.sync()
+        assert np.array_equal(outs[0].download(np.uint16, (m, QKV)),
+                              outs[1].download(np.uint16, (m, QKV))), f"replay {step}"
+        assert np.array_equal(bufs[0].download(np.uint8, (pool_bytes,)),
+                              bufs[1].download(np.uint8, (pool_bytes,))), f"replay {step}"
+    graph.destroy()
