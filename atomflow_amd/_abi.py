@@ -51,6 +51,10 @@ PROTOTYPES = {
     "af_kv_pool_bytes": (SZ, [PPOOL]),
     "af_paged_rope_append": (I, [P, I, PPOOL, I, P, P, P, P, I, I, P]),
     "af_paged_attention": (I, [P, I, PPOOL, I, P, I, P, I, I, P, I, I, I, P, SZ, P]),
+    "af_paged_attention_shared_prefix": (I, [P, I, PPOOL, I, P, I, I, P, I, P, I, I, P, I, I, I,
+                                             P, SZ, P]),
+    "af_paged_decode_fused_shared_prefix": (I, [P, I, PPOOL, I, P, P, P, P, I, P, I, I, P, I, I,
+                                                P, I, I, I, P, SZ, P]),
     "af_paged_gather": (I, [PPOOL, I, P, I, P, P, P]),
     "af_kv_copy_blocks": (I, [PPOOL, P, P, I, P]),
     "af_fp8_quantize": (I, [P, P, SZ, F, P]),

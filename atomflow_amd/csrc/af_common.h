@@ -86,4 +86,36 @@ int default_span(int batch, int n_kv_heads);
 // Fill kernel launcher shared by the runtime ABI and workspace init.
 int fill_u32(void* dst, uint32_t value, size_t n_words, hipStream_t stream);
 
+// Shared-prefix partials of paged decode attention: the matrix-core prefill
+// kernel attends the decode queries of `batch` sequences (packed per KV head:
+// the `group` Q heads of every sequence) over rows [0, prefix_len) of one block
+// table, in key_splits key ranges, and writes split s of (sequence, KV head)
+// to split-K record s (records rec_stride apart, the decode kernel's layout).
+// head_dim 128. With cos_t the queries are rotated (RoPE) at positions[b].
+struct PrefixPartialArgs {
+    const uint16_t* q;  // row b at q + b * q_stride, Q head h at + h * 128
+    int64_t q_stride;
+    const uint8_t* k;   // the layer's K / V slabs
+    const uint8_t* v;
+    int64_t row_bytes;  // n_kv_heads * 128 * element size
+    const float* scales;  // FP8 pools: this layer's [2][n_kv_heads]; NULL for fp16
+    const int32_t* table;
+    int bs_log2;
+    int prefix_len;
+    int batch;
+    int n_kv_heads;
+    int group;
+    int key_splits;
+    int rec_stride;
+    float* part_o;
+    float* part_ml;
+    const float* cos_t;
+    const float* sin_t;
+    const int32_t* positions;
+    int max_pos;
+};
+// Workgroups of the partial launch per key split.
+int prefix_partial_tiles(int batch, int group, int n_kv_heads);
+int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream);
+
 }  // namespace af

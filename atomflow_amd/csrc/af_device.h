@@ -40,6 +40,21 @@ __device__ __forceinline__ uint32_t quantize_fp8(uint16_t h, float scale) {
     return e4m3_encode(v);
 }
 
+// RoPE rotation of one fp16 pair (x, y) by (c, s): separately rounded fp32
+// products and sums, then fp16 round-to-nearest-even (the reference's
+// rope_kernel arithmetic, src/kernel/rope.cu:34-35; no FMA contraction).
+__device__ __forceinline__ void rope_rotate(uint16_t x, uint16_t y, float c, float s, uint16_t& xo,
+                                            uint16_t& yo) {
+#pragma clang fp contract(off)
+    const float xf = h2f(x), yf = h2f(y);
+    const float xc = xf * c;
+    const float ys = yf * s;
+    const float xs = xf * s;
+    const float yc = yf * c;
+    xo = f2h(xc - ys);
+    yo = f2h(xs + yc);
+}
+
 // 2^x on v_exp_f32 (1 ulp; flushes below 2^-126, 2^-inf = 0).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -25,6 +25,7 @@
 //    counter, so the kernel is one launch and replays inside a hipGraph.
 //  * Paged: the split's block-table entries are staged in LDS once; rows are
 //    addressed block * block_size + (t mod block_size) within the layer slab.
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <vector>
@@ -112,9 +113,16 @@ struct AttnArgs {
     int32_t span_tokens;  // target tokens per split: a sequence uses ceil(L / span) splits
     float qk_scale;       // log2(e) / sqrt(head_dim)
     const float* scales;  // FP8: [2][n_kv_heads] (K, V) of this layer
-    float* part_o;        // [batch][n_kv_heads][splits][GROUP * head_dim]
-    float* part_ml;       // [batch][n_kv_heads][splits][2 * GROUP]  (m..., l...)
+    float* part_o;        // [batch][n_kv_heads][rec_stride][GROUP * head_dim]
+    float* part_ml;       // [batch][n_kv_heads][rec_stride][2 * GROUP]  (m..., l...)
     uint32_t* counters;   // [batch][n_kv_heads]
+    // Shared prefix: rows [0, row_start) of every sequence are covered by
+    // pre_records partials already in records 0 .. pre_records-1 (written by an
+    // earlier launch); the splits cover rows [row_start, L) and write records
+    // pre_records + split. rec_stride = records per (sequence, KV head).
+    int32_t row_start;
+    int32_t pre_records;
+    int32_t rec_stride;
 };
 
 template <int HD, bool FP8>
@@ -216,18 +224,24 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
-    // Balanced partition in whole workgroup steps (kStepTokens rows): a
-    // sequence of C steps uses n = min(num_splits, ceil(C / span)) splits and
-    // split s owns steps [s*C/n, (s+1)*C/n).
-    const int total_steps = (L + kStepTokens - 1) / kStepTokens;
+    // Balanced partition of rows [t_lo, L) in whole workgroup steps
+    // (kStepTokens rows): C steps use n = min(num_splits, ceil(C / span)) splits
+    // and split s owns steps [s*C/n, (s+1)*C/n). t_lo = row_start, the first row
+    // after a shared prefix (0 without one). A sequence no longer than the
+    // prefix gets one split over its last row with every row masked (an empty
+    // partial), so the combine still runs over the prefix records.
+    const int t_lo = min(a.row_start, L - 1);
+    const int total_steps = (L - t_lo + kStepTokens - 1) / kStepTokens;
     const int span_steps = max(1, a.span_tokens / kStepTokens);
     const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
     if (split >= n_active) return;
     const int step_begin = int(int64_t(split) * total_steps / n_active);
     const int step_end = int(int64_t(split + 1) * total_steps / n_active);
-    const int t_begin = step_begin * kStepTokens;
-    const int t_end = min(L, step_end * kStepTokens);
+    const int t_begin = t_lo + step_begin * kStepTokens;
+    const int t_end = min(L, t_lo + step_end * kStepTokens);
+    const int t_valid = L > a.row_start ? t_end : t_begin;  // rows below t_valid are scored
     const int n_steps = step_end - step_begin;  // >= 1
+    const bool direct = n_active == 1 && a.pre_records == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -247,9 +261,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 
     const uint8_t* kbase = a.k + size_t(h) * LY::kRowBytes + j * 16;
     const uint8_t* vbase = a.v + size_t(h) * LY::kRowBytes + j * 16;
-    // Rows that may be read from memory: [0, L) unfused; [0, L-1) fused (row
-    // L-1 is the token being appended and comes from LDS).
-    const int last_row = FUSED ? max(L - 2, 0) : L - 1;
+    // Rows that may be read from memory: [t_begin, L) unfused; [t_begin, L-1)
+    // fused (row L-1 is the token being appended and comes from LDS). A fused
+    // split that starts at row L-1 reads row t_begin (staged, discarded): the
+    // row clamp never leaves the split's staged block-table window.
+    const int last_row = FUSED ? max(L - 2, t_begin) : L - 1;
     // Token of this lane in step s: waves interleave 8-row slices of each step.
     const int lane_t0 = t_begin + wave * kRowsPerStep + g;
 
@@ -456,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                 }
             }
         }
-        const bool valid = t < t_end;
+        const bool valid = t < t_valid;
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh) {
             const float x = group8_sum(s[gh]) * qk_scale;
@@ -577,7 +593,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 
     // ---- merge the partials: the output, or this split's partial ------------
     // Thread t owns head-dim pair (2t, 2t+1).
-    const size_t rec = (size_t(b) * nkv + h) * a.num_splits;  // first record of (b, h)
+    const size_t rec = (size_t(b) * nkv + h) * a.rec_stride;  // first record of (b, h)
+    const size_t own = rec + a.pre_records + split;            // this split's record
     for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
         const int gh = (2 * q2) / HD;
         float M = -INFINITY;
@@ -592,22 +609,22 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             o0 += f * v.x;
             o1 += f * v.y;
         }
-        if (n_active == 1) {
+        if (direct) {
             const uint32_t pair = uint32_t(__builtin_bit_cast(uint16_t, f16(o0 * v_scale / lsum))) |
                                   (uint32_t(__builtin_bit_cast(uint16_t, f16(o1 * v_scale / lsum))) << 16);
             *reinterpret_cast<uint32_t*>(out_b + 2 * q2) = pair;
         } else {  // the partial, as 64-bit agent-scope stores
             const uint64_t v = uint64_t(__builtin_bit_cast(uint32_t, o0 * v_scale)) |
                                (uint64_t(__builtin_bit_cast(uint32_t, o1 * v_scale)) << 32);
-            __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_o + (rec + split) * GHD) + q2, v,
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_o + own * GHD) + q2, v,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if ((2 * q2) % HD == 0) {
-                store_agent(a.part_ml + (rec + split) * 2 * GROUP + gh, M);
-                store_agent(a.part_ml + (rec + split) * 2 * GROUP + GROUP + gh, lsum);
+                store_agent(a.part_ml + own * 2 * GROUP + gh, M);
+                store_agent(a.part_ml + own * 2 * GROUP + GROUP + gh, lsum);
             }
         }
     }
-    if (n_active == 1) {
+    if (direct) {
         if constexpr (FUSED) {  // the only reader of Q heads h*GROUP.. : rotate in place now
             uint16_t* qd = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
             for (int o = tid; o < GHD; o += kThreads) qd[o] = s_q[o];
@@ -643,7 +660,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // flight.
     constexpr int CB = 16;  // splits per batch
     constexpr int MLPT = (2 * GROUP * kMaxSplits + kThreads - 1) / kThreads;
-    const int n_ml = n_active * 2 * GROUP;
+    const int n_rec = a.pre_records + n_active;  // shared-prefix records, then the splits'
+    const int n_ml = n_rec * 2 * GROUP;
     const float* ml = a.part_ml + rec * 2 * GROUP;
     const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + rec * GHD);
     float mlv[MLPT];
@@ -656,7 +674,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     auto issue = [&](int q2, int base) {
 #pragma unroll
         for (int k = 0; k < CB; ++k)
-            val[k] = __hip_atomic_load(po + size_t(min(base + k, n_active - 1)) * (GHD / 2) + q2,
+            val[k] = __hip_atomic_load(po + size_t(min(base + k, n_rec - 1)) * (GHD / 2) + q2,
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     issue(min(tid, GHD / 2 - 1), 0);
@@ -669,20 +687,20 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s, one wave per head
     for (int gh = wave; gh < GROUP; gh += kWaves) {
         float mx = -INFINITY;
-        for (int sp = lane; sp < n_active; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
+        for (int sp = lane; sp < n_rec; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
         mx = wave_max(mx);
         float ls = 0.f;
-        for (int sp = lane; sp < n_active; sp += 64)
+        for (int sp = lane; sp < n_rec; sp += 64)
             ls += fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * s_ml[sp * 2 * GROUP + GROUP + gh];
         const float inv = 1.0f / wave_sum(ls);
-        for (int sp = lane; sp < n_active; sp += 64)
+        for (int sp = lane; sp < n_rec; sp += 64)
             s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * inv;
     }
     __syncthreads();
     for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
         const int gh = (2 * q2) / HD;
         float r0 = 0.f, r1 = 0.f;
-        for (int base = 0; base < n_active; base += CB) {
+        for (int base = 0; base < n_rec; base += CB) {
             if (base > 0 || q2 != tid) issue(q2, base);
 #pragma unroll
             for (int k4 = 0; k4 < CB; k4 += 4) {
@@ -690,7 +708,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                 const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    if (base + k4 + u < n_active) {
+                    if (base + k4 + u < n_rec) {
                         const uint64_t v = val[k4 + u];
                         r0 = fmaf(wk[u], __builtin_bit_cast(float, uint32_t(v)), r0);
                         r1 = fmaf(wk[u], __builtin_bit_cast(float, uint32_t(v >> 32)), r1);
@@ -926,6 +944,7 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.counters = w.counters;
+    a.rec_stride = num_splits;
     return dispatch(a, head_dim, n_q_heads / n_kv_heads, false, false, fused,
                     num_splits * n_kv_heads, stream);
 }
@@ -982,13 +1001,29 @@ extern "C" int af_cached_attention(const void* q, const void* k_cache, const voi
                                   bytes, stream);
 }
 
+// Rows [0, len) shared by every sequence of a launch, mapped by `table`.
+struct SharedPrefix {
+    const int32_t* table = nullptr;
+    int len = 0;
+    int splits = 0;  // key splits of the prefix launch; 0 = default
+};
+
+// Default key splits of the shared-prefix launch: about one workgroup per CU,
+// at least one 64-key tile per split.
+static int default_prefix_splits(int prefix_len, int batch, int group, int n_kv_heads) {
+    const int per_split = std::max(1, prefix_partial_tiles(batch, group, n_kv_heads));
+    int s = std::max(1, device_compute_units() / per_split);
+    return std::min(std::min(s, 32), ceil_div(prefix_len, 64));
+}
+
 static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int layer,
                            const int32_t* d_block_tables, int max_blocks_per_seq,
                            const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,
                            int out_stride, int n_q_heads, int num_splits, void* workspace,
                            size_t workspace_bytes, bool fused, const int64_t* d_slots,
                            const int32_t* d_positions, const float* cos_table,
-                           const float* sin_table, int max_pos, hipStream_t stream) {
+                           const float* sin_table, int max_pos, hipStream_t stream,
+                           const SharedPrefix& prefix = SharedPrefix()) {
     if (!q || !pool || !pool->base || !d_block_tables || !out || batch < 0 || max_seq_len < 0 ||
         max_blocks_per_seq <= 0)
         return AF_ERR_INVALID_ARG;
@@ -1007,20 +1042,46 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     if (q_stride < n_q_heads * hd || out_stride < n_q_heads * hd) return AF_ERR_INVALID_ARG;
     if (!aligned16(q) || !aligned16(pool->base) || (q_stride % 8)) return AF_ERR_INVALID_ARG;
     if (int64_t(max_blocks_per_seq) * bs < max_seq_len) return AF_ERR_OUT_OF_RANGE;
+    if (prefix.len < 0 || prefix.splits < 0) return AF_ERR_INVALID_ARG;
+    if (prefix.len > 0) {
+        if (!prefix.table) return AF_ERR_INVALID_ARG;
+        if (hd != 128) return AF_ERR_UNSUPPORTED;
+        if (int64_t(max_blocks_per_seq) * bs < prefix.len) return AF_ERR_OUT_OF_RANGE;
+        if (prefix.splits > ceil_div(prefix.len, 64)) return AF_ERR_INVALID_ARG;
+    }
     if (batch == 0) return AF_OK;
     if (int64_t(batch) * nkv > kMaxCounters) return AF_ERR_UNSUPPORTED;
-    const int min_sp = min_splits_for_table(std::max(max_seq_len, 1), bs);
+    // The splits cover the rows after the prefix (at least one row each).
+    const int suffix_max = std::max(max_seq_len - prefix.len, 1);
+    const int min_sp = min_splits_for_table(suffix_max, bs);
     int span = kMinSpan;
     if (num_splits <= 0) {
-        num_splits = std::max(default_splits(max_seq_len, batch, nkv), min_sp);
+        num_splits = std::max(default_splits(suffix_max, batch, nkv), min_sp);
         span = default_span(batch, nkv);
+        if (prefix.len > 0 && span == kBatchSpan) {
+            // Batched suffixes behind a shared prefix are short: splits of up to
+            // ~256 rows (measured best on MI355X for 64 forks of a 2048-row
+            // prefix, suffixes 1..1024), each sequence using as many as its
+            // steps allow.
+            num_splits = std::max(std::min(ceil_div(suffix_max, 256), kMaxSplits / 2), min_sp);
+            span = kMinSpan;
+        }
     } else if (num_splits < min_sp) {
         return AF_ERR_INVALID_ARG;
     }
     if (num_splits > kMaxSplits) return AF_ERR_OUT_OF_RANGE;
-    if (!workspace || workspace_bytes < attn_workspace_bytes(batch, n_q_heads, hd, num_splits))
+    int pre = 0;  // prefix records per (sequence, KV head)
+    if (prefix.len > 0) {
+        pre = prefix.splits;
+        if (pre == 0)
+            pre = std::max(1, std::min(default_prefix_splits(prefix.len, batch, n_q_heads / nkv, nkv),
+                                       kMaxSplits - num_splits));
+        if (num_splits + pre > kMaxSplits) return AF_ERR_OUT_OF_RANGE;
+    }
+    const int rec_stride = num_splits + pre;
+    if (!workspace || workspace_bytes < attn_workspace_bytes(batch, n_q_heads, hd, rec_stride))
         return AF_ERR_WORKSPACE;
-    const AttnWorkspace w = attn_workspace_carve(workspace, batch, n_q_heads, num_splits);
+    const AttnWorkspace w = attn_workspace_carve(workspace, batch, n_q_heads, rec_stride);
     const size_t esz = fp8 ? 1 : 2;
     const size_t slab = size_t(pool->total_blocks) * bs * nkv * hd * esz;
     uint8_t* base = static_cast<uint8_t*>(pool->base);
@@ -1055,8 +1116,37 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     a.part_o = w.part_o;
     a.part_ml = w.part_ml;
     a.counters = w.counters;
+    a.row_start = prefix.len;
+    a.pre_records = pre;
+    a.rec_stride = rec_stride;
     const int64_t grid = int64_t(batch) * num_splits * nkv;
     if (grid > INT32_MAX) return AF_ERR_UNSUPPORTED;
+    if (pre > 0) {  // the prefix's partials first: records 0 .. pre-1
+        PrefixPartialArgs pp{};
+        pp.q = a.q;
+        pp.q_stride = q_stride;
+        pp.k = a.k;
+        pp.v = a.v;
+        pp.row_bytes = a.row_bytes;
+        pp.scales = a.scales;
+        pp.table = prefix.table;
+        pp.bs_log2 = a.block_shift;
+        pp.prefix_len = prefix.len;
+        pp.batch = batch;
+        pp.n_kv_heads = nkv;
+        pp.group = n_q_heads / nkv;
+        pp.key_splits = pre;
+        pp.rec_stride = rec_stride;
+        pp.part_o = w.part_o;
+        pp.part_ml = w.part_ml;
+        if (fused) {  // the decode launch ropes Q in place afterwards: rotate a copy here
+            pp.cos_t = cos_table;
+            pp.sin_t = sin_table;
+            pp.positions = d_positions;
+            pp.max_pos = max_pos;
+        }
+        if (int st = launch_prefix_partials(pp, stream)) return st;
+    }
     return dispatch(a, hd, n_q_heads / nkv, fp8, true, fused, int(grid), stream);
 }
 
@@ -1084,4 +1174,38 @@ extern "C" int af_paged_decode_fused(void* qkv_out, int batch, const af_kv_pool*
                            nullptr, batch, max_seq_len, out, out_stride, n_q_heads, num_splits,
                            workspace, workspace_bytes, true, d_slots, d_positions, cos_table,
                            sin_table, max_pos, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_paged_attention_shared_prefix(
+    const void* q, int q_stride, const af_kv_pool* pool, int layer, const int32_t* d_prefix_table,
+    int prefix_len, int prefix_splits, const int32_t* d_block_tables, int max_blocks_per_seq,
+    const int32_t* d_seq_lens, int batch, int max_seq_len, void* out, int out_stride,
+    int n_q_heads, int num_splits, void* workspace, size_t workspace_bytes, af_stream_t stream) {
+    SharedPrefix sp;
+    sp.table = d_prefix_table;
+    sp.len = prefix_len;
+    sp.splits = prefix_splits;
+    return paged_attention(const_cast<void*>(q), q_stride, pool, layer, d_block_tables,
+                           max_blocks_per_seq, d_seq_lens, batch, max_seq_len, out, out_stride,
+                           n_q_heads, num_splits, workspace, workspace_bytes, false, nullptr,
+                           nullptr, nullptr, nullptr, 0, static_cast<hipStream_t>(stream), sp);
+}
+
+extern "C" int af_paged_decode_fused_shared_prefix(
+    void* qkv_out, int batch, const af_kv_pool* pool, int layer, const int64_t* d_slots,
+    const int32_t* d_positions, const float* cos_table, const float* sin_table, int max_pos,
+    const int32_t* d_prefix_table, int prefix_len, int prefix_splits,
+    const int32_t* d_block_tables, int max_blocks_per_seq, int max_seq_len, void* out,
+    int out_stride, int n_q_heads, int num_splits, void* workspace, size_t workspace_bytes,
+    af_stream_t stream) {
+    if (!pool) return AF_ERR_INVALID_ARG;
+    SharedPrefix sp;
+    sp.table = d_prefix_table;
+    sp.len = prefix_len;
+    sp.splits = prefix_splits;
+    const int qkv_stride = (n_q_heads + 2 * pool->n_kv_heads) * pool->head_dim;
+    return paged_attention(qkv_out, qkv_stride, pool, layer, d_block_tables, max_blocks_per_seq,
+                           nullptr, batch, max_seq_len, out, out_stride, n_q_heads, num_splits,
+                           workspace, workspace_bytes, true, d_slots, d_positions, cos_table,
+                           sin_table, max_pos, static_cast<hipStream_t>(stream), sp);
 }

@@ -94,6 +94,27 @@ struct PrefillArgs {
     const int32_t* tile_map;
     const int32_t* chunks;
     int32_t max_blocks;
+    // Shared-prefix partials (part_o != NULL): the queries are the decode
+    // tokens of many sequences, packed per KV head — query row i is sequence
+    // i / q_group, Q head kv_head * q_group + i % q_group (n_q_heads is set to
+    // n_kv_heads) — and every query sees all kv_len keys (p0 = kv_len). The
+    // key tiles are split key_splits ways (workgroup id / (n_tiles * n_kv_heads)
+    // is the split), and each (query, split) leaves an unnormalised partial in
+    // the decode kernel's split-K record layout instead of an output row:
+    //   part_o [seq][kv_head][rec_stride][q_group * 128] = o * v_scale
+    //   part_ml[seq][kv_head][rec_stride][2 * q_group]   = (m, l), m in log2 units
+    // at record index = split.
+    int32_t q_group;
+    int32_t key_splits;
+    int32_t rec_stride;
+    float* part_o;
+    float* part_ml;
+    // Partials with RoPE (cos_t != NULL): query rows hold pre-RoPE values and
+    // sequence s is rotated at positions[s] (clamped into [0, max_pos)).
+    const float* cos_t;
+    const float* sin_t;
+    const int32_t* positions;
+    int32_t max_pos;
 };
 
 // Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
@@ -256,8 +277,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     // Block order: KV head fastest, then Q head of the group, then query tile
     // heaviest first.
     const int group = a.n_q_heads / a.n_kv_heads;
-    const int kvh = int(blockIdx.x) % a.n_kv_heads;
-    const int rest = int(blockIdx.x) / a.n_kv_heads;
+    int bid = int(blockIdx.x);
+    int ks = 0;  // key split (shared-prefix partials)
+    if (a.part_o) {
+        const int per = a.n_tiles * a.n_q_heads;
+        ks = bid / per;
+        bid -= ks * per;
+    }
+    const int kvh = bid % a.n_kv_heads;
+    const int rest = bid / a.n_kv_heads;
     const int head = kvh * group + rest % group;
     int tile;
     if (a.tile_map) {  // batched chunks: the host orders the tiles heaviest first
@@ -280,7 +308,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     const bool wave_live = wq0 < a.n;
 
     const int wg_keys = min(a.p0 + min(t0 + kQueries, a.n), a.kv_len);
-    const int n_kt = (wg_keys + kPfKeys - 1) / kPfKeys;
+    // Key tiles [kt_lo, n_kt) of this workgroup: all of them, or one key split's.
+    int kt_lo = 0, n_kt = (wg_keys + kPfKeys - 1) / kPfKeys;
+    if (a.part_o) {
+        const int all = n_kt;
+        kt_lo = ks * all / a.key_splits;
+        n_kt = (ks + 1) * all / a.key_splits;
+    }
     // Keys the wave needs.
     const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32, a.n), a.kv_len) : 0;
 
@@ -289,9 +323,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     const int qi_lane = min(wq0 + col, a.n - 1);  // clamped
     const int lim = min(a.p0 + qi_lane + 1, a.kv_len);     // this lane's query attends [0, lim)
     const int mask_from = min(a.p0 + wq0 + 1, a.kv_len);  // first key hidden from some query
+    // Packed partials with RoPE: this lane's (dim, dim + 64) pairs are qf[s][t],
+    // qf[s + 4][t] at dim 16s + 8hi + t (s < 4); their cos / sin go in flight here.
+    float4 rope_c[8], rope_s[8];
     {
-        const uint16_t* qrow =
-            a.q + size_t(qi_lane) * a.q_stride + size_t(head) * kPfHd + 8 * hi;
+        const uint16_t* qrow;
+        if (a.q_group) {
+            const int sq = qi_lane / a.q_group;
+            qrow = a.q + size_t(sq) * a.q_stride +
+                   size_t(head * a.q_group + qi_lane - sq * a.q_group) * kPfHd + 8 * hi;
+            if (a.cos_t) {
+                const int pos = min(max(a.positions[sq], 0), a.max_pos - 1);
+                const float* cr = a.cos_t + size_t(pos) * (kPfHd / 2) + 8 * hi;
+                const float* sr = a.sin_t + size_t(pos) * (kPfHd / 2) + 8 * hi;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    rope_c[2 * s] = *reinterpret_cast<const float4*>(cr + 16 * s);
+                    rope_c[2 * s + 1] = *reinterpret_cast<const float4*>(cr + 16 * s + 4);
+                    rope_s[2 * s] = *reinterpret_cast<const float4*>(sr + 16 * s);
+                    rope_s[2 * s + 1] = *reinterpret_cast<const float4*>(sr + 16 * s + 4);
+                }
+            }
+        } else {
+            qrow = a.q + size_t(qi_lane) * a.q_stride + size_t(head) * kPfHd + 8 * hi;
+        }
 #pragma unroll
         for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(half8, ld16(qrow + 16 * s));
     }
@@ -306,19 +361,53 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     int blk[4] = {0, 0, 0, 0};
     int blk8 = 0;  // FP8: this thread's row's block for the next tile
     Fp8Tile f8;
+    const int key_lo = kt_lo * kPfKeys;
     if constexpr (FP8) {
-        if constexpr (PAGED) blk8 = a.table[min(tid >> 2, a.kv_len - 1) >> a.bs_log2];
-        fp8_load<PAGED>(kb, vb, a.kv_row_bytes, 0, a.kv_len, tid, blk8, a.bs_log2, f8);
+        if constexpr (PAGED) blk8 = a.table[min(key_lo + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
+        fp8_load<PAGED>(kb, vb, a.kv_row_bytes, key_lo, a.kv_len, tid, blk8, a.bs_log2, f8);
         fp8_store(s_lds, s_lds + kVBase, tid, f8);
         if constexpr (PAGED)
-            if (n_kt > 1) blk8 = a.table[min(kPfKeys + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
+            if (kt_lo + 1 < n_kt)
+                blk8 = a.table[min(key_lo + kPfKeys + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
     } else {
-        if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, 0, a.kv_len, wave, lane, blk);
-        dma_tile<true, PAGED>(kb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds, blk, a.bs_log2);
-        dma_tile<false, PAGED>(vb, a.kv_row_bytes, 0, a.kv_len, wave, lane, s_lds + kVBase, blk,
-                               a.bs_log2);
+        if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, kt_lo, a.kv_len, wave, lane, blk);
+        dma_tile<true, PAGED>(kb, a.kv_row_bytes, key_lo, a.kv_len, wave, lane, s_lds, blk,
+                              a.bs_log2);
+        dma_tile<false, PAGED>(vb, a.kv_row_bytes, key_lo, a.kv_len, wave, lane, s_lds + kVBase,
+                               blk, a.bs_log2);
         if constexpr (PAGED)
-            if (n_kt > 1) tile_blocks(a.table, a.bs_log2, 1, a.kv_len, wave, lane, blk);
+            if (kt_lo + 1 < n_kt) tile_blocks(a.table, a.bs_log2, kt_lo + 1, a.kv_len, wave, lane, blk);
+    }
+    if (a.cos_t) {  // packed partials with RoPE (wave-uniform)
+        // Whole 32-bit words in and out: two fp16 elements per word, low half
+        // first. (Element-wise read-modify-write of the half8 vectors compiled
+        // to code that fed each rotated element into the next pair.)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint4 xw = __builtin_bit_cast(uint4, qf[s]);
+            const uint4 yw = __builtin_bit_cast(uint4, qf[s + 4]);
+            const uint32_t xs[4] = {xw.x, xw.y, xw.z, xw.w};
+            const uint32_t ys[4] = {yw.x, yw.y, yw.z, yw.w};
+            const float cs[8] = {rope_c[2 * s].x, rope_c[2 * s].y, rope_c[2 * s].z,
+                                 rope_c[2 * s].w, rope_c[2 * s + 1].x, rope_c[2 * s + 1].y,
+                                 rope_c[2 * s + 1].z, rope_c[2 * s + 1].w};
+            const float sn[8] = {rope_s[2 * s].x, rope_s[2 * s].y, rope_s[2 * s].z,
+                                 rope_s[2 * s].w, rope_s[2 * s + 1].x, rope_s[2 * s + 1].y,
+                                 rope_s[2 * s + 1].z, rope_s[2 * s + 1].w};
+            uint32_t xo[4], yo[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint16_t x0, y0, x1, y1;
+                rope_rotate(uint16_t(xs[w] & 0xffffu), uint16_t(ys[w] & 0xffffu), cs[2 * w],
+                            sn[2 * w], x0, y0);
+                rope_rotate(uint16_t(xs[w] >> 16), uint16_t(ys[w] >> 16), cs[2 * w + 1],
+                            sn[2 * w + 1], x1, y1);
+                xo[w] = uint32_t(x0) | (uint32_t(x1) << 16);
+                yo[w] = uint32_t(y0) | (uint32_t(y1) << 16);
+            }
+            qf[s] = __builtin_bit_cast(half8, make_uint4(xo[0], xo[1], xo[2], xo[3]));
+            qf[s + 4] = __builtin_bit_cast(half8, make_uint4(yo[0], yo[1], yo[2], yo[3]));
+        }
     }
 
     // Per-lane LDS operand offsets; the buffer, the key block and the key step
@@ -444,7 +533,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
                 fp8_store(s_lds + (BUF ^ 1) * kTileBytes, s_lds + kVBase + (BUF ^ 1) * kTileBytes,
                           tid, f8);
     };
-    int kt = 0;
+    int kt = kt_lo;
     for (; kt + 2 <= n_kt; kt += 2) {
         step(kt, std::integral_constant<int, 0>{});
         step(kt + 1, std::integral_constant<int, 1>{});
@@ -453,8 +542,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
 
     if (!wave_live) return;
     const int qi = wq0 + col;
-    const float inv = v_scale / halves_sum(l_run);
+    const float l_sum = halves_sum(l_run);
     if (qi >= a.n) return;
+    if (a.part_o) {  // shared-prefix partial: (o * v_scale, m, l) of split ks
+        const int sq = qi / a.q_group, gh = qi - sq * a.q_group;
+        const size_t rec = (size_t(sq) * a.n_kv_heads + kvh) * a.rec_stride + ks;
+        float* po = a.part_o + rec * (size_t(a.q_group) * kPfHd) + gh * kPfHd + 4 * hi;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(po + 32 * db + 8 * g) =
+                    make_float4(o[db][4 * g] * v_scale, o[db][4 * g + 1] * v_scale,
+                                o[db][4 * g + 2] * v_scale, o[db][4 * g + 3] * v_scale);
+        if (hi == 0) {
+            float* ml = a.part_ml + rec * 2 * a.q_group;
+            ml[gh] = m_run;
+            ml[a.q_group + gh] = l_sum;
+        }
+        return;
+    }
+    const float inv = v_scale / l_sum;
     uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -484,6 +592,47 @@ int launch_prefill(PrefillArgs a, hipStream_t stream) {
 }
 
 }  // namespace
+
+int prefix_partial_tiles(int batch, int group, int n_kv_heads) {
+    return ceil_div(batch * group, 32 * kPfWaves) * n_kv_heads;
+}
+
+int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream) {
+    PrefillArgs a{};
+    a.q = p.q;
+    a.q_stride = p.q_stride;
+    a.k = reinterpret_cast<const uint16_t*>(p.k);
+    a.v = reinterpret_cast<const uint16_t*>(p.v);
+    a.kv_stride = int64_t(p.n_kv_heads) * kPfHd;
+    a.kv_row_bytes = uint32_t(p.row_bytes);
+    a.n = p.batch * p.group;  // packed: one query per (sequence, Q head of the group)
+    a.p0 = p.prefix_len;      // every query follows the whole prefix
+    a.kv_len = p.prefix_len;
+    a.n_q_heads = p.n_kv_heads;
+    a.n_kv_heads = p.n_kv_heads;
+    a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
+    a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
+    a.table = p.table;
+    a.bs_log2 = p.bs_log2;
+    a.scales = p.scales;
+    a.q_group = p.group;
+    a.key_splits = p.key_splits;
+    a.rec_stride = p.rec_stride;
+    a.part_o = p.part_o;
+    a.part_ml = p.part_ml;
+    a.cos_t = p.cos_t;
+    a.sin_t = p.sin_t;
+    a.positions = p.positions;
+    a.max_pos = p.max_pos;
+    const dim3 grid(a.n_tiles * a.n_q_heads * p.key_splits), block(kPfThreads);
+    if (p.scales)
+        hipLaunchKernelGGL((prefill_attention_kernel<true, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((prefill_attention_kernel<true, false>), grid, block, 0, stream, a);
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}
+
 }  // namespace af
 
 using namespace af;

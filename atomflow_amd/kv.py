@@ -246,6 +246,33 @@ def launch_paged_decode_fused(qkv_out, batch, pool, layer, d_slots, d_positions,
                                       workspace.nbytes, _s(stream)), "launch_paged_decode_fused")
 
 
+def launch_paged_attention_shared_prefix(q, q_stride, pool, layer, d_prefix_table, prefix_len,
+                                         d_block_tables, max_blocks_per_seq, d_seq_lens, batch,
+                                         max_seq_len, out, out_stride, n_q_heads, workspace,
+                                         num_splits=0, prefix_splits=0, stream=None):
+    """af_paged_attention for sequences sharing rows [0, prefix_len): the prefix is
+    attended once for the batch on the matrix cores, the rest per sequence."""
+    check(lib().af_paged_attention_shared_prefix(
+        _p(q), q_stride, ctypes.byref(pool), layer, _p(d_prefix_table), prefix_len, prefix_splits,
+        _p(d_block_tables), max_blocks_per_seq, _p(d_seq_lens), batch, max_seq_len, _p(out),
+        out_stride, n_q_heads, num_splits, workspace.ptr, workspace.nbytes, _s(stream)),
+        "launch_paged_attention_shared_prefix")
+
+
+def launch_paged_decode_fused_shared_prefix(qkv_out, batch, pool, layer, d_slots, d_positions,
+                                            cos_table, sin_table, max_pos, d_prefix_table,
+                                            prefix_len, d_block_tables, max_blocks_per_seq,
+                                            max_seq_len, out, out_stride, n_q_heads, workspace,
+                                            num_splits=0, prefix_splits=0, stream=None):
+    """launch_paged_decode_fused with a shared prefix (two launches)."""
+    check(lib().af_paged_decode_fused_shared_prefix(
+        _p(qkv_out), batch, ctypes.byref(pool), layer, _p(d_slots), _p(d_positions),
+        _p(cos_table), _p(sin_table), max_pos, _p(d_prefix_table), prefix_len, prefix_splits,
+        _p(d_block_tables), max_blocks_per_seq, max_seq_len, _p(out), out_stride, n_q_heads,
+        num_splits, workspace.ptr, workspace.nbytes, _s(stream)),
+        "launch_paged_decode_fused_shared_prefix")
+
+
 def paged_gather(pool, layer, d_block_table, seq_len, k_dst, v_dst, stream=None):
     check(lib().af_paged_gather(ctypes.byref(pool), layer, _p(d_block_table), seq_len, _p(k_dst),
                                 _p(v_dst), _s(stream)), "paged_gather")

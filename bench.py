@@ -9,7 +9,8 @@ synthetic N(0,1) fp16 generated on the device and resident in HBM before timing.
 
 ``--config 3|4|5`` run the paged workloads (BASELINE configs[2..4]) through the
 BlockManager: paged fp16 (B=32, L~U[128,8192], 16-token blocks), paged with a
-2048-token shared prefix (64 forks, copy-on-write measured separately), FP8
+2048-token shared prefix (64 forks through the shared-prefix entry points, the
+plain paged kernel timed beside them, copy-on-write measured separately), FP8
 E4M3 paged (B=128, L~U[8192,16384], 32-token blocks, ~100 GB pool).
 
 Printed JSON line (one per run):
@@ -59,6 +60,8 @@ def parse():
                     help="BASELINE configs[n-1]: 2 contiguous, 3 paged, 4 paged+CoW, 5 paged FP8")
     ap.add_argument("--ctx", type=int, default=8192, choices=[1024, 8192, 32768])
     ap.add_argument("--splits", type=int, default=0, help="attention split count (0 = library default)")
+    ap.add_argument("--prefix-splits", type=int, default=0,
+                    help="configs[3]: key splits of the shared-prefix launch (0 = library default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--no-serving", action="store_true", help="skip the continuous-batching step")
@@ -758,15 +761,47 @@ def bench_paged(args, dev, kv, lib, info):
                                       num_splits=launch_splits, stream=stream)
 
     graphs = {"step": dev.Graph.capture(stream, step), "attn": dev.Graph.capture(stream, attention_only)}
+    if cfg == 4:
+        # Shared-prefix form: rows [0, 2048) of every fork are the root's, attended
+        # once for the batch (matrix-core launch), the suffixes per sequence.
+        d_root = dev.DeviceBuffer.from_array(np.ascontiguousarray(tables[0]))
+        ws_sp = kv.AttentionWorkspace(B, NQ, NKV, HD, 0, stream)
+        stream.sync()
+
+        def step_sp():
+            for l in range(LAYERS):
+                kv.launch_paged_decode_fused_shared_prefix(
+                    qkv.ptr + l * B * QKV * 2, B, desc, l, d_slots, d_pos, d_cos, d_sin, max_pos,
+                    d_root, prefix, d_tables, max_blocks, max_len, out.ptr + l * B * Q_DIM * 2,
+                    Q_DIM, NQ, ws_sp, num_splits=launch_splits, prefix_splits=args.prefix_splits,
+                    stream=stream)
+
+        def attention_sp():
+            for l in range(LAYERS):
+                kv.launch_paged_attention_shared_prefix(
+                    qkv.ptr + l * B * QKV * 2, QKV, desc, l, d_root, prefix, d_tables, max_blocks,
+                    d_lens, B, max_len, out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ, ws_sp,
+                    num_splits=launch_splits, prefix_splits=args.prefix_splits, stream=stream)
+
+        graphs["step_sp"] = dev.Graph.capture(stream, step_sp)
+        graphs["attn_sp"] = dev.Graph.capture(stream, attention_sp)
     t = Timer(dev, stream, args.warmup)
     ms_step = t.graph_ms(graphs["step"], args.steps)
     ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
+    ms_step_plain = ms_attn_plain = None
+    if cfg == 4:
+        ms_step_plain, ms_attn_plain = ms_step, ms_attn
+        ms_step = t.graph_ms(graphs["step_sp"], args.steps)
+        ms_attn = t.graph_ms(graphs["attn_sp"], args.steps) / LAYERS
     for g in graphs.values():
         g.destroy()
     row = KV_DIM * esz
     logical = int(lens_after.sum()) * row * 2
     step_gbs = LAYERS * logical / (ms_step * 1e-3) / 1e9
-    attn_gbs = logical / (ms_attn * 1e-3) / 1e9
+    # Roofline bytes: every KV row the step must read once. With a shared prefix
+    # (configs[3]) that is the unique rows: the prefix once, then each suffix.
+    algo_bytes = unique_tokens * row * 2 if cfg == 4 else logical
+    attn_gbs = algo_bytes / (ms_attn * 1e-3) / 1e9
     result = {
         "metric": METRIC + f" [paged configs[{cfg - 1}]]", "value": round(step_gbs, 1),
         "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -782,11 +817,18 @@ def bench_paged(args, dev, kv, lib, info):
                    "logical_kv_bytes_per_layer": logical,
                    "unique_kv_bytes_per_layer": unique_tokens * row * 2, "layers": LAYERS},
         "kernels": {"paged_attn_us": round(ms_attn * 1e3, 3)},
+        "roofline_bytes": "unique KV rows (shared prefix once)" if cfg == 4 else "KV rows attended",
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None,
     }
     if cfg == 4:
+        result["path"] = ("af_paged_decode_fused_shared_prefix (step) / "
+                          "af_paged_attention_shared_prefix (attention)")
+        result["kernels"].update({
+            "plain_paged_attn_us": round(ms_attn_plain * 1e3, 3),
+            "plain_us_per_layer_step": round(ms_step_plain * 1e3 / LAYERS, 3),
+            "plain_step_gbs_logical": round(LAYERS * logical / (ms_step_plain * 1e-3) / 1e9, 1)})
         result["kernels"].update(cow_copy_timing(dev, kv, bm, prefix, B, stream, desc))
     if args.calibrate_copy:
         calibrate_copy(dev, kv, stream)

@@ -199,6 +199,44 @@ int af_paged_decode_fused(void* qkv_out, int batch, const af_kv_pool* pool, int 
                           void* out, int out_stride, int n_q_heads, int num_splits,
                           void* workspace, size_t workspace_bytes, af_stream_t stream);
 
+/* Shared-prefix ("cascade") form of af_paged_attention for a batch whose
+ * sequences all begin with the same prefix_len rows (forks of one prompt under
+ * copy-on-write, src/experimental/server_arch/paged_kv_manager.h:51,61: the
+ * reference reads the shared blocks once per sequence through its tables). Same
+ * result as af_paged_attention, within its tolerance, when rows
+ * [0, prefix_len) of every sequence hold the values d_prefix_table maps
+ * (one row of max_blocks_per_seq entries, e.g. the root sequence's table).
+ * The prefix is attended once for the whole batch on the matrix cores (one
+ * launch, prefix_splits key ranges; 0 = default), the per-sequence rows
+ * [prefix_len, L) by the split-K decode kernel, whose combine merges both.
+ * head_dim 128. A sequence with L <= prefix_len attends the prefix only.
+ * Workspace: af_attention_workspace_size(batch, ..., num_splits +
+ * prefix_splits); one sized with num_splits = 0 (the maximum) always fits.
+ * No counterpart entry in the reference (an optimisation of the same op). */
+int af_paged_attention_shared_prefix(const void* q, int q_stride, const af_kv_pool* pool,
+                                     int layer, const int32_t* d_prefix_table, int prefix_len,
+                                     int prefix_splits, const int32_t* d_block_tables,
+                                     int max_blocks_per_seq, const int32_t* d_seq_lens, int batch,
+                                     int max_seq_len, void* out, int out_stride, int n_q_heads,
+                                     int num_splits, void* workspace, size_t workspace_bytes,
+                                     af_stream_t stream);
+
+/* af_paged_decode_fused with a shared prefix: the prefix launch rotates its own
+ * copy of each query (same arithmetic), then the fused decode launch ropes,
+ * appends and attends rows [prefix_len, pos] and merges the prefix partials.
+ * Outputs as af_paged_decode_fused (qkv_out, pool rows bit for bit; attention
+ * within tolerance). */
+int af_paged_decode_fused_shared_prefix(void* qkv_out, int batch, const af_kv_pool* pool,
+                                        int layer, const int64_t* d_slots,
+                                        const int32_t* d_positions, const float* cos_table,
+                                        const float* sin_table, int max_pos,
+                                        const int32_t* d_prefix_table, int prefix_len,
+                                        int prefix_splits, const int32_t* d_block_tables,
+                                        int max_blocks_per_seq, int max_seq_len, void* out,
+                                        int out_stride, int n_q_heads, int num_splits,
+                                        void* workspace, size_t workspace_bytes,
+                                        af_stream_t stream);
+
 /* Gathers one sequence's first seq_len logical rows of `layer` into
  * contiguous [seq_len, kv_dim] buffers (K and V; elements copied bit for bit). */
 int af_paged_gather(const af_kv_pool* pool, int layer, const int32_t* d_block_table,

@@ -305,10 +305,13 @@ def test_cow_decode_step_end_to_end(gpu):
 
 @pytest.mark.parametrize("fp8", [False, True])
 def test_paged_fused_equals_append_then_attention(gpu, fp8):
-    """af_paged_decode_fused == af_paged_rope_append + af_paged_attention, bit for bit."""
+    """af_paged_decode_fused == af_paged_rope_append + af_paged_attention, bit for bit.
+    Lengths 64 and 128 (L = 65, 129 after the append, 8 splits) give a last split
+    that starts at the appended row itself: its only row comes from LDS and the
+    rows it reads stay inside its staged block-table window."""
     say(f"paged fused fp8={fp8}")
     bs, layers = (32 if fp8 else 16), 2
-    lengths = [0, 1, 15, 16, 31, 200, 1000, 2500]
+    lengths = [0, 1, 15, 16, 31, 64, 128, 200, 1000, 2500]
     B = len(lengths)
     total = sum(n // bs + 2 for n in lengths) + 4
     dt = AF_KV_FP8_E4M3 if fp8 else AF_KV_FP16
