@@ -863,8 +863,13 @@ int default_splits(int max_seq_len, int batch, int n_kv_heads) {
     // About 3/4 of a workgroup per CU: measured best on MI355X for batch 1
     // (the split-K combine grows with the split count faster than more
     // workgroups add bandwidth).
-    int splits = std::max(1, (3 * device_compute_units()) / (4 * pairs));
-    splits = std::max(splits, ceil_div(max_seq_len, 1024));  // long sequences: bounded spans
+    const int cus = device_compute_units();
+    int splits = std::max(1, (3 * cus) / (4 * pairs));
+    // Long sequences: spans of about 1024 rows, but never more workgroups than
+    // CUs. A grid just past the CU count doubles up a few CUs, and the launch
+    // then waits on them (ctx 32k on MI355X: 33 splits x 8 heads = 264
+    // workgroups ran 40.5 us, 32 splits 29.6 us, 64 splits 31.3 us).
+    splits = std::max(splits, std::min(ceil_div(max_seq_len, 1024), std::max(1, cus / pairs)));
     splits = std::min(splits, std::max(1, ceil_div(max_seq_len, kMinSpan)));
     return std::min(std::max(splits, 1), kMaxSplits);
 }

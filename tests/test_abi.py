@@ -67,6 +67,22 @@ def test_host_only_entry_points_without_gpu():
                               None) == atomflow_amd.AF_ERR_INVALID_ARG
 
 
+def test_default_split_counts():
+    """The split heuristic on a 256-CU device (the CU count a host without a GPU
+    assumes, MI355X's). Batch 1, 8 KV heads: ~3/4 of a workgroup per CU up to
+    ctx 24k, then ~1024-row spans but never more workgroups than CUs (33 splits
+    at ctx 32k put two workgroups on 8 CUs and ran a third slower). Batches:
+    ~512 rows per split."""
+    from atomflow_amd import kv
+    assert kv.default_splits(8193, 1, 8) == 24
+    assert kv.default_splits(24577, 1, 8) == 25  # ceil(24577 / 1024)
+    assert kv.default_splits(32769, 1, 8) == 32
+    assert kv.default_splits(131072, 1, 8) == 32
+    assert kv.default_splits(1025, 1, 8) == 17   # one 64-row step per split
+    assert kv.default_splits(8193, 32, 8) == 17  # batched: ceil(8193 / 512)
+    assert kv.default_splits(0, 1, 8) == 1
+
+
 def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(atomflow_amd, "_lib", None)
     monkeypatch.setattr(atomflow_amd, "LIB_PATH", "/nonexistent/libatomflow_kv.so")
