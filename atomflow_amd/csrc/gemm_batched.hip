@@ -11,22 +11,24 @@
 // and writes K and V to each token's slot of the paged pool, exactly as
 // af_paged_rope_append does on the projection's output.
 //
-// Design (HBM-bound: one weight byte per 2*M flops; M <= 32 per token tile):
-//  * D = X W^T on v_mfma_f32_32x32x16_f16. A = 32 tokens x 16 k of x (read
-//    from L2, tokens past m read as zero), B = 16 k x 32 weight rows (E4M3 ->
-//    fp16 in registers with v_cvt_scalef32_pk_f16_fp8 at scale 1, exact). A
-//    lane loads 16 contiguous weight bytes per pair of MFMAs; the pair's k
-//    order is permuted identically on both operands.
+// Design (HBM-bound: one weight byte per 2*M flops; M <= 32 per launch tile):
+//  * D = X W^T on v_mfma_f32_16x16x32_f16: A = 16 tokens x 32 k of x (read
+//    from L2; rows past m repeat row m-1 and are not stored), B = 32 k x 16
+//    weight rows (E4M3 -> fp16 in registers with v_cvt_scalef32_pk_f16_fp8 at
+//    scale 1, exact). With group sizes that are multiples of 64, a lane loads 16 contiguous weight
+//    bytes per pair of MFMAs and the pair's k order is permuted identically on
+//    both operands; otherwise 8 bytes per MFMA.
 //  * D's column is the lane's weight row, so a group scale is one value per
 //    lane: each group accumulates into a fresh fragment, then acc += scale * it.
-//  * A workgroup is 16 waves: two 32-row tiles x eight group-aligned parts of
-//    K. It owns its 64 rows' whole K, so no partial leaves the workgroup: the
-//    parts are summed through LDS in a fixed tree (results do not depend on
-//    timing) and the epilogue follows at once. Each wave keeps 8 weight loads
-//    (8 KB) in flight, 128 KB per workgroup.
-//  * For the fused kernel the two tiles are the rotation partners (d, d + 64)
-//    of one head, exchanged through LDS; RoPE runs on the rounded fp16
-//    projections.
+//  * A workgroup is 8 waves over 16 weight rows: wave p owns the p-th
+//    group-aligned part of K, so each workgroup owns its rows' whole K and no
+//    partial leaves it. The parts are summed through LDS in a fixed order
+//    (results do not depend on timing). 16-row workgroups spread the weights
+//    over every CU (320 workgroups for the 5120-row QKV projection); up to 32
+//    tokens (two token tiles) share each weight load.
+//  * For the fused kernel the 16 columns are 8 head dims d and their rotation
+//    partners d + 64, so a pair sits in lanes l and l ^ 8 of a 16-lane row;
+//    RoPE runs on the rounded fp16 projections.
 #include <algorithm>
 #include <cmath>
 
@@ -38,14 +40,13 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
-typedef float float16v_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBgParts = 8;                 // K parts per workgroup
-constexpr int kBgWaves = 2 * kBgParts;       // two row tiles per part
-constexpr int kBgThreads = 64 * kBgWaves;    // 1024
-constexpr int kBgTok = 32;                   // tokens per token tile (one MFMA operand)
-constexpr int kBgRows = 64;                  // weight rows per workgroup
-constexpr int kBgDepth = 8;                  // weight loads in flight per wave
+typedef float float4v_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBgParts = 8;               // K parts = waves per workgroup
+constexpr int kBgThreads = 64 * kBgParts;  // 512
+constexpr int kBgRows = 16;               // weight rows per workgroup (one MFMA column tile)
+constexpr int kBgTile = 16;               // tokens per token tile (one MFMA row tile)
 
 struct BatchedArgs {
     const uint16_t* x;  // [m][x_stride] fp16
@@ -80,157 +81,208 @@ __device__ __forceinline__ half8_t e4m3x8(uint32_t lo, uint32_t hi) {
     return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-// One rotation pair with the reference's separately rounded products.
-__device__ __forceinline__ void rotate1(uint16_t x, uint16_t y, float c, float s, uint16_t& xo,
-                                        uint16_t& yo) {
-#pragma clang fp contract(off)
-    const float xf = h2f(x), yf = h2f(y);
-    const float xc = xf * c;
-    const float ys = yf * s;
-    const float xs = xf * s;
-    const float yc = yf * c;
-    xo = f2h(xc - ys);
-    yo = f2h(xs + yc);
-}
+// Weight bytes of one lane for one chunk: 16 (KC = 64) or 8 (KC = 32).
+template <int KC>
+struct WChunk {
+    uint4 v;
+};
+template <>
+struct WChunk<32> {
+    uint2 v;
+};
 
-template <bool FUSED, bool FP8>
-__global__ __launch_bounds__(kBgThreads) void w8a16_batched_kernel(const BatchedArgs a) {
-    __shared__ float s_red[kBgParts][16][64];  // partial fragments, half the parts at a time
-    __shared__ uint16_t s_y[16][64];           // fused: tile 1's rounded projections
+// TT token tiles x KC k per chunk; DEPTH chunks in flight per wave.
+template <bool FUSED, bool FP8, int TT, int KC>
+__global__ __launch_bounds__(kBgThreads, 4) void w8a16_batched_kernel(const BatchedArgs a) {
+    constexpr int DEPTH = TT == 1 ? 6 : 3;  // <= 128 VGPRs: two workgroups per CU
+    constexpr int XV = KC / 32;  // 16-byte x loads per token tile per chunk
+    __shared__ float s_red[kBgParts][TT * 4][64];
+    __shared__ int32_t s_pos[FUSED ? kBgTile * TT : 1];
+    __shared__ int64_t s_slot[FUSED ? kBgTile * TT : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int tile = wave & 1, part = wave >> 1;
-    const int col = lane & 31, hi = lane >> 5;
-    const int blk = int(blockIdx.x), t0 = int(blockIdx.y) * kBgTok;
-    // The workgroup's tiles: plain, rows [64 blk, +64); fused (head_dim 128),
-    // rows d and d + 64 of one head for d in [32 j, 32 j + 32).
-    const int c0 = FUSED ? (blk >> 1) * 128 + 32 * (blk & 1) : blk * kBgRows;
-    const int c = c0 + tile * (FUSED ? 64 : 32);
-    const int nrow = min(c + col, a.n - 1);  // clamped loads
-    const int tok = t0 + col;
-    const bool tok_live = tok < a.m;
+    const int part = tid >> 6;
+    const int j = lane & 15, sub = lane >> 4;  // MFMA column / row index, k sub-block
+    const int blk = int(blockIdx.x), t0 = int(blockIdx.y) * kBgTile * TT;
+    // The workgroup's 16 weight rows: plain, [16 blk, +16); fused (head_dim 128),
+    // dims d0 .. d0+7 of head blk/8 (d0 = 8 (blk % 8)) and their partners d + 64.
+    int row;
+    if constexpr (FUSED)
+        row = (blk >> 3) * 128 + (blk & 7) * 8 + (j & 7) + (j >> 3) * 64;
+    else
+        row = blk * kBgRows + j;
+    const int nrow = min(row, a.n - 1);  // clamped loads
 
     const int g_lo = part * a.groups / kBgParts, g_hi = (part + 1) * a.groups / kBgParts;
-    const int iters = (g_hi - g_lo) * a.group_size / 32;
-    const int kbase = g_lo * a.group_size + 16 * hi;
+    const int chunks = (g_hi - g_lo) * a.group_size / KC;
+    const int per_group = a.group_size / KC;
+    const int kbase = g_lo * a.group_size + sub * (KC / 4);  // this lane's first k in a chunk
     const uint8_t* wrow = a.w + size_t(nrow) * a.k + kbase;
-    const uint16_t* xr = a.x + size_t(tok_live ? tok : 0) * a.x_stride + kbase;
-
-    uint4 wq[kBgDepth];
+    // Token rows past m load row m-1 instead: an MFMA output row depends only on
+    // its own A row, and those rows' outputs are never written. (Loading zeros
+    // there instead made the compiler select between the x address and a
+    // scratch copy of zero, i.e. flat loads, at twice the kernel's time.)
+    const uint16_t* xr[TT];
 #pragma unroll
-    for (int i = 0; i < kBgDepth; ++i)
-        if (i < iters) wq[i] = *reinterpret_cast<const uint4*>(wrow + 32 * i);
-    const uint4 zero4 = {0u, 0u, 0u, 0u};
-    uint4 xa = zero4, xb = zero4;
-    if (tok_live && iters > 0) {
-        xa = *reinterpret_cast<const uint4*>(xr);
-        xb = *reinterpret_cast<const uint4*>(xr + 8);
+    for (int tt = 0; tt < TT; ++tt) {
+        const int tok = min(t0 + kBgTile * tt + j, a.m - 1);
+        xr[tt] = a.x + size_t(tok) * a.x_stride + kbase;
     }
 
-    float16v_t acc, f;
+    WChunk<KC> wq[DEPTH];
+    uint4 xq[DEPTH][TT][XV];
+    uint16_t sq[DEPTH];  // the group scale of each chunk in flight
+    const uint16_t* srow = a.scales + size_t(nrow) * a.groups + g_lo;
+    auto issue = [&](int slot, int c) __attribute__((always_inline)) {
+        sq[slot] = srow[c / per_group];
+        if constexpr (KC == 64)
+            wq[slot].v = *reinterpret_cast<const uint4*>(wrow + size_t(c) * KC);
+        else
+            wq[slot].v = *reinterpret_cast<const uint2*>(wrow + size_t(c) * KC);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = f[r] = 0.0f;
-    const int per_group = a.group_size / 32;
-    for (int it0 = 0; it0 < iters; it0 += kBgDepth) {
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-        for (int i = 0; i < kBgDepth; ++i) {
-            const int it = it0 + i;
-            if (it < iters) {
-                const uint4 wv = wq[i];
-                const half8_t x0 = __builtin_bit_cast(half8_t, xa);
-                const half8_t x1 = __builtin_bit_cast(half8_t, xb);
-                if (it + kBgDepth < iters)  // refill the slot kBgDepth iterations ahead
-                    wq[i] = *reinterpret_cast<const uint4*>(wrow + 32 * (it + kBgDepth));
-                if (tok_live && it + 1 < iters) {  // the next iteration's activations
-                    xa = *reinterpret_cast<const uint4*>(xr + 32 * (it + 1));
-                    xb = *reinterpret_cast<const uint4*>(xr + 32 * (it + 1) + 8);
+            for (int v = 0; v < XV; ++v)
+                xq[slot][tt][v] = *reinterpret_cast<const uint4*>(xr[tt] + size_t(c) * KC + 8 * v);
+    };
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i)
+        if (i < chunks) issue(i, i);
+    if constexpr (FUSED) {  // the tokens' positions and slots, read during the weight stream
+        if (tid < kBgTile * TT) {
+            const int t = min(t0 + tid, a.m - 1);
+            s_pos[tid] = a.d_positions[t];
+            s_slot[tid] = a.d_slots[t];
+        }
+    }
+
+    float4v_t acc[TT], f[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[tt][r] = f[tt][r] = 0.0f;
+    for (int c0 = 0; c0 < chunks; c0 += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const int c = c0 + i;
+            if (c < chunks) {
+                const float sc = h2f(sq[i]);
+                half8_t wb[XV];
+                if constexpr (KC == 64) {
+                    wb[0] = e4m3x8(wq[i].v.x, wq[i].v.y);
+                    wb[XV - 1] = e4m3x8(wq[i].v.z, wq[i].v.w);
+                } else {
+                    wb[0] = e4m3x8(wq[i].v.x, wq[i].v.y);
                 }
-                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, e4m3x8(wv.x, wv.y), f, 0, 0, 0);
-                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, e4m3x8(wv.z, wv.w), f, 0, 0, 0);
-                if ((it + 1) % per_group == 0) {  // group done: scale into the accumulator
-                    const float sc = h2f(a.scales[size_t(nrow) * a.groups + g_lo + it / per_group]);
+                half8_t xa[TT][XV];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        acc[r] = fmaf(sc, f[r], acc[r]);
-                        f[r] = 0.0f;
-                    }
+                for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+                    for (int v = 0; v < XV; ++v) xa[tt][v] = __builtin_bit_cast(half8_t, xq[i][tt][v]);
+                if (c + DEPTH < chunks) issue(i, c + DEPTH);  // refill the slot DEPTH chunks ahead
+#pragma unroll
+                for (int v = 0; v < XV; ++v)
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt)
+                        f[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[tt][v], wb[v], f[tt], 0, 0, 0);
+                if ((c + 1) % per_group == 0) {  // group done: scale into the accumulator
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            acc[tt][r] = fmaf(sc, f[tt][r], acc[tt][r]);
+                            f[tt][r] = 0.0f;
+                        }
                 }
             }
         }
     }
 
-    // Sum the parts: a fixed tree through LDS (parts p and p + h, h = 4, 2, 1).
+    // Sum the parts in a fixed order (part 0 + 1 + ... + 7) through LDS.
 #pragma unroll
-    for (int h = kBgParts / 2; h >= 1; h >>= 1) {
-        if (part >= h && part < 2 * h) {
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s_red[(part - h) * 2 + tile][r][lane] = acc[r];
-        }
-        __syncthreads();
-        if (part < h) {
+        for (int r = 0; r < 4; ++r) s_red[part][tt * 4 + r][lane] = acc[tt][r];
+    __syncthreads();
+    if (part != 0) return;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += s_red[part * 2 + tile][r][lane];
-        }
-        __syncthreads();
+    for (int q = 0; q < TT * 4; ++q) {
+        float v = s_red[0][q][lane];
+#pragma unroll
+        for (int p = 1; p < kBgParts; ++p) v += s_red[p][q][lane];
+        acc[q >> 2][q & 3] = v;
     }
 
-    // Register r of lane l: token t0 + 8(r/4) + 4(l/32) + r%4, weight row c + l%32.
+    // Register r of token tile tt, lane l: token t0 + 16 tt + 4 (l/16) + r, weight row `row`.
     if constexpr (!FUSED) {
-        if (part != 0) return;
+        if (row >= a.n) return;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = t0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if (t < a.m && c + col < a.n) a.y[size_t(t) * a.y_stride + c + col] = f2h(acc[r]);
-        }
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + kBgTile * tt + 4 * sub + r;
+                if (t < a.m) a.y[size_t(t) * a.y_stride + row] = f2h(acc[tt][r]);
+            }
     } else {
-        if (part == 0 && tile == 1) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s_y[r][lane] = f2h(acc[r]);
-        }
-        __syncthreads();
-        if (wave != 0) return;  // wave 0 finishes the pairs (d, d + 64)
         const int hd = a.head_dim, half = hd / 2;
-        const int head = c0 / hd;
-        const int d = c0 % hd + col;
+        const int head = blk >> 3;
+        const bool lo = j < 8;               // this lane holds dim d; lane ^ 8 holds d + 64
+        const int d = (blk & 7) * 8 + (j & 7);  // pair index, 0 .. 63
+        const int dim = lo ? d : d + half;      // the element this lane writes
         const int kind = head < a.n_q_heads ? 0 : (head < a.n_q_heads + a.n_kv_heads ? 1 : 2);
         const int kh = head - a.n_q_heads - (kind == 2 ? a.n_kv_heads : 0);
         const int kv_dim = a.n_kv_heads * hd;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = t0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            if (t >= a.m) continue;
-            const uint16_t y0 = f2h(acc[r]), y1 = s_y[r][lane];
-            uint16_t* yrow = a.y + size_t(t) * a.y_stride + size_t(head) * hd;
-            const int pos = a.d_positions[t];
-            const int64_t row = a.d_slots[t];
-            if (pos < 0 || pos >= a.max_pos || row < 0 || row >= a.max_rows) {
-                // nothing is rotated or appended for an out-of-range token
-                yrow[d] = y0;
-                yrow[d + half] = y1;
-                if (a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
-                continue;
-            }
-            uint16_t o0 = y0, o1 = y1;
-            if (kind < 2)
-                rotate1(y0, y1, a.cos_t[size_t(pos) * half + d], a.sin_t[size_t(pos) * half + d],
-                        o0, o1);
-            yrow[d] = o0;
-            yrow[d + half] = o1;
-            if (kind > 0) {
-                const size_t e = size_t(row) * kv_dim + size_t(kh) * hd + d;
-                uint8_t* base = kind == 1 ? a.k_dst : a.v_dst;
-                if constexpr (FP8) {
-                    const float sc = (kind == 1 ? a.k_scales : a.v_scales)[kh];
-                    base[e] = uint8_t(quantize_fp8(o0, sc));
-                    base[e + half] = uint8_t(quantize_fp8(o1, sc));
-                } else {
-                    reinterpret_cast<uint16_t*>(base)[e] = o0;
-                    reinterpret_cast<uint16_t*>(base)[e + half] = o1;
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint16_t mine = f2h(acc[tt][r]);
+                const uint16_t other = uint16_t(__shfl_xor(int(mine), 8));
+                const int t = t0 + kBgTile * tt + 4 * sub + r;
+                if (t >= a.m) continue;
+                uint16_t* yrow = a.y + size_t(t) * a.y_stride + size_t(head) * hd;
+                const int pos = s_pos[t - t0];
+                const int64_t slot = s_slot[t - t0];
+                if (pos < 0 || pos >= a.max_pos || slot < 0 || slot >= a.max_rows) {
+                    // nothing is rotated or appended for an out-of-range token
+                    yrow[dim] = mine;
+                    if (a.d_status && j == 0) *a.d_status = AF_ERR_OUT_OF_RANGE;
+                    continue;
+                }
+                const uint16_t y0 = lo ? mine : other, y1 = lo ? other : mine;
+                uint16_t o0 = y0, o1 = y1;
+                if (kind < 2)
+                    rope_rotate(y0, y1, a.cos_t[size_t(pos) * half + d],
+                                a.sin_t[size_t(pos) * half + d], o0, o1);
+                const uint16_t out = lo ? o0 : o1;
+                yrow[dim] = out;
+                if (kind > 0) {
+                    const size_t e = size_t(slot) * kv_dim + size_t(kh) * hd + dim;
+                    uint8_t* base = kind == 1 ? a.k_dst : a.v_dst;
+                    if constexpr (FP8) {
+                        const float sc = (kind == 1 ? a.k_scales : a.v_scales)[kh];
+                        base[e] = uint8_t(quantize_fp8(out, sc));
+                    } else {
+                        reinterpret_cast<uint16_t*>(base)[e] = out;
+                    }
                 }
             }
-        }
+    }
+}
+
+template <bool FUSED, bool FP8>
+void launch_batched(const BatchedArgs& a, int row_blocks, hipStream_t s) {
+    const bool two = a.m > kBgTile;
+    const int per = kBgTile * (two ? 2 : 1);
+    const dim3 grid(row_blocks, (a.m + per - 1) / per), block(kBgThreads);
+    const bool k64 = a.group_size % 64 == 0;
+    if (two) {
+        if (k64) hipLaunchKernelGGL((w8a16_batched_kernel<FUSED, FP8, 2, 64>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((w8a16_batched_kernel<FUSED, FP8, 2, 32>), grid, block, 0, s, a);
+    } else {
+        if (k64) hipLaunchKernelGGL((w8a16_batched_kernel<FUSED, FP8, 1, 64>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((w8a16_batched_kernel<FUSED, FP8, 1, 32>), grid, block, 0, s, a);
     }
 }
 
@@ -274,9 +326,7 @@ extern "C" int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, con
     fill_common(a, x, x_stride, m, weight, scales, n, k, group_size);
     a.y = static_cast<uint16_t*>(y);
     a.y_stride = y_stride;
-    const dim3 grid((n + kBgRows - 1) / kBgRows, (m + kBgTok - 1) / kBgTok);
-    hipLaunchKernelGGL((w8a16_batched_kernel<false, false>), grid, dim3(kBgThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    launch_batched<false, false>(a, (n + kBgRows - 1) / kBgRows, static_cast<hipStream_t>(stream));
     AF_TRY_LAUNCH();
     return AF_OK;
 }
@@ -297,7 +347,7 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
     if (fp8 && !pool->scales) return AF_ERR_INVALID_ARG;
     if (pool->n_kv_heads <= 0) return AF_ERR_INVALID_ARG;
     const int hd = pool->head_dim;
-    if (hd != 128) return AF_ERR_UNSUPPORTED;  // a workgroup's tiles are d and d + 64
+    if (hd != 128) return AF_ERR_UNSUPPORTED;  // a workgroup's columns are d and d + 64
     const int n = (n_q_heads + 2 * pool->n_kv_heads) * hd;
     if (int st = check_batched(x, x_stride, m, w_qkv, scales, n, k, group_size)) return st;
     if (m == 0) return AF_OK;
@@ -325,12 +375,11 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
         a.v_scales = a.k_scales + pool->n_kv_heads;
     }
     a.d_status = d_status;
-    const dim3 grid(n / kBgRows, (m + kBgTok - 1) / kBgTok);  // two per head
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fp8)
-        hipLaunchKernelGGL((w8a16_batched_kernel<true, true>), grid, dim3(kBgThreads), 0, s, a);
+        launch_batched<true, true>(a, n / kBgRows, s);  // eight workgroups per head
     else
-        hipLaunchKernelGGL((w8a16_batched_kernel<true, false>), grid, dim3(kBgThreads), 0, s, a);
+        launch_batched<true, false>(a, n / kBgRows, s);
     AF_TRY_LAUNCH();
     return AF_OK;
 }
