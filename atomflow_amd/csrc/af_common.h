@@ -101,6 +101,7 @@ struct PrefixPartialArgs {
     const float* scales;  // FP8 pools: this layer's [2][n_kv_heads]; NULL for fp16
     const int32_t* table;
     int bs_log2;
+    int64_t total_blocks;  // block ids are clamped to [0, total_blocks)
     int prefix_len;
     int batch;
     int n_kv_heads;

@@ -1036,7 +1036,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
                  !aligned16(cos_table) || !aligned16(sin_table))
               : !d_seq_lens)
         return AF_ERR_INVALID_ARG;
-    if (layer < 0 || layer >= pool->n_layers) return AF_ERR_INVALID_ARG;
+    if (layer < 0 || layer >= pool->n_layers || pool->total_blocks <= 0) return AF_ERR_INVALID_ARG;
     const int hd = pool->head_dim, nkv = pool->n_kv_heads;
     if (int st = check_heads(hd, n_q_heads, nkv)) return st;
     const int bs = pool->block_size;
@@ -1136,6 +1136,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
         pp.scales = a.scales;
         pp.table = prefix.table;
         pp.bs_log2 = a.block_shift;
+        pp.total_blocks = a.total_blocks;
         pp.prefix_len = prefix.len;
         pp.batch = batch;
         pp.n_kv_heads = nkv;

@@ -85,6 +85,7 @@ struct PrefillArgs {
     // logical row t lives in slot table[t >> bs_log2] * block_size + t % block_size.
     const int32_t* table;
     int32_t bs_log2;
+    int32_t max_block;  // table entries are clamped to [0, max_block] (the pool's last block)
     // FP8 pools: this layer's fp32 scales [2][n_kv_heads] (K, V); the slabs hold
     // E4M3 codes (one byte per element).
     const float* scales;
@@ -162,13 +163,18 @@ __device__ __forceinline__ void dma_tile(const char* base, uint32_t row_bytes, i
 }
 
 // Physical blocks of the rows this lane fetches for tile `kt` (paged pools).
-__device__ __forceinline__ void tile_blocks(const int32_t* table, int bs_log2, int kt, int kv_len,
-                                            int wave, int lane, int (&blk)[4]) {
+__device__ __forceinline__ void tile_blocks(const int32_t* table, int bs_log2, int max_block, int kt,
+                                            int kv_len, int wave, int lane, int (&blk)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int key = min(kt * kPfKeys + 16 * wave + 4 * i + (lane >> 4), kv_len - 1);
-        blk[i] = table[key >> bs_log2];
+        blk[i] = min(max(table[key >> bs_log2], 0), max_block);  // never address outside the pool
     }
+}
+
+// Physical block of logical row `key` (paged pools), clamped to the pool.
+__device__ __forceinline__ int table_block(const PrefillArgs& a, int key) {
+    return min(max(a.table[key >> a.bs_log2], 0), a.max_block);
 }
 
 // FP8 pools: tile rows go through registers, 32 codes of K and of V per thread
@@ -363,20 +369,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     Fp8Tile f8;
     const int key_lo = kt_lo * kPfKeys;
     if constexpr (FP8) {
-        if constexpr (PAGED) blk8 = a.table[min(key_lo + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
+        if constexpr (PAGED) blk8 = table_block(a, min(key_lo + (tid >> 2), a.kv_len - 1));
         fp8_load<PAGED>(kb, vb, a.kv_row_bytes, key_lo, a.kv_len, tid, blk8, a.bs_log2, f8);
         fp8_store(s_lds, s_lds + kVBase, tid, f8);
         if constexpr (PAGED)
             if (kt_lo + 1 < n_kt)
-                blk8 = a.table[min(key_lo + kPfKeys + (tid >> 2), a.kv_len - 1) >> a.bs_log2];
+                blk8 = table_block(a, min(key_lo + kPfKeys + (tid >> 2), a.kv_len - 1));
     } else {
-        if constexpr (PAGED) tile_blocks(a.table, a.bs_log2, kt_lo, a.kv_len, wave, lane, blk);
+        if constexpr (PAGED)
+            tile_blocks(a.table, a.bs_log2, a.max_block, kt_lo, a.kv_len, wave, lane, blk);
         dma_tile<true, PAGED>(kb, a.kv_row_bytes, key_lo, a.kv_len, wave, lane, s_lds, blk,
                               a.bs_log2);
         dma_tile<false, PAGED>(vb, a.kv_row_bytes, key_lo, a.kv_len, wave, lane, s_lds + kVBase,
                                blk, a.bs_log2);
         if constexpr (PAGED)
-            if (kt_lo + 1 < n_kt) tile_blocks(a.table, a.bs_log2, kt_lo + 1, a.kv_len, wave, lane, blk);
+            if (kt_lo + 1 < n_kt)
+                tile_blocks(a.table, a.bs_log2, a.max_block, kt_lo + 1, a.kv_len, wave, lane, blk);
     }
     if (a.cos_t) {  // packed partials with RoPE (wave-uniform)
         // Whole 32-bit words in and out: two fp16 elements per word, low half
@@ -450,8 +458,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
                                 a.bs_log2, f8);
                 if constexpr (PAGED)
                     if (kt + 2 < n_kt)
-                        blk8 = a.table[min((kt + 2) * kPfKeys + (tid >> 2), a.kv_len - 1) >>
-                                       a.bs_log2];
+                        blk8 = table_block(a, min((kt + 2) * kPfKeys + (tid >> 2), a.kv_len - 1));
             } else {
                 dma_tile<true, PAGED>(kb, a.kv_row_bytes, (kt + 1) * kPfKeys, a.kv_len, wave, lane,
                                       s_lds + (BUF ^ 1) * kTileBytes, blk, a.bs_log2);
@@ -460,7 +467,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
                                        a.bs_log2);
                 if constexpr (PAGED)
                     if (kt + 2 < n_kt)
-                        tile_blocks(a.table, a.bs_log2, kt + 2, a.kv_len, wave, lane, blk);
+                        tile_blocks(a.table, a.bs_log2, a.max_block, kt + 2, a.kv_len, wave, lane,
+                                    blk);
             }
         }
         const int key0 = kt * kPfKeys;
@@ -614,6 +622,7 @@ int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream) {
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
     a.table = p.table;
     a.bs_log2 = p.bs_log2;
+    a.max_block = int32_t(std::min<int64_t>(p.total_blocks - 1, INT32_MAX));
     a.scales = p.scales;
     a.q_group = p.group;
     a.key_splits = p.key_splits;
@@ -681,7 +690,7 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
         n_q_heads <= 0 || max_blocks <= 0)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
-        n_q_heads % pool->n_kv_heads)
+        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0)
         return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
@@ -716,6 +725,7 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
     a.table = d_block_table;
     a.bs_log2 = __builtin_ctz(unsigned(bs));
+    a.max_block = int32_t(std::min<int64_t>(pool->total_blocks - 1, INT32_MAX));
     return launch_prefill(a, static_cast<hipStream_t>(stream));
 }
 
@@ -754,7 +764,7 @@ extern "C" int af_paged_prefill_attention_batched(
         n_tiles < 0 || n_q_heads <= 0 || max_blocks <= 0)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
-        n_q_heads % pool->n_kv_heads)
+        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0)
         return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
@@ -785,6 +795,7 @@ extern "C" int af_paged_prefill_attention_batched(
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(kPfHd)));
     a.table = d_tables;
     a.bs_log2 = __builtin_ctz(unsigned(bs));
+    a.max_block = int32_t(std::min<int64_t>(pool->total_blocks - 1, INT32_MAX));
     a.tile_map = d_tile_map;
     a.chunks = d_chunks;
     a.max_blocks = max_blocks;
