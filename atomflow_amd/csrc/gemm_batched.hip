@@ -94,9 +94,11 @@ struct WChunk<32> {
 // TT token tiles x KC k per chunk; DEPTH chunks in flight per wave.
 template <bool FUSED, bool FP8, int TT, int KC>
 __global__ __launch_bounds__(kBgThreads, 4) void w8a16_batched_kernel(const BatchedArgs a) {
-    constexpr int DEPTH = TT == 1 ? 6 : 3;  // <= 128 VGPRs: two workgroups per CU
+    constexpr int DEPTH = TT == 1 ? 6 : (KC == 64 ? 2 : 3);  // <= 128 VGPRs: two workgroups per CU
     constexpr int XV = KC / 32;  // 16-byte x loads per token tile per chunk
     __shared__ float s_red[kBgParts][TT * 4][64];
+    // KC = 64: each wave's x chunk goes through LDS (see below), 2 KB per token tile.
+    __shared__ uint4 s_x[KC == 64 ? kBgParts : 1][TT][2][64];
     __shared__ int32_t s_pos[FUSED ? kBgTile * TT : 1];
     __shared__ int64_t s_slot[FUSED ? kBgTile * TT : 1];
 
@@ -123,11 +125,30 @@ __global__ __launch_bounds__(kBgThreads, 4) void w8a16_batched_kernel(const Batc
     // its own A row, and those rows' outputs are never written. (Loading zeros
     // there instead made the compiler select between the x address and a
     // scratch copy of zero, i.e. flat loads, at twice the kernel's time.)
-    const uint16_t* xr[TT];
+    //
+    // KC = 64: x is loaded row-contiguous, not in the MFMA operand layout (which
+    // gives the 16 lanes of a k block 16 different token rows, so each load
+    // instruction would touch 16 half-used cache lines). Load v of a token tile
+    // covers tokens 8v .. 8v+7, one 128-byte line (64 k) per 8 lanes: lane l
+    // fetches piece p = (l % 8) ^ ((r / 2) % 8) of token r = 8v + l / 8. The chunk
+    // is written to the wave's LDS stage in lane order and read back in operand
+    // order; the XOR makes the read of the 16 lanes of a k block hit 16 distinct
+    // 16-byte bank groups.
+    const uint16_t* xr[TT][KC / 32];
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
-        const int tok = min(t0 + kBgTile * tt + j, a.m - 1);
-        xr[tt] = a.x + size_t(tok) * a.x_stride + kbase;
+        if constexpr (KC == 64) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const int r = 8 * v + (lane >> 3);
+                const int piece = (lane & 7) ^ ((r >> 1) & 7);
+                const int tok = min(t0 + kBgTile * tt + r, a.m - 1);
+                xr[tt][v] = a.x + size_t(tok) * a.x_stride + g_lo * a.group_size + 8 * piece;
+            }
+        } else {
+            const int tok = min(t0 + kBgTile * tt + j, a.m - 1);
+            xr[tt][0] = a.x + size_t(tok) * a.x_stride + kbase;
+        }
     }
 
     WChunk<KC> wq[DEPTH];
@@ -144,7 +165,7 @@ __global__ __launch_bounds__(kBgThreads, 4) void w8a16_batched_kernel(const Batc
         for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
             for (int v = 0; v < XV; ++v)
-                xq[slot][tt][v] = *reinterpret_cast<const uint4*>(xr[tt] + size_t(c) * KC + 8 * v);
+                xq[slot][tt][v] = *reinterpret_cast<const uint4*>(xr[tt][v] + size_t(c) * KC);
     };
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i)
@@ -176,10 +197,33 @@ __global__ __launch_bounds__(kBgThreads, 4) void w8a16_batched_kernel(const Batc
                     wb[0] = e4m3x8(wq[i].v.x, wq[i].v.y);
                 }
                 half8_t xa[TT][XV];
+                if constexpr (KC == 64) {
+                    // Through the LDS stage: MFMA v takes piece 2 sub + v of token j.
 #pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
+                    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-                    for (int v = 0; v < XV; ++v) xa[tt][v] = __builtin_bit_cast(half8_t, xq[i][tt][v]);
+                        for (int v = 0; v < 2; ++v) {
+                            // (a value store: storing the array element directly became a
+                            // copy out of private memory and kept xq in scratch)
+                            const uint4 val = xq[i][tt][v];
+                            s_x[part][tt][v][lane] = make_uint4(val.x, val.y, val.z, val.w);
+                        }
+                    // The stage writes and reads index one LDS array at run time, so the
+                    // compiler keeps their order; the wait orders them in the LDS queue.
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+                        for (int v = 0; v < 2; ++v) {
+                            const int q = 2 * sub + v;
+                            const int pos = 8 * (j & 7) + (q ^ ((j >> 1) & 7));
+                            xa[tt][v] = __builtin_bit_cast(half8_t, s_x[part][tt][j >> 3][pos]);
+                        }
+                } else {
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt)
+                        xa[tt][0] = __builtin_bit_cast(half8_t, xq[i][tt][0]);
+                }
                 if (c + DEPTH < chunks) issue(i, c + DEPTH);  // refill the slot DEPTH chunks ahead
 #pragma unroll
                 for (int v = 0; v < XV; ++v)
