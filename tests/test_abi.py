@@ -83,6 +83,32 @@ def test_default_split_counts():
     assert kv.default_splits(0, 1, 8) == 1
 
 
+def test_shared_prefix_argument_checks_without_gpu():
+    """af_paged_attention_shared_prefix validates its arguments before any device
+    call: a negative prefix, a missing prefix table, more key splits than 64-row
+    tiles, a prefix past the table, head_dim other than 128, an empty pool."""
+    import ctypes
+    from atomflow_amd import kv
+    lib = atomflow_amd.lib()
+    fake = 0x10000  # never dereferenced: every call below fails validation first
+    pool = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 128, 1000)
+
+    def call(p, prefix_table, prefix, psplits, max_blocks=64):
+        return lib.af_paged_attention_shared_prefix(
+            fake, 3072, ctypes.byref(p), 0, prefix_table, prefix, psplits, fake, max_blocks, fake,
+            4, 1000, fake, 3072, 24, 0, fake, 1 << 30, None)
+
+    assert call(pool, fake, -1, 0) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert call(pool, None, 200, 0) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert call(pool, fake, 200, -1) == atomflow_amd.AF_ERR_INVALID_ARG
+    assert call(pool, fake, 200, 5) == atomflow_amd.AF_ERR_INVALID_ARG  # ceil(200 / 64) = 4
+    assert call(pool, fake, 64 * 16 + 1, 0) == atomflow_amd.AF_ERR_OUT_OF_RANGE
+    p64 = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 64, 1000)
+    assert call(p64, fake, 200, 0) == atomflow_amd.AF_ERR_UNSUPPORTED
+    empty = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 128, 0)
+    assert call(empty, fake, 200, 0) == atomflow_amd.AF_ERR_INVALID_ARG
+
+
 def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(atomflow_amd, "_lib", None)
     monkeypatch.setattr(atomflow_amd, "LIB_PATH", "/nonexistent/libatomflow_kv.so")
