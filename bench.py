@@ -365,7 +365,8 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
 
 
 def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
-    """Continuous batching through the Scheduler: configs[2]'s
+    """Continuous batching through the Scheduler (the intended caller of the paged path,
+    server_engine.cu:55-68): configs[2]'s
     32 sequences (contexts uniform in [128, 8192]) decoding while a 2048-token prompt
     arrives every step and is prefilled in 512-token chunks under a 2048-token step
     budget. A step = the host plan (af_sched_step) + upload of slots / positions /
@@ -611,7 +612,7 @@ def bench_gemv(dev, kv, lib, steps, warmup):
 
 
 def bench_weights(dev, path_dir="/tmp"):
-    """Loading the reference's .bin format: a
+    """Loading the reference's .bin format (weight_loader.h:23-130): a
     Llama-3.2-3B-shaped file (header of the real model, random contents) is
     uploaded by af_weights_upload (one streamed block through pinned double
     buffers) and, for comparison, the way the reference engine does it
@@ -873,7 +874,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the KV path is single-GPU; DESIGN.md describes how it would shard)", file=sys.stderr)
+              "(the KV path runs on one GPU here; sharding is a design note only)", file=sys.stderr)
         sys.exit(2)
     import atomflow_amd
     from atomflow_amd import device as dev

@@ -4,8 +4,8 @@ The reference's ServerEngine::step is a stub whose comment lists the intended
 iteration (src/experimental/server_arch/server_engine.cu:55-68): take pending
 requests from a queue, build a micro-batch, look up each active sequence's
 PageTable and run the batched attention, then advance token counts and retire
-finished sequences. SURVEY.md names admission control on num_free_blocks()
-(paged_kv_manager.h:115). The rules below fill that in; the C++ Scheduler
+finished sequences. Admission control follows the BlockManager's
+num_free_blocks() (paged_kv_manager.h:115). The rules below fill that in; the C++ Scheduler
 (atomflow_amd/csrc/scheduler.cpp) must reproduce them decision for decision.
 
 A request is (id, prompt_len, max_new_tokens). Its sequence holds prompt_eff
