@@ -137,20 +137,6 @@ struct Layout {
     __device__ static int dim(int i, int j, int u) { return (i * 128 + j * 16) / kElem + u; }
 };
 
-// One rotation of pair (x, y) by (c, s): separately rounded fp32 products and
-// sum, then fp16 round-to-nearest-even — the reference's rope_kernel numerics
-// (src/kernel/rope.cu:34-35); contraction into an FMA is disabled.
-__device__ __forceinline__ void rotate_pair(uint16_t x, uint16_t y, float c, float s,
-                                            uint16_t& xo, uint16_t& yo) {
-#pragma clang fp contract(off)
-    const float xf = float(__builtin_bit_cast(f16, x)), yf = float(__builtin_bit_cast(f16, y));
-    const float xc = xf * c;
-    const float ys = yf * s;
-    const float xs = xf * s;
-    const float yc = yf * c;
-    xo = __builtin_bit_cast(uint16_t, f16(xc - ys));
-    yo = __builtin_bit_cast(uint16_t, f16(xs + yc));
-}
 
 __device__ __forceinline__ uint32_t quantize_fp8_dev(uint16_t h, float scale) {
     float v = float(__builtin_bit_cast(f16, h)) / scale;
@@ -366,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             const int gh = it / half, d = it % half;
             if (it >= kRopeItems || !(gh < GROUP || owner)) continue;
             uint16_t xo, yo;
-            rotate_pair(rx[r], ry[r], rc[r], rs[r], xo, yo);
+            rope_rotate(rx[r], ry[r], rc[r], rs[r], xo, yo);
             if (gh < GROUP) {
                 s_q[gh * HD + d] = xo;
                 s_q[gh * HD + d + half] = yo;

@@ -184,19 +184,10 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(
     const int kind = head < n_q_heads ? 0 : (head < n_q_heads + n_kv_heads ? 1 : 2);  // Q, K, V
     uint16_t out[4] = {yv[0], yv[1], yv[2], yv[3]};
     if (kind < 2) {
-#pragma clang fp contract(off)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {  // the reference's rope_kernel arithmetic, rope.cu:30-45
-            const float c = cos_t[size_t(pos) * half + dA + p];
-            const float s = sin_t[size_t(pos) * half + dA + p];
-            const float xf = h2f(yv[p]), yf = h2f(yv[2 + p]);
-            const float xc = xf * c;
-            const float ys = yf * s;
-            const float xs = xf * s;
-            const float yc = yf * c;
-            out[p] = f2h(xc - ys);
-            out[2 + p] = f2h(xs + yc);
-        }
+        for (int p = 0; p < 2; ++p)  // the reference's rope_kernel arithmetic, rope.cu:30-45
+            rope_rotate(yv[p], yv[2 + p], cos_t[size_t(pos) * half + dA + p],
+                        sin_t[size_t(pos) * half + dA + p], out[p], out[2 + p]);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) qkv[rows[r]] = out[r];

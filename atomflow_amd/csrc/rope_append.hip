@@ -4,8 +4,8 @@
 // Numerics follow the reference bit for bit: each rotated element is
 // (x*c - y*s) or (x*s + y*c) with separately rounded fp32 products and sum
 // (src/kernel/rope.cu:34-35,43-44), then one fp32 -> fp16 round-to-nearest-even
-// (the `(T)` cast). `#pragma clang fp contract(off)` keeps hipcc from fusing the
-// product into an FMA, which would change the last bit.
+// (the `(T)` cast). rope_rotate (af_device.h) disables FMA contraction, which
+// would change the last bit.
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -20,17 +20,8 @@ namespace {
 __device__ __forceinline__ void rotate4(const uint16_t (&x)[4], const uint16_t (&y)[4],
                                         const float (&c)[4], const float (&s)[4],
                                         uint16_t (&xo)[4], uint16_t (&yo)[4]) {
-#pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float xf = h2f(x[i]), yf = h2f(y[i]);
-        const float xc = xf * c[i];
-        const float ys = yf * s[i];
-        const float xs = xf * s[i];
-        const float yc = yf * c[i];
-        xo[i] = f2h(xc - ys);
-        yo[i] = f2h(xs + yc);
-    }
+    for (int i = 0; i < 4; ++i) rope_rotate(x[i], y[i], c[i], s[i], xo[i], yo[i]);
 }
 
 __device__ __forceinline__ void load4h(const uint16_t* p, uint16_t (&v)[4]) {
