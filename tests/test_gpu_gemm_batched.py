@@ -38,17 +38,21 @@ def batched_gpu(w, xs, s, group=128, x_stride=None):
     return y.download(np.float16, (max(m, 1), n))[:m]
 
 
-@pytest.mark.parametrize("n,k,m", [(QKV, 3072, 32), (QKV, 3072, 1), (3072, 3072, 7),
-                                   (8192, 3072, 45), (3072, 8192, 16), (100, 1024, 33)])
-def test_gemm_batched_parity(gpu, n, k, m):
-    say(f"batched gemm n={n} k={k} m={m}")
-    w, _, s = gemv_case(n, k, 0xA70F30 + n + k, group=128)
+@pytest.mark.parametrize("n,k,m,group", [(QKV, 3072, 32, 128), (QKV, 3072, 1, 128),
+                                         (3072, 3072, 7, 128), (8192, 3072, 45, 128),
+                                         (3072, 8192, 16, 128), (100, 1024, 33, 128),
+                                         (512, 1024, 20, 32), (256, 768, 5, 96), (272, 640, 3, 64)])
+def test_gemm_batched_parity(gpu, n, k, m, group):
+    """Group sizes 32 and 96 take the 32-k chunk path (8 weight bytes per MFMA),
+    the others the 64-k path with the activations staged through LDS."""
+    say(f"batched gemm n={n} k={k} m={m} group={group}")
+    w, _, s = gemv_case(n, k, 0xA70F30 + n + k, group=group)
     xs = np.random.default_rng(m + n).standard_normal((m, k)).astype(np.float16)
-    got = batched_gpu(w, xs, s, 128, x_stride=k + (8 if m % 2 else 0)).astype(np.float64)
+    got = batched_gpu(w, xs, s, group, x_stride=k + (8 if m % 2 else 0)).astype(np.float64)
     assert np.all(np.isfinite(got))
     for i in range(m):
-        y64 = oracle.w8a16_gemv_f64(w, xs[i], s, 128)
-        bound = k * 2.0 ** -24 * gemv_abs_terms(w, xs[i], s, 128)
+        y64 = oracle.w8a16_gemv_f64(w, xs[i], s, group)
+        bound = k * 2.0 ** -24 * gemv_abs_terms(w, xs[i], s, group)
         err = np.abs(got[i] - y64)
         assert np.all(err <= 0.5 * fp16_ulp(y64) + bound), f"token {i}: max err {err.max():.3e}"
 
@@ -69,11 +73,11 @@ def test_gemm_batched_rejects_bad_shapes(gpu):
     assert call(dx.ptr, 1024, 0, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, None) == 0
 
 
-@pytest.mark.parametrize("fp8", [False, True])
-def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
-    say(f"paged qkv rope append, fp8 {fp8}")
+@pytest.mark.parametrize("fp8,group", [(False, 128), (True, 128), (False, 32)])
+def test_paged_qkv_rope_append_equals_unfused(gpu, fp8, group):
+    say(f"paged qkv rope append, fp8 {fp8}, group {group}")
     k_in, m, bs, total, max_pos = 3072, 19, 16, 96, 700
-    w, _, s = gemv_case(QKV, k_in, 0xA70F31, group=128)
+    w, _, s = gemv_case(QKV, k_in, 0xA70F31, group=group)
     xs = np.random.default_rng(3).standard_normal((m, k_in)).astype(np.float16)
     r = np.random.default_rng(4)
     slots = r.permutation(total * bs)[:m].astype(np.int64)
@@ -96,10 +100,10 @@ def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
     q1 = dev.DeviceBuffer(m * QKV * 2)
     st = up(np.zeros(1, np.int32))
     kv.launch_paged_qkv_rope_append(dx, k_in, m, dw, ds, k_in, q1, pools[0][1], 1, d_slots,
-                                    d_pos, d_c, d_s, max_pos, NQ, d_status=st)
+                                    d_pos, d_c, d_s, max_pos, NQ, d_status=st, group_size=group)
     # unfused: batched projection, then the paged append
     q2 = dev.DeviceBuffer(m * QKV * 2)
-    kv.launch_w8a16_gemm_batched(dx, k_in, m, dw, ds, q2, QKV, QKV, k_in)
+    kv.launch_w8a16_gemm_batched(dx, k_in, m, dw, ds, q2, QKV, QKV, k_in, group)
     kv.launch_paged_rope_append(q2, m, pools[1][1], 1, d_slots, d_pos, d_c, d_s, max_pos, NQ)
     assert np.array_equal(q1.download(np.uint16, (m, QKV)), q2.download(np.uint16, (m, QKV)))
     p1 = pools[0][0].download(np.uint8, (pool_bytes,))
@@ -108,7 +112,7 @@ def test_paged_qkv_rope_append_equals_unfused(gpu, fp8):
     assert not np.array_equal(p1, init)  # something was appended
     assert st.download(np.int32, (1,))[0] == atomflow_amd.AF_ERR_OUT_OF_RANGE
     # the out-of-range token's projection is unrotated: equal to the plain projection
-    plain = batched_gpu(w, xs, s)
+    plain = batched_gpu(w, xs, s, group)
     assert np.array_equal(q1.download(np.uint16, (m, QKV))[5], plain[5].view(np.uint16))
 
 
