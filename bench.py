@@ -44,6 +44,7 @@ THETA = 500000.0
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx8k_pmc.txt")
+PAGED_PMC_SUMMARY = os.path.join(ROOT, "profiles", "paged_attn_pmc.txt")
 METRIC = "decode-attn KV-read GB/s (% of 8 TB/s HBM) + us/layer-step at ctx 8k"
 
 
@@ -71,12 +72,12 @@ def parse():
     return ap.parse_args()
 
 
-def read_traffic():
-    """HBM bytes per attention launch from the committed PMC summary (or None)."""
-    if not os.path.exists(PMC_SUMMARY):
+def read_traffic(path=PMC_SUMMARY, key="traffic_bytes_per_launch:"):
+    """HBM bytes per attention launch from a committed PMC summary (or None)."""
+    if not os.path.exists(path):
         return None
-    for line in open(PMC_SUMMARY):
-        if line.startswith("traffic_bytes_per_launch:"):
+    for line in open(path):
+        if line.startswith(key):
             return float(line.split(":", 1)[1])
     return None
 
@@ -819,8 +820,12 @@ def bench_paged(args, dev, kv, lib, info):
                    "unique_kv_bytes_per_layer": unique_tokens * row * 2, "layers": LAYERS},
         "kernels": {"paged_attn_us": round(ms_attn * 1e3, 3)},
         "roofline_bytes": "unique KV rows (shared prefix once)" if cfg == 4 else "KV rows attended",
+        # traffic: measured HBM bytes per attention call (FETCH_SIZE + WRITE_SIZE passes, scaled
+        # by a copy kernel) from the committed PMC summary of this config
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(PAGED_PMC_SUMMARY,
+                                             f"traffic_bytes_per_launch configs[{cfg - 1}]:")},
         "cpu_baseline": None,
     }
     if cfg == 4:
