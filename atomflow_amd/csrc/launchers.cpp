@@ -159,6 +159,83 @@ void launch_kv_copy_blocks(const af_kv_pool& pool, const int32_t* d_copies, cons
     check(af_kv_copy_blocks(&pool, d_copies, d_count, max_copies, stream), "launch_kv_copy_blocks");
 }
 
+void launch_paged_decode_fused(__half* qkv_out, int batch, const af_kv_pool& pool, int layer,
+                               const int64_t* d_slots, const int32_t* d_positions,
+                               const float* cos_table, const float* sin_table, int max_pos,
+                               const int32_t* d_block_tables, int max_blocks_per_seq,
+                               int max_seq_len, __half* out, int out_stride, int n_q_heads,
+                               int num_splits, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    check(af_paged_decode_fused(qkv_out, batch, &pool, layer, d_slots, d_positions, cos_table,
+                                sin_table, max_pos, d_block_tables, max_blocks_per_seq,
+                                max_seq_len, out, out_stride, n_q_heads, num_splits, workspace,
+                                workspace_bytes, stream),
+          "launch_paged_decode_fused");
+}
+
+void launch_paged_attention_shared_prefix(const __half* q, int q_stride, const af_kv_pool& pool,
+                                          int layer, const int32_t* d_prefix_table,
+                                          int prefix_len, int prefix_splits,
+                                          const int32_t* d_block_tables, int max_blocks_per_seq,
+                                          const int32_t* d_seq_lens, int batch, int max_seq_len,
+                                          __half* out, int out_stride, int n_q_heads,
+                                          int num_splits, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+    check(af_paged_attention_shared_prefix(q, q_stride, &pool, layer, d_prefix_table, prefix_len,
+                                           prefix_splits, d_block_tables, max_blocks_per_seq,
+                                           d_seq_lens, batch, max_seq_len, out, out_stride,
+                                           n_q_heads, num_splits, workspace, workspace_bytes,
+                                           stream),
+          "launch_paged_attention_shared_prefix");
+}
+
+void launch_paged_decode_fused_shared_prefix(
+    __half* qkv_out, int batch, const af_kv_pool& pool, int layer, const int64_t* d_slots,
+    const int32_t* d_positions, const float* cos_table, const float* sin_table, int max_pos,
+    const int32_t* d_prefix_table, int prefix_len, int prefix_splits,
+    const int32_t* d_block_tables, int max_blocks_per_seq, int max_seq_len, __half* out,
+    int out_stride, int n_q_heads, int num_splits, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+    check(af_paged_decode_fused_shared_prefix(
+              qkv_out, batch, &pool, layer, d_slots, d_positions, cos_table, sin_table, max_pos,
+              d_prefix_table, prefix_len, prefix_splits, d_block_tables, max_blocks_per_seq,
+              max_seq_len, out, out_stride, n_q_heads, num_splits, workspace, workspace_bytes,
+              stream),
+          "launch_paged_decode_fused_shared_prefix");
+}
+
+void launch_w8a16_gemv_pair(const View& act_x, const View& w0, const View& s0, View& y0,
+                            const View& w1, const View& s1, View& y1, int group_size,
+                            hipStream_t stream) {
+    check(af_w8a16_gemv_pair(act_x.data_ptr, static_cast<const uint8_t*>(w0.data_ptr),
+                             s0.data_ptr, y0.data_ptr, int(w0.dims[0]),
+                             static_cast<const uint8_t*>(w1.data_ptr), s1.data_ptr, y1.data_ptr,
+                             int(w1.dims[0]), int(w0.dims[1]), group_size, stream),
+          "launch_w8a16_gemv_pair");
+}
+
+void launch_w8a16_gemm_batched(const __half* x, int64_t x_stride, int m, const View& weight,
+                               const View& scales, __half* y, int64_t y_stride, int group_size,
+                               hipStream_t stream) {
+    check(af_w8a16_gemm_batched(x, x_stride, m, static_cast<const uint8_t*>(weight.data_ptr),
+                                scales.data_ptr, y, y_stride, int(weight.dims[0]),
+                                int(weight.dims[1]), group_size, stream),
+          "launch_w8a16_gemm_batched");
+}
+
+void launch_paged_qkv_rope_append(const __half* x, int64_t x_stride, int m, const View& w_qkv,
+                                  const View& scales, int group_size, __half* qkv_out,
+                                  const af_kv_pool& pool, int layer, const int64_t* d_slots,
+                                  const int32_t* d_positions, const float* cos_table,
+                                  const float* sin_table, int max_pos, int n_q_heads,
+                                  int32_t* d_status, hipStream_t stream) {
+    check(af_paged_qkv_rope_append(x, x_stride, m, static_cast<const uint8_t*>(w_qkv.data_ptr),
+                                   scales.data_ptr, int(w_qkv.dims[1]), group_size, qkv_out,
+                                   &pool, layer, d_slots, d_positions, cos_table, sin_table,
+                                   max_pos, n_q_heads, d_status, stream),
+          "launch_paged_qkv_rope_append");
+}
+
 ArenaAllocator::ArenaAllocator(size_t total_size) {
     capacity_ = align_to_128(total_size);
     offset_ = 0;

@@ -104,3 +104,48 @@ void launch_paged_attention(const __half* q, int q_stride, const af_kv_pool& poo
 
 void launch_kv_copy_blocks(const af_kv_pool& pool, const int32_t* d_copies, const int32_t* d_count,
                            int max_copies, hipStream_t stream);
+
+// af_paged_decode_fused: paged RoPE + append + attention (lengths = positions + 1).
+void launch_paged_decode_fused(__half* qkv_out, int batch, const af_kv_pool& pool, int layer,
+                               const int64_t* d_slots, const int32_t* d_positions,
+                               const float* cos_table, const float* sin_table, int max_pos,
+                               const int32_t* d_block_tables, int max_blocks_per_seq,
+                               int max_seq_len, __half* out, int out_stride, int n_q_heads,
+                               int num_splits, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
+// af_paged_attention_shared_prefix: forks of one prompt; rows [0, prefix_len)
+// through d_prefix_table once for the batch, the rest per sequence.
+void launch_paged_attention_shared_prefix(const __half* q, int q_stride, const af_kv_pool& pool,
+                                          int layer, const int32_t* d_prefix_table,
+                                          int prefix_len, int prefix_splits,
+                                          const int32_t* d_block_tables, int max_blocks_per_seq,
+                                          const int32_t* d_seq_lens, int batch, int max_seq_len,
+                                          __half* out, int out_stride, int n_q_heads,
+                                          int num_splits, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream);
+
+// af_paged_decode_fused_shared_prefix: the fused step of a shared-prefix batch.
+void launch_paged_decode_fused_shared_prefix(
+    __half* qkv_out, int batch, const af_kv_pool& pool, int layer, const int64_t* d_slots,
+    const int32_t* d_positions, const float* cos_table, const float* sin_table, int max_pos,
+    const int32_t* d_prefix_table, int prefix_len, int prefix_splits,
+    const int32_t* d_block_tables, int max_blocks_per_seq, int max_seq_len, __half* out,
+    int out_stride, int n_q_heads, int num_splits, void* workspace, size_t workspace_bytes,
+    hipStream_t stream);
+
+// W8A16 projections beside the path: the MLP's gate and up GEMVs in one launch
+// (engine.cu:418-436 issues two launch_w8a16_gemv), the batched projection of m
+// tokens, and the paged serving step's QKV projection + RoPE + append.
+void launch_w8a16_gemv_pair(const View& act_x, const View& w0, const View& s0, View& y0,
+                            const View& w1, const View& s1, View& y1, int group_size,
+                            hipStream_t stream);
+void launch_w8a16_gemm_batched(const __half* x, int64_t x_stride, int m, const View& weight,
+                               const View& scales, __half* y, int64_t y_stride, int group_size,
+                               hipStream_t stream);
+void launch_paged_qkv_rope_append(const __half* x, int64_t x_stride, int m, const View& w_qkv,
+                                  const View& scales, int group_size, __half* qkv_out,
+                                  const af_kv_pool& pool, int layer, const int64_t* d_slots,
+                                  const int32_t* d_positions, const float* cos_table,
+                                  const float* sin_table, int max_pos, int n_q_heads,
+                                  int32_t* d_status, hipStream_t stream);

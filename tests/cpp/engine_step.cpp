@@ -3,7 +3,8 @@
 // include/server/scheduler.h) the way the reference engine calls its launchers
 // (src/core/engine.cu:326-370: launch_rope, launch_write_kv_cache,
 // launch_cached_attention on one stream), then the paged step of the server
-// sandbox (BlockManager fork + copy-on-write, paged append, paged attention).
+// sandbox (BlockManager fork + copy-on-write, paged append, paged attention,
+// and the shared-prefix form over the forked pair).
 // Inputs come from a fixed xorshift stream; inputs and outputs are written to
 // <out_dir>/*.bin so tests/test_gpu_cpp_host.py can check them against the
 // oracle. Exit status 0 only if every call succeeded and the in-program checks
@@ -233,10 +234,36 @@ int paged_step(const std::string& dir, hipStream_t s) {
     launch_paged_attention(reinterpret_cast<const __half*>(d_qkv), QKV, pool, 0, d_tables,
                            max_blocks, d_lens, 3, max_len, reinterpret_cast<__half*>(d_out), Q_DIM,
                            NH, 0, ws, ws_bytes, s);
+    // Seq 2 is a fork of seq 0: their rows [0, 100) hold the same values (the
+    // shared partial tail was copied above). The shared-prefix form over
+    // {seq 0, seq 2} (q rows 0 and 2 of qkv_out: stride 2 * QKV) must agree with
+    // the paged attention of those rows within twice the attention tolerance.
+    std::vector<int32_t> t02(size_t(2) * max_blocks), l02 = {seq_lens[0], seq_lens[2]};
+    std::memcpy(t02.data(), tables.data(), size_t(max_blocks) * 4);
+    std::memcpy(t02.data() + max_blocks, tables.data() + size_t(2) * max_blocks,
+                size_t(max_blocks) * 4);
+    int32_t* d_t02 = dev_upload(t02);
+    int32_t* d_l02 = dev_upload(l02);
+    uint16_t* d_out_sp = nullptr;
+    HIP_OK(hipMalloc(&d_out_sp, size_t(2) * Q_DIM * 2));
+    launch_paged_attention_shared_prefix(reinterpret_cast<const __half*>(d_qkv), 2 * QKV, pool, 0,
+                                         d_t02, lens[0], 0, d_t02, max_blocks, d_l02, 2, max_len,
+                                         reinterpret_cast<__half*>(d_out_sp), Q_DIM, NH, 0, ws,
+                                         ws_bytes, s);
     HIP_OK(hipStreamSynchronize(s));
     auto pool_out = dev_download(static_cast<const uint16_t*>(pool.base), pool_halves);
     auto qkv_out = dev_download(d_qkv, size_t(3) * QKV);
     auto out = dev_download(d_out, size_t(3) * Q_DIM);
+    auto out_sp = dev_download(d_out_sp, size_t(2) * Q_DIM);
+    for (int r = 0; r < 2; ++r)
+        for (int e = 0; e < Q_DIM; ++e) {
+            const float a = __half2float(__ushort_as_half(out_sp[size_t(r) * Q_DIM + e]));
+            const float b = __half2float(__ushort_as_half(out[size_t(2 * r) * Q_DIM + e]));
+            if (!(std::fabs(a - b) <= 4e-3f + 2e-2f * std::fabs(b))) return 20;
+        }
+    HIP_OK(hipFree(d_t02));
+    HIP_OK(hipFree(d_l02));
+    HIP_OK(hipFree(d_out_sp));
     save(dir, "p_pool_out", pool_out.data(), pool_out.size() * 2);
     save(dir, "p_qkv_out", qkv_out.data(), qkv_out.size() * 2);
     save(dir, "p_attn", out.data(), out.size() * 2);

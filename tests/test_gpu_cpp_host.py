@@ -3,8 +3,10 @@ built with the library): one contiguous decode step the way the reference
 engine issues it (launch_rope, launch_write_kv_cache, launch_cached_attention;
 src/core/engine.cu:326-370) and the sandbox's paged step (BlockManager fork +
 copy-on-write, launch_kv_copy_blocks, launch_paged_rope_append,
-launch_paged_attention). The program checks in itself that launch_rope_append
-equals the three-launch sequence bit for bit; here its outputs are checked
+launch_paged_attention), plus launch_paged_attention_shared_prefix over the
+forked pair. The program checks in itself that launch_rope_append equals the
+three-launch sequence bit for bit and that the shared-prefix form agrees with
+the paged attention of the forked pair; here its outputs are checked
 against the oracle: append and copies bit-exact, attention within the
 north-star tolerance of the float64 oracle."""
 import os
