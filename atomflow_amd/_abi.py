@@ -85,6 +85,7 @@ PROTOTYPES = {
     "af_sched_plan_prefix": (I, [P, P, P, P, P]),
     "af_sched_step": (I, [P, P]),
     "af_sched_plan_decode": (I, [P, P, P, P, P]),
+    "af_sched_plan_decode_shared": (I, [P, P, P]),
     "af_sched_plan_prefill": (I, [P, P, P, P, P]),
     "af_sched_plan_copies": (I, [P, P]),
     "af_sched_plan_events": (I, [P, P, P]),

@@ -14,6 +14,8 @@ void StepPlan::clear() {
     decode_seqs.clear();
     decode_slots.clear();
     decode_positions.clear();
+    decode_share_groups.clear();
+    decode_share_rows.clear();
     prefill.clear();
     prefill_slots.clear();
     prefill_positions.clear();
@@ -57,7 +59,7 @@ bool Scheduler::evict_oldest(StepPlan* plan) {
 
 // After a chunk: a request whose prefill just reached its prefix caches it
 // (a fork of its sequence, which holds exactly the prefix now).
-void Scheduler::maybe_cache(StepPlan* plan, const Entry& e) {
+void Scheduler::maybe_cache(StepPlan* plan, Entry& e) {
     if (!caching(e) || e.prefilled != e.req.prefix_len) return;
     if (find_prefix(e.req.prefix_key, e.req.prefix_len, false) >= 0) return;
     if (int(cache_.size()) >= cfg_.max_cached_prefixes) (void)evict_oldest(plan);
@@ -65,6 +67,9 @@ void Scheduler::maybe_cache(StepPlan* plan, const Entry& e) {
     c.key = e.req.prefix_key;
     c.seq = bm_.fork_sequence(e.seq);
     c.len = e.req.prefix_len;
+    c.group = next_group_++;
+    e.share_group = c.group;
+    e.share_rows = c.len;
     cache_.push_back(c);
     plan->cached.push_back(c.key);
 }
@@ -90,6 +95,8 @@ void Scheduler::preempt_youngest(StepPlan* plan) {
     v.seq = -1;
     v.prompt_eff = v.req.prompt_len + v.generated;
     v.prefilled = 0;
+    v.share_group = -1;
+    v.share_rows = 0;
     plan->preempted.push_back(v.req.id);
     waiting_.push_front(v);
 }
@@ -151,6 +158,8 @@ int Scheduler::step(StepPlan* plan) {
             plan->decode_seqs.push_back(e.seq);
             plan->decode_slots.push_back(slots[j].slot);
             plan->decode_positions.push_back(slots[j].position);
+            plan->decode_share_groups.push_back(e.share_group);
+            plan->decode_share_rows.push_back(e.share_rows);
             if (slots[j].cow.src >= 0) plan->copies.push_back(slots[j].cow);
             ++e.generated;
         }
@@ -213,6 +222,8 @@ int Scheduler::step(StepPlan* plan) {
             cache_.push_back(c);  // youngest
             e.seq = bm_.fork_sequence(c.seq);
             e.prefilled = base;
+            e.share_group = c.group;
+            e.share_rows = c.len;
             plan->prefix_hits.push_back(e.req.id);
         } else {
             e.seq = bm_.create_sequence();
@@ -349,6 +360,17 @@ extern "C" int af_sched_plan_decode(const af_scheduler* s, int64_t* requests, in
         if (seqs) seqs[i] = p.decode_seqs[i];
         if (slots) slots[i] = p.decode_slots[i];
         if (positions) positions[i] = p.decode_positions[i];
+    }
+    return AF_OK;
+}
+
+extern "C" int af_sched_plan_decode_shared(const af_scheduler* s, int64_t* groups,
+                                           int32_t* rows) {
+    if (!s) return AF_ERR_INVALID_ARG;
+    const StepPlan& p = s->plan;
+    for (size_t i = 0; i < p.decode_share_groups.size(); ++i) {
+        if (groups) groups[i] = p.decode_share_groups[i];
+        if (rows) rows[i] = p.decode_share_rows[i];
     }
     return AF_OK;
 }

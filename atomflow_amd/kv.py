@@ -303,6 +303,10 @@ class BlockManager:
         self.block_size = block_size
 
     def close(self):
+        """Destroys the manager, after every Scheduler built on it (a scheduler's
+        teardown frees its cached sequences through the manager)."""
+        for sched in list(getattr(self, "_schedulers", ())):
+            sched.close()
         if self.h:
             lib().af_bm_destroy(self.h)
             self.h = None
@@ -410,7 +414,9 @@ class Scheduler:
 
     ``step()`` returns the plan as a dict: finished / preempted request ids,
     decode [(request, seq, slot, position)], copies [(src, dst, rows)], prefill
-    [(request, seq, p0, n, last, slots)], and the running / waiting counts.
+    [(request, seq, p0, n, last, slots)], and the running / waiting counts;
+    ``arrays`` also holds each decode entry's share group (-1: none) and shared
+    rows (af_sched_plan_decode_shared).
     """
 
     def __init__(self, bm, max_running, max_step_tokens, prefill_chunk, watermark=0,
@@ -420,6 +426,11 @@ class Scheduler:
                                     ctypes.byref(h)), "af_sched_create")
         self.h = h.value
         self.bm = bm  # keeps the manager alive
+        # Strong references both ways: whichever finaliser runs first (the garbage
+        # collector picks the order within a cycle) tears the scheduler down first.
+        if not hasattr(bm, "_schedulers"):
+            bm._schedulers = []
+        bm._schedulers.append(self)
         if max_cached_prefixes:
             self.set_prefix_cache(max_cached_prefixes)
 
@@ -433,6 +444,9 @@ class Scheduler:
         if self.h:
             lib().af_sched_destroy(self.h)
             self.h = None
+        owners = getattr(self.bm, "_schedulers", [])
+        if self in owners:
+            owners.remove(self)
 
     def __del__(self):
         try:
@@ -454,6 +468,8 @@ class Scheduler:
         dslot, dpos = np.zeros(nd, np.int64), np.zeros(nd, np.int32)
         lib().af_sched_plan_decode(self.h, dreq.ctypes.data, dseq.ctypes.data, dslot.ctypes.data,
                                    dpos.ctypes.data)
+        dgrp, drows = np.zeros(nd, np.int64), np.zeros(nd, np.int32)
+        lib().af_sched_plan_decode_shared(self.h, dgrp.ctypes.data, drows.ctypes.data)
         preq, chunks = np.zeros(nc, np.int64), np.zeros((nc, 5), np.int32)
         pslot, ppos = np.zeros(nt, np.int64), np.zeros(nt, np.int32)
         lib().af_sched_plan_prefill(self.h, preq.ctypes.data, chunks.ctypes.data,
@@ -474,14 +490,57 @@ class Scheduler:
         return {
             "finished": [int(x) for x in fin], "preempted": [int(x) for x in pre],
             "decode": [(int(dreq[i]), int(dseq[i]), int(dslot[i]), int(dpos[i])) for i in range(nd)],
+            "decode_shared": [(int(dgrp[i]), int(drows[i])) for i in range(nd)],
             "copies": [tuple(int(x) for x in row) for row in copies],
             "prefill": prefill, "running": nrun, "waiting": nwait,
             "prefix_hits": [int(x) for x in hits], "cached": [int(x) for x in cached],
             "evicted": [int(x) for x in evicted], "cache_entries": int(pc[3]),
             "arrays": {"decode_seqs": dseq, "decode_slots": dslot, "decode_positions": dpos,
+                       "decode_share_groups": dgrp, "decode_share_rows": drows,
                        "prefill_slots": pslot, "prefill_positions": ppos, "copies": copies,
                        "chunks": chunks},
         }
+
+
+def decode_share_segments(groups, rows, min_members=2, min_saved_rows=0):
+    """Orders a decode batch by share group (Scheduler.step's decode_share_groups /
+    decode_share_rows) for one attention launch per segment.
+
+    A group qualifies with at least ``min_members`` entries this step whose
+    shared rows are read ``(members - 1) * rows >= min_saved_rows`` fewer times
+    when attended once (a group's own launches cost about as much as reading
+    10-12k KV rows of 8 heads x 128 on MI355X, so smaller groups run faster in
+    the batch's plain launch).
+
+    Returns (order, segments): ``order`` permutes the decode entries so that
+    entries without a qualifying group come first, then each group's entries
+    together; ``segments`` lists
+    (start, count, prefix_rows) over the permuted batch, prefix_rows 0 for the
+    leading run (plain af_paged_attention) and the group's shared rows otherwise
+    (af_paged_attention_shared_prefix with any member's table as the prefix).
+    """
+    groups = np.asarray(groups, np.int64)
+    rows = np.asarray(rows, np.int32)
+    if len(groups) != len(rows):
+        raise ValueError("groups and rows differ in length")
+    ids, counts = np.unique(groups[groups >= 0], return_counts=True)
+    big = set()
+    for g, c in zip(ids, counts):
+        shared = int(rows[groups == g][0])
+        if c >= min_members and (c - 1) * shared >= min_saved_rows:
+            big.add(int(g))
+    solo = [i for i, g in enumerate(groups) if int(g) not in big]
+    order, segments = list(solo), []
+    if solo:
+        segments.append((0, len(solo), 0))
+    for g in sorted(big):
+        members = [i for i, x in enumerate(groups) if int(x) == g]
+        shared = {int(rows[i]) for i in members}
+        if len(shared) != 1:
+            raise ValueError(f"group {g} has differing shared rows {sorted(shared)}")
+        segments.append((len(order), len(members), shared.pop()))
+        order += members
+    return np.array(order, np.int64), segments
 
 
 def _nonneg(r, what):
@@ -492,7 +551,7 @@ def _nonneg(r, what):
 
 __all__ = [
     "AF_KV_FP16", "AF_KV_FP8_E4M3", "AttentionWorkspace", "BlockManager", "build_rope_cache",
-    "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
+    "decode_share_segments", "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",
     "launch_paged_decode_fused", "launch_paged_rope_append", "launch_qkv_rope_append",
     "launch_w8a16_gemv", "launch_prefill_rope_append", "launch_prefill_attention",

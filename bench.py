@@ -261,6 +261,9 @@ def bench_contiguous(args, dev, kv, lib, info):
         result["serving"] = bench_serving(dev, kv, lib)
         log("serving with a shared 1544-token prompt prefix and the prefix cache ...")
         result["serving_shared_prefix"] = bench_serving(dev, kv, lib, shared_prefix=1544)
+        log("the same, decode attention grouped by the plan's share groups ...")
+        result["serving_shared_prefix_grouped"] = bench_serving(dev, kv, lib, shared_prefix=1544,
+                                                                group_decode=True)
     log("projection GEMVs ...")
     result["gemv"] = bench_gemv(dev, kv, lib, args.steps, args.warmup)
     if not args.no_weights:
@@ -365,7 +368,7 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     return res
 
 
-def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
+def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decode=False):
     """Continuous batching through the Scheduler (the intended caller of the paged path,
     server_engine.cu:55-68): configs[2]'s
     32 sequences (contexts uniform in [128, 8192]) decoding while a 2048-token prompt
@@ -375,7 +378,10 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
     launches: one paged append for every new row (decode tokens and chunk tokens),
     decode attention for the batch, and one batched prefill attention for all chunks.
     With shared_prefix > 0 every arriving prompt starts with the same shared_prefix
-    tokens and the scheduler's prefix cache is on (4 entries)."""
+    tokens and the scheduler's prefix cache is on (4 entries). With group_decode the
+    decode batch is ordered by the plan's share groups (kv.decode_share_segments) and
+    each group of two or more sequences is attended through the shared-prefix entry
+    (its prompt prefix read once per layer), the other sequences by one plain launch."""
     import atomflow_amd
     r = np.random.Generator(np.random.PCG64(0xA70F10 + 6))
     bs, chunk, budget, max_running = 16, 512, 2048, 64
@@ -428,6 +434,12 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
                 ttft.append(k - arrived[c[0]] + 1)
         a = p["arrays"]
         nd = len(p["decode"])
+        segs = [(0, nd, 0)] if nd else []
+        if group_decode and nd:
+            order, segs = kv.decode_share_segments(a["decode_share_groups"],
+                                                   a["decode_share_rows"])
+            for key in ("decode_seqs", "decode_slots", "decode_positions"):
+                a[key] = a[key][order]
         # host -> device: slots / positions of every new row, block tables, chunk descriptors
         slots = np.concatenate([a["decode_slots"], a["prefill_slots"]])
         positions = np.concatenate([a["decode_positions"], a["prefill_positions"]])
@@ -457,9 +469,16 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
             q = qkv.ptr + l * rows * QKV * 2
             kv.launch_paged_rope_append(q, n_rows, pool, l, bufs[0], bufs[1], d_cos, d_sin,
                                         max_pos, NQ, stream=stream)
-            if nd:
-                kv.launch_paged_attention(q, QKV, pool, l, bufs[2], max_blocks, bufs[3], nd,
-                                          int(lens.max()), out, Q_DIM, NQ, ws, stream=stream)
+            for s0, sn, prefix in segs:
+                tab = bufs[2].ptr + s0 * max_blocks * 4
+                args = (tab, max_blocks, bufs[3].ptr + s0 * 4, sn, int(lens[s0:s0 + sn].max()),
+                        out.ptr + s0 * Q_DIM * 2, Q_DIM, NQ, ws)
+                if prefix:
+                    kv.launch_paged_attention_shared_prefix(q + s0 * QKV * 2, QKV, pool, l, tab,
+                                                            prefix, *args, stream=stream)
+                else:
+                    kv.launch_paged_attention(q + s0 * QKV * 2, QKV, pool, l, *args,
+                                              stream=stream)
             if nch:
                 kv.launch_paged_prefill_attention_batched(q, QKV, pool, l, cb[0], max_blocks,
                                                           cb[1], cb[2], len(tmap), out, Q_DIM,
@@ -471,16 +490,19 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
             b.free()
         if k >= warmup:
             rec.append((nd, sum(c[3] for c in p["prefill"]), nch, (t1 - t0) * 1e6,
-                        e0.elapsed_ms(e1), (t2 - t0) * 1e3, len(p["prefix_hits"]), ncp))
+                        e0.elapsed_ms(e1), (t2 - t0) * 1e3, len(p["prefix_hits"]), ncp,
+                        sum(sn for _, sn, pre in segs if pre)))
     rec = np.array(rec)
-    dec, pf, nch, plan_us, gpu_ms, wall_ms, hits, ncopies = rec.mean(axis=0)
+    dec, pf, nch, plan_us, gpu_ms, wall_ms, hits, ncopies, grouped = rec.mean(axis=0)
     res = {
         "workload": "configs[2] pool (bs 16, permuted free list), 32 sequences with contexts in "
                     "[128, 8192] decoding + one 2048-token prompt arriving per step, prefill chunk "
                     "512, step budget 2048 tokens, 28 layers x (one paged append for all new rows, "
                     "decode attention for the batch, one batched prefill attention for the "
                     "chunks)" + (f"; every prompt shares its first {shared_prefix} tokens, prefix "
-                                 "cache of 4 entries" if shared_prefix else ""),
+                                 "cache of 4 entries" if shared_prefix else "")
+                    + ("; decode batch grouped by share group, each group's prefix attended "
+                       "once (shared-prefix entry)" if group_decode else ""),
         "steps": steps, "decode_seqs_per_step": round(float(dec), 1),
         "prefill_tokens_per_step": round(float(pf), 1), "chunks_per_step": round(float(nch), 1),
         "host_plan_us": round(float(plan_us), 1), "gpu_ms_per_step": round(float(gpu_ms), 3),
@@ -492,6 +514,8 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0):
     if shared_prefix:
         res["prefix_hits_per_step"] = round(float(hits), 2)
         res["cow_copies_per_step"] = round(float(ncopies), 2)
+    if group_decode:
+        res["grouped_decode_seqs_per_step"] = round(float(grouped), 2)
     for b in (pool_buf, d_cos, d_sin, qkv, out):
         b.free()
     sched.close()

@@ -481,6 +481,13 @@ int af_sched_step(af_scheduler* s, int32_t* counts);
  * position; it attends position + 1 rows). Any pointer may be NULL. */
 int af_sched_plan_decode(const af_scheduler* s, int64_t* requests, int32_t* seqs, int64_t* slots,
                          int32_t* positions);
+/* Share groups of the decode batch (no counterpart in the reference): groups[i]
+ * is the prefix-cache group of decode entry i (-1: none) and rows[i] the rows
+ * [0, rows[i]) that every entry of that group holds with identical values (a
+ * cached prefix's creator and every request admitted on it), so a caller may
+ * attend them once per group with af_paged_attention_shared_prefix, using any
+ * member's block table as the prefix table. Either pointer may be NULL. */
+int af_sched_plan_decode_shared(const af_scheduler* s, int64_t* groups, int32_t* rows);
 /* Prefill chunks: requests[i], chunks[5i..5i+4] = (seq, p0, n, offset, last);
  * slots / positions of every chunk token, chunk i at [offset, offset + n). */
 int af_sched_plan_prefill(const af_scheduler* s, int64_t* requests, int32_t* chunks,

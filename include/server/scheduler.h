@@ -29,7 +29,10 @@
 //    partial shared tail block is a copy-on-write) and prefills the rest.
 //    Cached sequences are evicted oldest-first when the cache is full and
 //    before any preemption when the pool runs out; a hit makes an entry the
-//    youngest;
+//    youngest. Each cache entry opens a share group: its creator and every
+//    request admitted on it hold identical rows [0, prefix_len), so a decode
+//    batch can attend them once per group (af_paged_attention_shared_prefix).
+//    A preempted request leaves its group;
 //  * step(): (0) prefixes cached last step become usable; (1) retire finished
 //    entries; (2) decode every fully prefilled
 //    entry (plan_decode, all or nothing); if the pool cannot hold the batch,
@@ -81,6 +84,10 @@ struct StepPlan {
     std::vector<int> decode_seqs;
     std::vector<int64_t> decode_slots;
     std::vector<int32_t> decode_positions;  // the new token's position; attends position + 1 rows
+    // Share group of each decode entry (-1: none) and the rows [0, share_rows) that
+    // every member of the group holds with identical values.
+    std::vector<int64_t> decode_share_groups;
+    std::vector<int32_t> decode_share_rows;
     std::vector<PrefillChunk> prefill;
     std::vector<int64_t> prefill_slots;
     std::vector<int32_t> prefill_positions;
@@ -121,12 +128,15 @@ private:
         int prompt_eff = 0;
         int prefilled = 0;
         int generated = 0;
+        int64_t share_group = -1;  // the cache entry's group this sequence forked from
+        int share_rows = 0;
     };
     struct CachedPrefix {
         int64_t key = -1;
         int seq = -1;
         int len = 0;
         bool ready = false;  // false during the step that cached it
+        int64_t group = -1;  // shared by the creator and every request that forks it
     };
     void preempt_youngest(StepPlan* plan);
     void emit_chunk(StepPlan* plan, Entry& e, int first, int n);
@@ -135,13 +145,14 @@ private:
     }
     int find_prefix(int64_t key, int len, bool ready_only) const;  // index in cache_ or -1
     bool evict_oldest(StepPlan* plan);
-    void maybe_cache(StepPlan* plan, const Entry& e);
+    void maybe_cache(StepPlan* plan, Entry& e);
 
     BlockManager& bm_;
     SchedulerConfig cfg_;
     std::deque<Entry> waiting_;
     std::vector<Entry> running_;       // admission order
     std::vector<CachedPrefix> cache_;  // oldest first
+    int64_t next_group_ = 0;
 };
 
 }  // namespace atomflow::server

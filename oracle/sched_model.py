@@ -45,6 +45,10 @@ first prefix_len prompt tokens equal those of every request with that key.
    entry moves to the youngest end, seq = fork(entry's seq), prefilled = base,
    extend by n (its CoW copy joins the plan), and the request id is listed in
    prefix_hits. Without a hit, n is also capped at prefix_len;
+ * share groups: each new cache entry takes the next group number (from 0),
+   which its creator joins; a request admitted on the entry joins it too, with
+   shared rows = prefix_len; preemption leaves the group (-1, 0). Each decode
+   entry reports (group, rows) in decode_shared;
  * when the decode plan (step 2) or a prefill extend (step 3) finds the pool
    exhausted, the oldest cache entry is evicted (its sequence freed) and the
    same plan is retried; only with an empty cache do the preemption / stall
@@ -55,12 +59,13 @@ from .block_model import POOL_EXHAUSTED
 
 class _Entry:
     __slots__ = ("rid", "prompt_len", "max_new", "seq", "prompt_eff", "prefilled", "generated",
-                 "pkey", "plen")
+                 "pkey", "plen", "group", "srows")
 
     def __init__(self, rid, prompt_len, max_new, pkey=-1, plen=0):
         self.rid, self.prompt_len, self.max_new = rid, prompt_len, max_new
         self.seq, self.prompt_eff, self.prefilled, self.generated = -1, prompt_len, 0, 0
         self.pkey, self.plen = pkey, plen
+        self.group, self.srows = -1, 0
 
 
 class SchedModel:
@@ -71,7 +76,8 @@ class SchedModel:
         self.prefill_chunk, self.watermark = prefill_chunk, watermark
         self.max_cached = max_cached_prefixes
         self.waiting, self.running = [], []
-        self.cache = []  # [key, seq, len, ready], oldest first
+        self.cache = []  # [key, seq, len, ready, group], oldest first
+        self.next_group = 0
 
     def _caching(self, e):
         return self.max_cached > 0 and e.plen > 0
@@ -85,7 +91,8 @@ class SchedModel:
     def _evict_oldest(self, plan):
         if not self.cache:
             return False
-        key, seq, _, _ = self.cache.pop(0)
+        key, seq = self.cache[0][:2]
+        self.cache.pop(0)
         self.bm.seq_free(seq)
         plan["evicted"].append(key)
         return True
@@ -95,12 +102,14 @@ class SchedModel:
             return
         if len(self.cache) >= self.max_cached:
             self._evict_oldest(plan)
-        self.cache.append([e.pkey, self.bm.seq_fork(e.seq), e.plen, False])
+        self.cache.append([e.pkey, self.bm.seq_fork(e.seq), e.plen, False, self.next_group])
+        e.group, e.srows = self.next_group, e.plen
+        self.next_group += 1
         plan["cached"].append(e.pkey)
 
     def clear_prefix_cache(self):
-        for _, seq, _, _ in self.cache:
-            self.bm.seq_free(seq)
+        for c in self.cache:
+            self.bm.seq_free(c[1])
         self.cache = []
 
     def add_request(self, rid, prompt_len, max_new, prefix_key=-1, prefix_len=0):
@@ -117,6 +126,7 @@ class SchedModel:
         v = self.running.pop()
         self.bm.seq_free(v.seq)
         v.seq, v.prompt_eff, v.prefilled = -1, v.prompt_len + v.generated, 0
+        v.group, v.srows = -1, 0
         self.waiting.insert(0, v)
         plan["preempted"].append(v.rid)
 
@@ -130,7 +140,7 @@ class SchedModel:
 
     def step(self):
         plan = {"finished": [], "preempted": [], "decode": [], "copies": [], "prefill": [],
-                "prefix_hits": [], "cached": [], "evicted": []}
+                "prefix_hits": [], "cached": [], "evicted": [], "decode_shared": []}
         for c in self.cache:
             c[3] = True
         keep = []
@@ -153,6 +163,7 @@ class SchedModel:
             slots, positions, copies = r
             for e, sl, p in zip(dec, slots, positions):
                 plan["decode"].append((e.rid, e.seq, sl, p))
+                plan["decode_shared"].append((e.group, e.srows))
                 e.generated += 1
             plan["copies"].extend(copies)
             break
@@ -201,6 +212,7 @@ class SchedModel:
                 self.cache.append(c)
                 e.seq = self.bm.seq_fork(c[1])
                 e.prefilled = base
+                e.group, e.srows = c[4], c[2]
                 plan["prefix_hits"].append(e.rid)
             else:
                 e.seq = self.bm.seq_create()

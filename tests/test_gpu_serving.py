@@ -117,7 +117,10 @@ def test_scheduler_prefix_cache_drives_paged_kernels(gpu):
     """Requests sharing prompt prefixes: the scheduler forks cached prefixes, the
     plan's copy-on-write copies run on the device (af_kv_copy_blocks) before the
     step's appends, and every attention row still matches the oracle over each
-    request's own logical sequence (shared prefix rows + its own rows)."""
+    request's own logical sequence (shared prefix rows + its own rows). Each decode
+    batch is also attended grouped by the plan's share groups, every group through
+    af_paged_attention_shared_prefix with its first member's table as the prefix
+    table, to the same tolerance."""
     say("serving loop with a prefix cache: 40 blocks, 2 prefix keys, cache of 2")
     bs, total_blocks, max_pos = 16, 40, 512
     bm = kv.BlockManager(total_blocks, bs, 1, NKV, HD, atomflow_amd.AF_KV_FP16,
@@ -148,7 +151,7 @@ def test_scheduler_prefix_cache_drives_paged_kernels(gpu):
         prefix_mirror[key] = (k, v)
     mirror = {}
     ws = kv.AttentionWorkspace(6, NQ, NKV, HD, 0)
-    steps = rows = hits = copies = 0
+    steps = rows = hits = copies = grouped = 0
     while True:
         p = sched.step()
         if not p["decode"] and not p["prefill"]:
@@ -171,11 +174,32 @@ def test_scheduler_prefix_cache_drives_paged_kernels(gpu):
             kv.launch_paged_attention(d_qkv, QKV, pool, 0, up(tables), total_blocks, up(lens), nd,
                                       int(lens.max()), d_o, Q_DIM, NQ, ws)
             got = d_o.download(np.float16, (nd, Q_DIM))
+            # the same batch grouped by the plan's share groups: each group's prefix
+            # through the shared-prefix entry (lone members too on odd steps)
+            order, segs = kv.decode_share_segments(a["decode_share_groups"],
+                                                   a["decode_share_rows"], 1 + steps % 2)
+            q_perm = up(d_qkv.download(np.float16, (nd, QKV))[order])
+            t_perm, l_perm = up(tables[order]), up(lens[order])
+            d_g = dev.DeviceBuffer(nd * Q_DIM * 2)
+            for s0, sn, prefix in segs:
+                args = (t_perm.ptr + s0 * total_blocks * 4, total_blocks, l_perm.ptr + s0 * 4, sn,
+                        int(lens[order][s0:s0 + sn].max()), d_g.ptr + s0 * Q_DIM * 2, Q_DIM, NQ,
+                        ws)
+                if prefix:
+                    kv.launch_paged_attention_shared_prefix(q_perm.ptr + s0 * QKV * 2, QKV, pool,
+                                                            0, args[0], prefix, *args)
+                    grouped += sn
+                else:
+                    kv.launch_paged_attention(q_perm.ptr + s0 * QKV * 2, QKV, pool, 0, *args)
+            got_g = np.empty_like(got)
+            got_g[order] = d_g.download(np.float16, (nd, Q_DIM))
             for b, (rid, seq, slot, pos) in enumerate(p["decode"]):
                 k, v = mirror[rid]
                 roped = oracle.rope_append(qkv[b], k, v, c, s_, pos, NQ, NKV, HD)
                 ref = oracle.cached_attention_f64(roped[:Q_DIM], k, v, pos + 1, NQ, NKV, HD)
                 assert_attn_close(got[b], ref, what=f"step {steps} decode rid {rid} pos {pos}")
+                assert_attn_close(got_g[b], ref,
+                                  what=f"step {steps} grouped decode rid {rid} pos {pos}")
                 rows += 1
         for rid, seq, p0, n, last, slots in p["prefill"]:
             if rid in p["prefix_hits"]:
@@ -203,8 +227,9 @@ def test_scheduler_prefix_cache_drives_paged_kernels(gpu):
             rows += n
         steps += 1
         assert steps < 5000
-    say(f"{steps} steps, {rows} attention rows, {hits} prefix hits, {copies} CoW copies")
-    assert hits > 0 and copies > 0
+    say(f"{steps} steps, {rows} attention rows, {hits} prefix hits, {copies} CoW copies, "
+        f"{grouped} decode rows attended through a shared prefix")
+    assert hits > 0 and copies > 0 and grouped > 0
     sched.clear_prefix_cache()
     assert bm.num_free_blocks() == total_blocks
     sched.close()

@@ -11,7 +11,8 @@ from oracle.sched_model import SchedModel
 
 
 def _same(a, b, step):
-    for key in ("finished", "preempted", "decode", "copies", "prefix_hits", "cached", "evicted"):
+    for key in ("finished", "preempted", "decode", "copies", "prefix_hits", "cached", "evicted",
+                "decode_shared"):
         assert [tuple(x) if isinstance(x, (list, tuple)) else x for x in a[key]] == \
                [tuple(x) if isinstance(x, (list, tuple)) else x for x in b[key]], (step, key)
     assert len(a["prefill"]) == len(b["prefill"]), step
@@ -40,6 +41,7 @@ def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, water
             pl = plen + int(r.integers(1, max(2, max_prompt - plen + 1)))
         reqs.append((i, pl, mn, key, plen))
     generated = {q[0]: 0 for q in reqs}
+    max_blocks = -(-max(q[1] + q[2] for q in reqs) // bs) + 1
     finished = []
     pending = list(reqs)
     steps = hits = 0
@@ -52,6 +54,17 @@ def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, water
         a = sched.step()
         b = model.step()
         _same(a, b, steps)
+        # a share group's members map the group's full shared blocks to the same blocks
+        groups = {}
+        for (rid, seq, slot, pos), (g, rows) in zip(a["decode"], a["decode_shared"]):
+            if g >= 0:
+                assert 0 < rows <= pos
+                groups.setdefault(g, []).append((seq, rows))
+        for g, members in groups.items():
+            assert len({rows for _, rows in members}) == 1, g
+            full = members[0][1] // bs
+            tables, _ = bm.export_tables([seq for seq, _ in members], max_blocks)
+            assert (tables[:, :full] == tables[0, :full]).all(), g
         # invariants
         toks = len(a["decode"]) + sum(c[3] for c in a["prefill"])
         assert toks <= max_step_tokens
@@ -126,6 +139,9 @@ def test_scheduler_prefix_hit_skips_the_prefix():
     # both append into block 2 of the prefix (rows 32..39 filled, shared by the
     # cache entry, request 0 and request 1): each gets its own copy of 8 rows
     assert sorted(c[2] for c in p["copies"]) == [8, 8]
+    p = s.step()  # both prompts are complete: they decode in share group 0 (40 rows)
+    assert [d[0] for d in p["decode"]] == [0, 1]
+    assert p["decode_shared"] == [(0, 40), (0, 40)]
     assert not s.add_request(2, 40, 2, prefix_key=7, prefix_len=40)  # prefix must be shorter
     assert not s.add_request(3, 50, 2, prefix_key=-1, prefix_len=10)
     while p["running"] or p["waiting"]:
@@ -190,3 +206,23 @@ def test_prefill_tile_map_orders_heaviest_first():
     w = [work[tuple(x)] for x in m]
     assert w == sorted(w, reverse=True)
     assert kv.prefill_tile_map([]).shape == (0, 2)
+
+
+def test_decode_share_segments():
+    """Decode rows ordered for one attention launch per segment: entries with no
+    group or a lone member first (plain attention), then each group together."""
+    groups = [-1, 3, 5, 3, -1, 7, 3, 5]
+    rows = [0, 40, 100, 40, 0, 9, 40, 100]
+    order, segs = kv.decode_share_segments(groups, rows)
+    assert list(order) == [0, 4, 5, 1, 3, 6, 2, 7]
+    assert segs == [(0, 3, 0), (3, 3, 40), (6, 2, 100)]
+    order, segs = kv.decode_share_segments(groups, rows, min_members=3)
+    assert list(order) == [0, 2, 4, 5, 7, 1, 3, 6] and segs == [(0, 5, 0), (5, 3, 40)]
+    order, segs = kv.decode_share_segments([2, 2], [16, 16])
+    assert list(order) == [0, 1] and segs == [(0, 2, 16)]
+    assert kv.decode_share_segments([], [])[1] == []
+    # only groups that save enough row reads: group 3 saves 2 x 40, group 5 1 x 100
+    order, segs = kv.decode_share_segments(groups, rows, min_saved_rows=81)
+    assert list(order) == [0, 1, 3, 4, 5, 6, 2, 7] and segs == [(0, 6, 0), (6, 2, 100)]
+    with pytest.raises(ValueError):
+        kv.decode_share_segments([1, 1], [16, 17])
