@@ -264,6 +264,8 @@ def bench_contiguous(args, dev, kv, lib, info):
         log("the same, decode attention grouped by the plan's share groups ...")
         result["serving_shared_prefix_grouped"] = bench_serving(dev, kv, lib, shared_prefix=1544,
                                                                 group_decode=True)
+        log("fan-out: 64 forks of one cached 4096-token prompt, plain vs grouped decode ...")
+        result["serving_fanout"] = bench_fanout(dev, kv, lib)
     log("projection GEMVs ...")
     result["gemv"] = bench_gemv(dev, kv, lib, args.steps, args.warmup)
     if not args.no_weights:
@@ -521,6 +523,98 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
     sched.close()
     bm.close()
     return res
+
+
+def bench_fanout(dev, kv, lib, steps=8, n_req=64, prefix=4096, suffix=16):
+    """Decode of n_req requests that share one cached prompt prefix (the prefix cache
+    forks it; the fan-out of n samples or of one system prompt, paged_kv_manager.h:61).
+    Once all are decoding, steps alternate between the batch's plain decode
+    attention and the same batch grouped by the plan's share groups
+    (kv.decode_share_segments, the group through af_paged_attention_shared_prefix);
+    each step runs 28 layers of one paged append plus the attention. GPU time per
+    step of each form, same running set."""
+    import atomflow_amd
+    bs, max_blocks = 16, 512
+    prompt = prefix + suffix
+    total_blocks = n_req * (-(-(prompt + 64) // bs)) + 64
+    bm = kv.BlockManager(total_blocks, bs, LAYERS, NKV, HD, atomflow_amd.AF_KV_FP16)
+    stream = dev.Stream()
+    nbytes = kv.pool_bytes(bm.pool())
+    pool_buf = dev.DeviceBuffer(nbytes)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(pool_buf.ptr, nbytes // 2, 9, 1.0, stream.handle))
+    bm.attach_pool(pool_buf.ptr)
+    pool = bm.pool()
+    sched = kv.Scheduler(bm, n_req, 8192, 4096, 0, 1)
+    assert sched.add_request(0, prompt, 64, 3, prefix)
+    while sched.step()["cache_entries"] == 0:
+        pass
+    for i in range(1, n_req):
+        assert sched.add_request(i, prompt, 64, 3, prefix)
+    p = sched.step()
+    while len(p["decode"]) < n_req:  # host-only steps: the forks prefill their suffixes
+        p = sched.step()
+    max_pos = prompt + 64
+    d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+    kv.build_rope_cache(d_cos, d_sin, max_pos, HD, THETA, stream)
+    qkv = dev.DeviceBuffer(LAYERS * n_req * QKV * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, qkv.nbytes // 2, 13, 1.0, stream.handle))
+    out = dev.DeviceBuffer(n_req * Q_DIM * 2)
+    ws = kv.AttentionWorkspace(n_req, NQ, NKV, HD, 0, stream)
+    dev.synchronize()
+    e0, e1 = dev.Event(), dev.Event()
+    times = {False: [], True: []}
+    for k in range(2 * steps + 2):
+        grouped = bool(k % 2)
+        a = p["arrays"]
+        nd = len(p["decode"])
+        segs = [(0, nd, 0)]
+        if grouped:
+            order, segs = kv.decode_share_segments(a["decode_share_groups"],
+                                                   a["decode_share_rows"])
+            for key in ("decode_seqs", "decode_slots", "decode_positions"):
+                a[key] = a[key][order]
+        tables, lens = bm.export_tables(a["decode_seqs"], max_blocks)
+        bufs = [dev.DeviceBuffer.from_array(x) for x in
+                (a["decode_slots"], a["decode_positions"], tables, lens)]
+        e0.record(stream)
+        for l in range(LAYERS):
+            q = qkv.ptr + l * n_req * QKV * 2
+            kv.launch_paged_rope_append(q, nd, pool, l, bufs[0], bufs[1], d_cos, d_sin, max_pos,
+                                        NQ, stream=stream)
+            for s0, sn, pre in segs:
+                tab = bufs[2].ptr + s0 * max_blocks * 4
+                args = (tab, max_blocks, bufs[3].ptr + s0 * 4, sn, int(lens[s0:s0 + sn].max()),
+                        out.ptr + s0 * Q_DIM * 2, Q_DIM, NQ, ws)
+                if pre:
+                    kv.launch_paged_attention_shared_prefix(q + s0 * QKV * 2, QKV, pool, l, tab,
+                                                            pre, *args, stream=stream)
+                else:
+                    kv.launch_paged_attention(q + s0 * QKV * 2, QKV, pool, l, *args,
+                                              stream=stream)
+        e1.record(stream)
+        e1.sync()
+        if k >= 2:
+            times[grouped].append(e0.elapsed_ms(e1))
+        for b in bufs:
+            b.free()
+        p = sched.step()
+        assert len(p["decode"]) == n_req
+    plain, grp = float(np.mean(times[False])), float(np.mean(times[True]))
+    for b in (pool_buf, d_cos, d_sin, qkv, out):
+        b.free()
+    sched.close()
+    bm.close()
+    return {
+        "workload": f"{n_req} requests forking one cached {prefix}-token prompt prefix "
+                    f"({suffix} own prompt tokens each), decoding; fp16 pool bs 16; a step = "
+                    "28 layers x (paged append of the batch's new rows + decode attention), "
+                    "plain and grouped steps alternating over the same running set",
+        "steps_each": steps, "plain_ms_per_step": round(plain, 3),
+        "grouped_ms_per_step": round(grp, 3), "speedup": round(plain / grp, 3),
+        "decode_tokens_per_s_plain": round(n_req / (plain * 1e-3), 0),
+        "decode_tokens_per_s_grouped": round(n_req / (grp * 1e-3), 0),
+    }
 
 
 def bench_gemv(dev, kv, lib, steps, warmup):
