@@ -67,6 +67,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--no-serving", action="store_true", help="skip the continuous-batching step")
     ap.add_argument("--no-weights", action="store_true", help="skip the .bin load measurement")
+    ap.add_argument("--fanout-only", action="store_true",
+                    help="run only the fan-out decode measurement and print its JSON object")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
     return ap.parse_args()
@@ -1007,6 +1009,9 @@ def main():
     dev.set_device(0)
     info = dev.device_info()
     log(f"device {info}")
+    if args.fanout_only:
+        print(json.dumps({"serving_fanout": bench_fanout(dev, kv, lib)}), flush=True)
+        return
     if args.config == 2:
         result = bench_contiguous(args, dev, kv, lib, info)
         if not args.no_cpu:
