@@ -527,7 +527,7 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
     return res
 
 
-def bench_fanout(dev, kv, lib, steps=8, n_req=64, prefix=4096, suffix=16):
+def bench_fanout(dev, kv, lib, steps=8, n_req=64, prefix=4096, suffix=16, prefix_splits=0):
     """Decode of n_req requests that share one cached prompt prefix (the prefix cache
     forks it; the fan-out of n samples or of one system prompt, paged_kv_manager.h:61).
     Once all are decoding, steps alternate between the batch's plain decode
@@ -590,7 +590,8 @@ def bench_fanout(dev, kv, lib, steps=8, n_req=64, prefix=4096, suffix=16):
                         out.ptr + s0 * Q_DIM * 2, Q_DIM, NQ, ws)
                 if pre:
                     kv.launch_paged_attention_shared_prefix(q + s0 * QKV * 2, QKV, pool, l, tab,
-                                                            pre, *args, stream=stream)
+                                                            pre, *args, stream=stream,
+                                                            prefix_splits=prefix_splits)
                 else:
                     kv.launch_paged_attention(q + s0 * QKV * 2, QKV, pool, l, *args,
                                               stream=stream)
