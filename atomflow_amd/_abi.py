@@ -97,6 +97,8 @@ PROTOTYPES = {
     "af_bm_free_block": (I, [P, I]),
     "af_bm_num_free_blocks": (I, [P]),
     "af_bm_ref_count": (I, [P, I]),
+    "af_bm_hold_copy_source": (I, [P, I]),
+    "af_bm_release_copy_sources": (I, [P]),
     "af_bm_seq_create": (I, [P]),
     "af_bm_seq_fork": (I, [P, I]),
     "af_bm_seq_free": (I, [P, I]),

@@ -35,6 +35,8 @@ void BlockManager::initialize(const PoolConfig& cfg, bool allocate_pool, void* p
     owns_pool_ = false;
     cfg_ = cfg;
     ref_.assign(size_t(cfg.total_blocks), 0);
+    held_.assign(size_t(cfg.total_blocks), 0);
+    holds_.clear();
     free_list_.resize(size_t(cfg.total_blocks));
     for (int i = 0; i < cfg.total_blocks; ++i) free_list_[size_t(i)] = cfg.total_blocks - 1 - i;
     tables_.clear();
@@ -74,8 +76,23 @@ int BlockManager::allocate_block() { return pop_free(); }
 int BlockManager::try_free_block(int block_id) {
     if (block_id < 0 || block_id >= cfg_.total_blocks || ref_[size_t(block_id)] == 0)
         return AF_ERR_BAD_BLOCK;
-    if (--ref_[size_t(block_id)] == 0) free_list_.push_back(block_id);
+    if (--ref_[size_t(block_id)] == 0 && held_[size_t(block_id)] == 0)
+        free_list_.push_back(block_id);
     return AF_OK;
+}
+
+int BlockManager::hold_copy_source(int block_id) {
+    if (block_id < 0 || block_id >= cfg_.total_blocks || ref_[size_t(block_id)] == 0)
+        return AF_ERR_BAD_BLOCK;
+    ++held_[size_t(block_id)];
+    holds_.push_back(block_id);
+    return AF_OK;
+}
+
+void BlockManager::release_copy_sources() {
+    for (int b : holds_)
+        if (--held_[size_t(b)] == 0 && ref_[size_t(b)] == 0) free_list_.push_back(b);
+    holds_.clear();
 }
 
 void BlockManager::free_block(int block_id) {
@@ -342,6 +359,14 @@ extern "C" int af_bm_num_free_blocks(const af_block_manager* bm) {
 }
 extern "C" int af_bm_ref_count(const af_block_manager* bm, int block_id) {
     return bm ? bm->bm.ref_count(block_id) : AF_ERR_INVALID_ARG;
+}
+extern "C" int af_bm_hold_copy_source(af_block_manager* bm, int block_id) {
+    return bm ? bm->bm.hold_copy_source(block_id) : AF_ERR_INVALID_ARG;
+}
+extern "C" int af_bm_release_copy_sources(af_block_manager* bm) {
+    if (!bm) return AF_ERR_INVALID_ARG;
+    bm->bm.release_copy_sources();
+    return AF_OK;
 }
 extern "C" int af_bm_seq_create(af_block_manager* bm) {
     return bm ? bm->bm.create_sequence() : AF_ERR_INVALID_ARG;

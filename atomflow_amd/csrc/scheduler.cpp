@@ -118,8 +118,23 @@ void Scheduler::emit_chunk(StepPlan* plan, Entry& e, int first, int n) {
     if (c.last) ++e.generated;
 }
 
+// A planned copy's source keeps its rows until the caller has issued the step's
+// copies: evictions and preemptions later in the same plan may drop its last
+// reference, and the LIFO free list would otherwise hand it out again at once,
+// e.g. as the destination of another copy in the same batch of copies.
+void Scheduler::add_copy(StepPlan* plan, const CowCopy& c) {
+    (void)bm_.hold_copy_source(c.src);
+    plan->copies.push_back(c);
+}
+
 int Scheduler::step(StepPlan* plan) {
     if (!plan) return AF_ERR_INVALID_ARG;
+    const int st = plan_step(plan);
+    bm_.release_copy_sources();
+    return st;
+}
+
+int Scheduler::plan_step(StepPlan* plan) {
     plan->clear();
     // 0. prefixes cached last step are complete in the pool now
     for (CachedPrefix& c : cache_) c.ready = true;
@@ -160,7 +175,7 @@ int Scheduler::step(StepPlan* plan) {
             plan->decode_positions.push_back(slots[j].position);
             plan->decode_share_groups.push_back(e.share_group);
             plan->decode_share_rows.push_back(e.share_rows);
-            if (slots[j].cow.src >= 0) plan->copies.push_back(slots[j].cow);
+            if (slots[j].cow.src >= 0) add_copy(plan, slots[j].cow);
             ++e.generated;
         }
         break;
@@ -192,7 +207,7 @@ int Scheduler::step(StepPlan* plan) {
             break;
         }
         if (st) return st;
-        if (cow.src >= 0) plan->copies.push_back(cow);
+        if (cow.src >= 0) add_copy(plan, cow);
         emit_chunk(plan, e, first, n);
         maybe_cache(plan, e);
         budget -= n;
@@ -231,7 +246,7 @@ int Scheduler::step(StepPlan* plan) {
         int first = 0;
         const int st = bm_.extend(e.seq, n, &first, &cow);
         if (st) return st;  // cannot happen: the blocks were counted above
-        if (cow.src >= 0) plan->copies.push_back(cow);
+        if (cow.src >= 0) add_copy(plan, cow);
         running_.push_back(e);
         emit_chunk(plan, running_.back(), first, n);
         maybe_cache(plan, running_.back());

@@ -334,6 +334,12 @@ class BlockManager:
     def ref_count(self, block_id):
         return lib().af_bm_ref_count(self.h, block_id)
 
+    def hold_copy_source(self, block_id):
+        return lib().af_bm_hold_copy_source(self.h, block_id)
+
+    def release_copy_sources(self):
+        return check(lib().af_bm_release_copy_sources(self.h), "release_copy_sources")
+
     def attach_pool(self, base, scales=None):
         check(lib().af_bm_attach_pool(self.h, _p(base), _p(scales)), "attach_pool")
 

@@ -435,6 +435,19 @@ int64_t af_bm_seq_slot(const af_block_manager* bm, int seq, int pos);
  * On failure no sequence is changed. */
 int af_bm_plan_decode(af_block_manager* bm, const int32_t* seqs, int n, int64_t* slots,
                       int32_t* positions, int32_t* copies, int max_copies, int32_t* n_copies);
+/* Copy-source holds, for a caller that plans several operations before it issues
+ * their copies. A planned copy's source must keep its rows until the copy runs,
+ * but a later free in the same plan (af_bm_seq_free, af_bm_free_block) may drop
+ * its last reference, and the LIFO free list would hand it out again at once,
+ * possibly as another copy's destination. af_bm_hold_copy_source(src) keeps a
+ * referenced block off the free list when its references reach zero (a hold is
+ * not a reference: the copy-on-write test ignores it); af_bm_release_copy_sources
+ * drops every hold in the order taken and frees the unreferenced ones. The
+ * scheduler (af_sched_step) holds its plan's sources and releases them before
+ * returning. No reference counterpart (the reference declares no copy-on-write
+ * bookkeeping: paged_kv_manager.h:51,61). hold: AF_OK or AF_ERR_BAD_BLOCK. */
+int af_bm_hold_copy_source(af_block_manager* bm, int block_id);
+int af_bm_release_copy_sources(af_block_manager* bm);
 /* Block tables [n][max_blocks] (unused entries = 0) and lengths for n sequences. */
 int af_bm_export_tables(const af_block_manager* bm, const int32_t* seqs, int n, int32_t* tables,
                         int max_blocks, int32_t* seq_lens);

@@ -19,7 +19,12 @@
 //  * free_block drops one reference, the id returns to the stack at zero;
 //  * append: full or missing tail -> new block; partial tail with ref > 1 ->
 //    copy-on-write (new block, copy `fill` rows, old tail loses a reference);
-//    otherwise write in place; a failed append / extend / plan changes nothing.
+//    otherwise write in place; a failed append / extend / plan changes nothing;
+//  * a copy source can be held (hold_copy_source) until the copies that read it
+//    have been issued: a held block whose last reference is freed stays off the
+//    free list until release_copy_sources(), so no later allocation in the same
+//    plan hands it out as a destination while a planned copy still reads it.
+//    Holds do not count as references (the copy-on-write test is unchanged).
 #include <cstdint>
 #include <stdexcept>
 #include <vector>
@@ -104,6 +109,13 @@ public:
     int seq_len(int seq) const;             // tokens, or AF_ERR_BAD_SEQUENCE
     int64_t slot_of(int seq, int pos) const;
 
+    // Copy-source holds (see the rules above). hold: AF_ERR_BAD_BLOCK unless the
+    // block is referenced. release: holds drop in the order they were taken; a
+    // block with no references left returns to the free list then.
+    int hold_copy_source(int block_id);
+    void release_copy_sources();
+    int num_held_blocks() const { return int(holds_.size()); }
+
     int append_token(int seq, AppendSlot* out);
     int extend(int seq, int n_tokens, int* first_pos, CowCopy* cow);
     int plan_decode(const int* seqs, int n, AppendSlot* out);
@@ -121,6 +133,8 @@ private:
     PoolConfig cfg_;
     std::vector<int> ref_;
     std::vector<int> free_list_;  // stack: back() is handed out next
+    std::vector<int> held_;       // per block: outstanding copy-source holds
+    std::vector<int> holds_;      // held block ids, in the order taken
     std::vector<PageTable> tables_;
     std::vector<uint8_t> live_;
     void* pool_ = nullptr;

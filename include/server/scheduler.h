@@ -114,7 +114,10 @@ public:
     // Resizes the prefix cache (0 turns it off), evicting oldest entries first.
     void set_max_cached_prefixes(int n);
     int num_cached_prefixes() const { return int(cache_.size()); }
-    // Plans one step into *plan (cleared first). AF_OK or an AF_* error.
+    // Plans one step into *plan (cleared first). AF_OK or an AF_* error. Within
+    // one plan, copy sources and destinations are disjoint and every destination
+    // is unique: a copy's source block is held (BlockManager::hold_copy_source)
+    // until the plan is final, so no later allocation in the plan reuses it.
     int step(StepPlan* plan);
     int num_waiting() const { return int(waiting_.size()); }
     int num_running() const { return int(running_.size()); }
@@ -138,6 +141,8 @@ private:
         bool ready = false;  // false during the step that cached it
         int64_t group = -1;  // shared by the creator and every request that forks it
     };
+    int plan_step(StepPlan* plan);
+    void add_copy(StepPlan* plan, const CowCopy& c);
     void preempt_youngest(StepPlan* plan);
     void emit_chunk(StepPlan* plan, Entry& e, int first, int n);
     bool caching(const Entry& e) const {

@@ -18,7 +18,11 @@ must reproduce op for op:
 * append: full (or missing) tail -> new block; partial tail shared by another
   table (ref > 1) -> copy-on-write: new block, copy ``fill`` rows, old tail
   loses one reference; otherwise write in place;
-* a failed append / extend / batched plan changes nothing.
+* a failed append / extend / batched plan changes nothing;
+* a copy source can be held until the copies that read it are issued: a held
+  block whose last reference is freed stays off the free list until
+  ``release_copy_sources`` (holds drop in the order taken); holds are not
+  references, so the copy-on-write test is unchanged.
 """
 
 POOL_EXHAUSTED = -1
@@ -35,6 +39,8 @@ class BlockModel:
         self.free = list(range(total_blocks - 1, -1, -1))  # top of stack = end
         self.seqs = {}  # id -> [block_ids, fill]
         self.next_seq = 0
+        self.held = [0] * total_blocks
+        self.holds = []
 
     # ---- reference contract ---------------------------------------------
     def allocate_block(self):
@@ -48,9 +54,23 @@ class BlockModel:
         if b < 0 or b >= self.total or self.ref[b] == 0:
             return BAD_BLOCK
         self.ref[b] -= 1
-        if self.ref[b] == 0:
+        if self.ref[b] == 0 and self.held[b] == 0:
             self.free.append(b)
         return 0
+
+    def hold_copy_source(self, b):
+        if b < 0 or b >= self.total or self.ref[b] == 0:
+            return BAD_BLOCK
+        self.held[b] += 1
+        self.holds.append(b)
+        return 0
+
+    def release_copy_sources(self):
+        for b in self.holds:
+            self.held[b] -= 1
+            if self.held[b] == 0 and self.ref[b] == 0:
+                self.free.append(b)
+        self.holds = []
 
     def num_free_blocks(self):
         return len(self.free)

@@ -53,6 +53,12 @@ first prefix_len prompt tokens equal those of every request with that key.
    exhausted, the oldest cache entry is evicted (its sequence freed) and the
    same plan is retried; only with an empty cache do the preemption / stall
    rules apply.
+
+Copies: every copy-on-write copy that joins the plan holds its source block
+(BlockModel.hold_copy_source) until step() returns, so an eviction or
+preemption later in the same step cannot put the source back on the free list
+while the plan's copies still read it; within one plan, copy sources and
+destinations are disjoint and destinations unique.
 """
 from .block_model import POOL_EXHAUSTED
 
@@ -138,7 +144,16 @@ class SchedModel:
         if last:
             e.generated += 1
 
+    def _add_copy(self, plan, cow):
+        self.bm.hold_copy_source(cow[0])
+        plan["copies"].append(cow)
+
     def step(self):
+        plan = self._plan_step()
+        self.bm.release_copy_sources()
+        return plan
+
+    def _plan_step(self):
         plan = {"finished": [], "preempted": [], "decode": [], "copies": [], "prefill": [],
                 "prefix_hits": [], "cached": [], "evicted": [], "decode_shared": []}
         for c in self.cache:
@@ -165,7 +180,8 @@ class SchedModel:
                 plan["decode"].append((e.rid, e.seq, sl, p))
                 plan["decode_shared"].append((e.group, e.srows))
                 e.generated += 1
-            plan["copies"].extend(copies)
+            for cow in copies:
+                self._add_copy(plan, cow)
             break
         budget = self.max_step_tokens - len(plan["decode"])
         stalled = False
@@ -189,7 +205,7 @@ class SchedModel:
                 break
             first, cow = r
             if cow[0] >= 0:
-                plan["copies"].append(cow)
+                self._add_copy(plan, cow)
             self._chunk(plan, e, first, n)
             self._maybe_cache(plan, e)
             budget -= n
@@ -220,7 +236,7 @@ class SchedModel:
             assert r != POOL_EXHAUSTED
             first, cow = r
             if cow[0] >= 0:
-                plan["copies"].append(cow)
+                self._add_copy(plan, cow)
             self.running.append(e)
             self._chunk(plan, e, first, n)
             self._maybe_cache(plan, e)

@@ -31,12 +31,15 @@ def _invariants(model):
     for ids, _ in model.seqs.values():
         for b in ids:
             held[b] = held.get(b, 0) + 1
-    assert len(model.free) + len([b for b in range(model.total) if model.ref[b] > 0]) == model.total
+    off_list = [b for b in range(model.total) if model.ref[b] == 0 and model.held[b] > 0]
+    live_ids = [b for b in range(model.total) if model.ref[b] > 0]
+    assert len(model.free) + len(live_ids) + len(off_list) == model.total
     assert len(set(model.free)) == len(model.free)
     for b in range(model.total):
         assert model.ref[b] >= held.get(b, 0)
         if model.ref[b] == 0:
-            assert b in model.free
+            # an unreferenced block is free, unless a copy-source hold keeps it out
+            assert (b in model.free) == (model.held[b] == 0), b
 
 
 def test_reference_contract_allocate_free_exhaust():
@@ -100,7 +103,7 @@ def test_random_traces_match_model(seed):
     bm = kv.BlockManager(total, bs)
     model = BlockModel(total, bs)
     for step in range(400):
-        op = rng.integers(0, 9)
+        op = rng.integers(0, 11)
         live = sorted(model.seqs)
         if op == 0 or not live:
             assert bm.seq_create() == model.seq_create()
@@ -128,6 +131,12 @@ def test_random_traces_match_model(seed):
                 slots, pos, copies = got
                 assert list(slots) == exp[0] and list(pos) == exp[1]
                 assert [tuple(c) for c in copies] == exp[2]
+        elif op == 9:
+            b = int(rng.integers(-1, total + 1))
+            assert bm.hold_copy_source(b) == model.hold_copy_source(b)
+        elif op == 10:
+            bm.release_copy_sources()
+            model.release_copy_sources()
         elif op == 7:
             b = bm.allocate_block()
             assert b == model.allocate_block()
@@ -151,6 +160,28 @@ def test_random_traces_match_model(seed):
         for s in live:
             for pos in range(0, model.seq_len(s), 7):
                 assert bm.seq_slot(s, pos) == model.seq_slot(s, pos)
+
+
+def test_copy_source_hold_keeps_block_off_the_free_list():
+    """A copy source whose last reference is freed before the copy runs stays
+    unallocatable until the holds are released; then it returns to the stack."""
+    bm = kv.BlockManager(8, 16)
+    model = BlockModel(8, 16)
+    for m in (bm, model):
+        s = m.seq_create()
+        m.seq_extend(s, 20)  # blocks 0, 1 (tail fill 4)
+        f = m.seq_fork(s)
+        pos, slot, cow = m.seq_append(f)  # CoW 1 -> 2
+        assert cow == (1, 2, 4)
+        assert m.hold_copy_source(1) == 0
+        assert m.hold_copy_source(5) == BAD_BLOCK  # not referenced
+        m.seq_free(s)  # block 1 loses its last reference while held
+        assert m.ref_count(1) == 0
+        assert m.allocate_block() == 3  # not 1: held blocks are off the stack
+        assert m.free_block(1) == BAD_BLOCK if m is model else m.try_free_block(1) == BAD_BLOCK
+        m.release_copy_sources()
+        assert m.allocate_block() == 1  # released on top of the stack
+    _state(bm, model)
 
 
 def test_cow_storm_64_forks():

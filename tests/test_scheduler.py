@@ -66,6 +66,20 @@ def run_trace(seed, total_blocks, bs, max_running, max_step_tokens, chunk, water
             tables, _ = bm.export_tables([seq for seq, _ in members], max_blocks)
             assert (tables[:, :full] == tables[0, :full]).all(), g
         # invariants
+        # copies run together in one launch before the step's appends: a block is
+        # never both a source and a destination, and destinations are unique
+        srcs = [c[0] for c in a["copies"]]
+        dsts = [c[1] for c in a["copies"]]
+        assert not set(srcs) & set(dsts), (steps, a["copies"])
+        assert len(set(dsts)) == len(dsts), (steps, a["copies"])
+        # ... no row written this step is a row a copy reads
+        written = {int(sl) for _, _, sl, _ in a["decode"]}
+        for c in a["prefill"]:
+            written |= {int(sl) for sl in c[5]}
+        read = {src * bs + j for src, _, rows in a["copies"] for j in range(rows)}
+        assert not written & read, (steps, a["copies"])
+        # ... and the holds are gone once the plan is returned
+        assert model.bm.holds == [] and bm.num_free_blocks() == model.bm.num_free_blocks()
         toks = len(a["decode"]) + sum(c[3] for c in a["prefill"])
         assert toks <= max_step_tokens
         assert a["running"] <= max_running
@@ -121,6 +135,21 @@ def test_scheduler_prefix_cache_tight_pool(seed):
     run_trace(300 + seed, total_blocks=40, bs=16, max_running=8, max_step_tokens=64, chunk=32,
               watermark=0, n_req=30, max_prompt=200, max_new=60, arrivals_per_step=4,
               n_prefixes=2, max_cached=4)
+
+
+# Seeds whose traces, without the hold, plan a block as both a copy source and a
+# later copy's destination in one step (found by running the model with the hold
+# disabled); the remaining seeds are ordinary traces of the same shape.
+@pytest.mark.parametrize("seed", [7003, 7064, 7088, 7127, 7184, 7185, 7222, 7247, 7000, 7001])
+def test_scheduler_copy_sources_survive_eviction(seed):
+    """Tight pool, small blocks, partial shared prefix tails and a two-entry cache:
+    evictions inside a step drop the last reference of blocks that earlier copies
+    of the same plan still read. Without the copy-source hold the LIFO free list
+    handed such a block out as a later copy's destination (e.g. copies
+    (27, 17, 4) and (49, 27, 6) in one step)."""
+    run_trace(seed, total_blocks=61, bs=8, max_running=7, max_step_tokens=97, chunk=24,
+              watermark=2, n_req=30, max_prompt=120, max_new=40, arrivals_per_step=4,
+              n_prefixes=2, max_cached=2)
 
 
 def test_scheduler_prefix_hit_skips_the_prefix():
