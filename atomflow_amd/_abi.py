@@ -41,6 +41,8 @@ PROTOTYPES = {
     "af_write_kv_cache": (I, [P, P, P, I, I, I, I, P]),
     "af_rope_append": (I, [P, P, P, P, P, I, P, I, I, I, I, P, P]),
     "af_cached_attention": (I, [P, P, P, P, I, I, I, I, P]),
+    "af_cached_attention_noalloc": (I, [P, P, P, P, I, I, I, I, P]),
+    "af_cached_attention_noalloc_max_bytes": (SZ, []),
     "af_attention_reserve": (I, [I, I, I, I]),
     "af_attention_workspace_size": (SZ, [I, I, I, I, I]),
     "af_attention_workspace_init": (I, [P, SZ, P]),

@@ -992,6 +992,54 @@ extern "C" int af_cached_attention(const void* q, const void* k_cache, const voi
                                   bytes, stream);
 }
 
+// ---- allocation-free form of af_cached_attention ---------------------------
+// The split-K workspace of af_cached_attention_noalloc lives in this
+// file-scope device array (kScratchBytes per device, held until the process
+// ends). Host code never passes the array's name to a kernel: the device
+// address comes from hipGetSymbolAddress, once per device, and is kept per
+// device in g_scratch_ptr.
+constexpr size_t kScratchBytes = size_t(4) * 1024 * 1024 + size_t(128) * 1024;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_ptr;
+
+// Device address of this device's scratch. The first call on a device looks
+// the address up and clears the arrival counters with the fill kernel (stream-
+// ordered before the attention launch that follows; every launch leaves its
+// counters at zero again). No allocation.
+static int scratch_for_device(hipStream_t stream, void** out) {
+    int dev = 0;
+    AF_TRY_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (int(g_scratch_ptr.size()) <= dev) g_scratch_ptr.resize(size_t(dev) + 1, nullptr);
+    if (!g_scratch_ptr[size_t(dev)]) {
+        void* p = nullptr;
+        AF_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return AF_ERR_WORKSPACE;
+        if (int st = fill_u32(p, 0u, kCounterBytes / 4, stream)) return st;
+        g_scratch_ptr[size_t(dev)] = p;
+    }
+    *out = g_scratch_ptr[size_t(dev)];
+    return AF_OK;
+}
+
+extern "C" size_t af_cached_attention_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int af_cached_attention_noalloc(const void* q, const void* k_cache,
+                                           const void* v_cache, void* out, int seq_len,
+                                           int head_dim, int n_q_heads, int n_kv_heads,
+                                           af_stream_t stream) {
+    if (seq_len <= 0) return AF_ERR_INVALID_ARG;
+    if (int st = check_heads(head_dim, n_q_heads, n_kv_heads)) return st;
+    const int splits = default_splits(seq_len, 1, n_kv_heads);
+    const size_t need = attn_workspace_bytes(1, n_q_heads, head_dim, splits);
+    if (need > kScratchBytes) return AF_ERR_WORKSPACE;  // shape beyond the static scratch
+    void* ws = nullptr;
+    if (int st = scratch_for_device(static_cast<hipStream_t>(stream), &ws)) return st;
+    return af_cached_attention_ex(q, k_cache, v_cache, out, seq_len, nullptr, seq_len, head_dim,
+                                  n_q_heads, n_kv_heads, splits, ws, kScratchBytes, stream);
+}
+
 // Rows [0, len) shared by every sequence of a launch, mapped by `table`.
 struct SharedPrefix {
     const int32_t* table = nullptr;

@@ -110,6 +110,23 @@ int af_cached_attention(const void* q, const void* k_cache, const void* v_cache,
                         int seq_len, int head_dim, int n_q_heads, int n_kv_heads,
                         af_stream_t stream);
 
+/* Allocation-free form of af_cached_attention (same arguments, same split
+ * count, same results). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under hipGraph stream capture, serving
+ * loops and harnesses that forbid hipMalloc). The split-K workspace is a static
+ * device array of af_cached_attention_noalloc_max_bytes() bytes per device
+ * (4.125 MiB), held until the process ends; its address is looked up with
+ * hipGetSymbolAddress on the first call on a device, which also clears its
+ * arrival counters with a fill kernel on `stream`. No hipMalloc / hipFree.
+ * Shapes whose workspace exceeds the array (attn workspace of batch 1,
+ * n_q_heads, head_dim, default splits for seq_len) return AF_ERR_WORKSPACE.
+ * Every call on one device shares that array: calls that may overlap on one
+ * device (different streams, no ordering) race and must not be issued. */
+int af_cached_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                void* out, int seq_len, int head_dim, int n_q_heads,
+                                int n_kv_heads, af_stream_t stream);
+size_t af_cached_attention_noalloc_max_bytes(void);
+
 /* Pre-allocates the library-owned workspace for batch x n_q_heads heads. */
 int af_attention_reserve(int batch, int n_q_heads, int n_kv_heads, int head_dim);
 
