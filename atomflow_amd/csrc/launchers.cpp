@@ -244,8 +244,9 @@ ArenaAllocator::ArenaAllocator(size_t total_size) {
         throw std::runtime_error("ArenaAllocator: failed to allocate " +
                                  std::to_string(capacity_ >> 20) + " MB");
     }
+    owns_ = true;
 }
 
 ArenaAllocator::~ArenaAllocator() {
-    if (base_ptr_) (void)hipFree(base_ptr_);
+    if (owns_ && base_ptr_) (void)hipFree(base_ptr_);
 }

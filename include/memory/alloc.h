@@ -5,12 +5,21 @@
 // reset_workspace() rewinds). Where the reference calls std::exit on a failed
 // cudaMalloc (alloc.h:59), the constructor here throws, so a host process can
 // report the failure. Sized for a 288 GB HBM3E device: offsets are size_t.
+// A second constructor borrows caller-owned memory (a slice of a larger
+// allocation, or host memory): it allocates and frees nothing.
 #include <cstddef>
 #include <stdexcept>
 
 class ArenaAllocator {
 public:
+    // One hipMalloc of total_size rounded up to 128 B; throws std::runtime_error
+    // when the allocation fails.
     explicit ArenaAllocator(size_t total_size);
+    // Borrows [base, base + capacity); base must be 128-B aligned.
+    ArenaAllocator(void* base, size_t capacity) : base_ptr_(base), capacity_(capacity) {
+        if (reinterpret_cast<size_t>(base) & 127)
+            throw std::invalid_argument("ArenaAllocator: borrowed base is not 128-B aligned");
+    }
     ~ArenaAllocator();
     ArenaAllocator(const ArenaAllocator&) = delete;
     ArenaAllocator& operator=(const ArenaAllocator&) = delete;
@@ -33,4 +42,5 @@ private:
     void* base_ptr_ = nullptr;
     size_t offset_ = 0;
     size_t capacity_ = 0;
+    bool owns_ = false;
 };

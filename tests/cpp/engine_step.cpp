@@ -4,7 +4,9 @@
 // (src/core/engine.cu:326-370: launch_rope, launch_write_kv_cache,
 // launch_cached_attention on one stream), then the paged step of the server
 // sandbox (BlockManager fork + copy-on-write, paged append, paged attention,
-// and the shared-prefix form over the forked pair).
+// and the shared-prefix form over the forked pair), and a decode step of
+// several layers over the engine's one-arena KV pool [L0_K | L0_V | L1_K | ...]
+// (engine.cu:187-215, model_state.h:56-64).
 // Inputs come from a fixed xorshift stream; inputs and outputs are written to
 // <out_dir>/*.bin so tests/test_gpu_cpp_host.py can check them against the
 // oracle. Exit status 0 only if every call succeeded and the in-program checks
@@ -19,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "memory/alloc.h"
 #include "memory/block_manager.h"
 #include "ops/kernel.h"
 
@@ -274,6 +277,97 @@ int paged_step(const std::string& dir, hipStream_t s) {
     return 0;
 }
 
+// The engine's KV pool: one ArenaAllocator, [L0_K | L0_V | L1_K | ...], each
+// slab MAX_SEQ x KV_DIM fp16 wrapped in a View (engine.cu:187-215). Rows
+// [pos, MAX_SEQ) of every slab hold NaN, so a read outside a layer's own rows
+// [0, pos) (or past the end of the slab below it) poisons that layer's output.
+// Every layer runs the one-launch step (af_decode_attention_fused) on this
+// pool and the reference's three launches on a second pool; the two must
+// agree bit for bit, and the test compares the whole first pool with the
+// oracle, so a write outside the layer's row `pos` shows up too.
+int pooled_step(const std::string& dir, hipStream_t s) {
+    constexpr int NL = 4;
+    const int pos = 700;
+    const size_t slab = size_t(MAX_SEQ) * KV_DIM * 2;
+    ArenaAllocator arena(NL * 2 * slab);
+    ArenaAllocator arena2(NL * 2 * slab);
+    View kc[NL], vc[NL], kc2[NL], vc2[NL];
+    for (int l = 0; l < NL; ++l) {
+        kc[l] = create_contiguous_view(arena.allocate(slab), DataType::FP16, {MAX_SEQ, KV_DIM});
+        vc[l] = create_contiguous_view(arena.allocate(slab), DataType::FP16, {MAX_SEQ, KV_DIM});
+        kc2[l] = create_contiguous_view(arena2.allocate(slab), DataType::FP16, {MAX_SEQ, KV_DIM});
+        vc2[l] = create_contiguous_view(arena2.allocate(slab), DataType::FP16, {MAX_SEQ, KV_DIM});
+        char* base = static_cast<char*>(arena.base());
+        if (kc[l].data_ptr != base + (2 * l) * slab || vc[l].data_ptr != base + (2 * l + 1) * slab)
+            return 40;
+    }
+    const size_t halves = size_t(NL) * 2 * MAX_SEQ * KV_DIM;
+    std::vector<uint16_t> pool(halves);
+    for (int sl = 0; sl < 2 * NL; ++sl) {
+        auto rows = randn_like(size_t(pos) * KV_DIM, 60 + sl);
+        uint16_t* dst = pool.data() + size_t(sl) * MAX_SEQ * KV_DIM;
+        std::memcpy(dst, rows.data(), rows.size() * 2);
+        for (size_t i = size_t(pos) * KV_DIM; i < size_t(MAX_SEQ) * KV_DIM; ++i) dst[i] = 0x7e00;
+    }
+    auto qkv = randn_like(size_t(NL) * QKV, 70);
+    save(dir, "pl_pool_in", pool.data(), halves * 2);
+    save(dir, "pl_qkv_in", qkv.data(), qkv.size() * 2);
+    HIP_OK(hipMemcpy(arena.base(), pool.data(), halves * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(arena2.base(), pool.data(), halves * 2, hipMemcpyHostToDevice));
+    float *d_cos = nullptr, *d_sin = nullptr;
+    HIP_OK(hipMalloc(&d_cos, size_t(MAX_SEQ) * HD / 2 * 4));
+    HIP_OK(hipMalloc(&d_sin, size_t(MAX_SEQ) * HD / 2 * 4));
+    build_rope_cache(d_cos, d_sin, MAX_SEQ, HD, THETA, s);
+    uint16_t* d_qkv = dev_upload(qkv);
+    uint16_t* d_qkv2 = dev_upload(qkv);
+    uint16_t *d_out = nullptr, *d_out2 = nullptr;
+    HIP_OK(hipMalloc(&d_out, size_t(NL) * Q_DIM * 2));
+    HIP_OK(hipMalloc(&d_out2, size_t(NL) * Q_DIM * 2));
+    const size_t ws_bytes = af_attention_workspace_size(1, NH, NKV, HD, 0);
+    void* ws = nullptr;
+    HIP_OK(hipMalloc(&ws, ws_bytes));
+    if (af_attention_workspace_init(ws, ws_bytes, s) != AF_OK) return 41;
+    // the split count launch_cached_attention picks for pos + 1 rows
+    const int splits = af_attention_default_splits(pos + 1, 1, NKV);
+    for (int l = 0; l < NL; ++l) {
+        uint16_t* q = d_qkv + size_t(l) * QKV;
+        if (af_decode_attention_fused(q, kc[l].data_ptr, vc[l].data_ptr, d_cos, d_sin, pos,
+                                      nullptr, MAX_SEQ, d_out + size_t(l) * Q_DIM, NH, NKV, HD,
+                                      splits, ws, ws_bytes, nullptr, s) != AF_OK)
+            return 42;
+        // the reference's three launches on the second pool (engine.cu:340-369)
+        uint16_t* q2 = d_qkv2 + size_t(l) * QKV;
+        View qv = create_contiguous_view(q2, DataType::FP16, {1, Q_DIM});
+        View kv = create_contiguous_view(q2 + Q_DIM, DataType::FP16, {1, KV_DIM});
+        View qkv_v = create_contiguous_view(q2, DataType::FP16, {1, QKV});
+        launch_rope(qv, kv, d_cos + size_t(pos) * (HD / 2), d_sin + size_t(pos) * (HD / 2), 1, NKV,
+                    NH, HD, s);
+        launch_write_kv_cache(qkv_v, kc2[l], vc2[l], pos, Q_DIM, KV_DIM, s);
+        launch_cached_attention(reinterpret_cast<const __half*>(q2),
+                                static_cast<const __half*>(kc2[l].data_ptr),
+                                static_cast<const __half*>(vc2[l].data_ptr),
+                                reinterpret_cast<__half*>(d_out2 + size_t(l) * Q_DIM), pos + 1, HD,
+                                NH, NKV, s);
+    }
+    HIP_OK(hipStreamSynchronize(s));
+    auto pool_out = dev_download(static_cast<const uint16_t*>(arena.base()), halves);
+    auto qkv_out = dev_download(d_qkv, size_t(NL) * QKV);
+    auto out = dev_download(d_out, size_t(NL) * Q_DIM);
+    save(dir, "pl_pool_out", pool_out.data(), halves * 2);
+    save(dir, "pl_qkv_out", qkv_out.data(), qkv_out.size() * 2);
+    save(dir, "pl_attn", out.data(), out.size() * 2);
+    int bad = 0;
+    if (dev_download(static_cast<const uint16_t*>(arena2.base()), halves) != pool_out) bad |= 1;
+    if (dev_download(d_qkv2, size_t(NL) * QKV) != qkv_out) bad |= 2;
+    // Same split count on both sides, so the attention bits agree.
+    if (dev_download(d_out2, size_t(NL) * Q_DIM) != out) bad |= 4;
+    for (void* p : {(void*)d_cos, (void*)d_sin, (void*)d_qkv, (void*)d_qkv2, (void*)d_out,
+                    (void*)d_out2, ws})
+        HIP_OK(hipFree(p));
+    if (bad) std::fprintf(stderr, "pooled fused step differs from the three launches (mask %d)\n", bad);
+    return bad ? 43 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -288,6 +382,7 @@ int main(int argc, char** argv) {
         HIP_OK(hipStreamCreate(&s));
         int rc = contiguous_step(dir, s);
         if (rc == 0) rc = paged_step(dir, s);
+        if (rc == 0) rc = pooled_step(dir, s);
         HIP_OK(hipStreamDestroy(s));
         if (rc == 0) std::puts("ok");
         return rc;

@@ -32,7 +32,11 @@ def contiguous_case(max_seq, filled, seed, nq=NQ, nkv=NKV, hd=HD):
 
 
 # Attention tolerance: fp16 KV within max-abs 2e-3 /
-# rel 1e-2, FP8 KV within 5e-2, read elementwise as |got - ref| <= atol + rtol*|ref|.
+# rel 1e-2, FP8 KV within 5e-2. Two separate bounds, both enforced literally:
+#   max |got - ref|                       <= atol  (2e-3 fp16 KV, 5e-2 FP8 KV)
+#   ||got - ref||_2 / ||ref||_2           <= rtol  (1e-2)
+# The relative bound is norm-wise: an elementwise ratio is unbounded where the
+# reference is near zero, and there the absolute bound already holds the error.
 ATOL_F16, RTOL_F16 = 2e-3, 1e-2
 ATOL_FP8, RTOL_FP8 = 5e-2, 1e-2
 
@@ -40,12 +44,20 @@ ATOL_FP8, RTOL_FP8 = 5e-2, 1e-2
 def assert_attn_close(got, ref, atol=ATOL_F16, rtol=RTOL_F16, what=""):
     g = np.asarray(got, np.float64)
     r = np.asarray(ref, np.float64)
+    assert g.shape == r.shape or g.size == r.size, (what, g.shape, r.shape)
+    g, r = g.ravel(), r.ravel()
     assert np.all(np.isfinite(g)), f"{what}: non-finite output"
     err = np.abs(g - r)
-    bad = err > atol + rtol * np.abs(r)
-    assert not bad.any(), (f"{what}: {bad.sum()} elements outside atol={atol} rtol={rtol}; "
-                           f"max abs err {err.max():.3e} at {int(err.argmax())}")
-    return float(err.max())
+    max_abs = float(err.max()) if err.size else 0.0
+    norm_ref = float(np.linalg.norm(r))
+    rel = float(np.linalg.norm(g - r)) / norm_ref if norm_ref > 0 else max_abs
+    print(f"[err] {what}: max abs {max_abs:.3e} (bar {atol:g}), rel {rel:.3e} (bar {rtol:g})",
+          flush=True)
+    assert max_abs <= atol, (f"{what}: max abs err {max_abs:.3e} > {atol:g} at element "
+                             f"{int(err.argmax())} (got {g[err.argmax()]:.6f}, "
+                             f"ref {r[err.argmax()]:.6f})")
+    assert rel <= rtol, f"{what}: relative err {rel:.3e} > {rtol:g}"
+    return max_abs
 
 
 # ---- W8A16 GEMV inputs (FP8 E4M3 weights with fp16 group scales) ------------

@@ -83,3 +83,31 @@ def test_cpp_host_decode_steps(gpu, tmp_path):
                           np.stack(roped_rows).view(np.uint16))
     assert np.array_equal(load(d, "p_pool_out", np.uint16, (2, total * bs, KV_DIM)),
                           pool.view(np.uint16))
+
+
+def test_cpp_host_pooled_layers(gpu, tmp_path):
+    """Row a4: the engine's one-arena KV pool [L0_K | L0_V | L1_K | ...] of
+    MAX_SEQ x KV_DIM fp16 slabs (engine.cu:187-215, model_state.h:56-64) carved
+    by ArenaAllocator into Views; four layers' fused decode steps at pos 700.
+    Rows [700, MAX_SEQ) of every slab hold NaN. The whole pool after the step
+    must equal the oracle's (each layer's row 700 appended, nothing else
+    touched, canaries included); each layer's attention must meet the bar."""
+    print("[case] C++ host: pooled 4-layer decode step", flush=True)
+    r = subprocess.run([EXE, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
+    d = str(tmp_path)
+    NL, pos = 4, 700
+    pool = load(d, "pl_pool_in", np.float16, (NL, 2, MAX_SEQ, KV_DIM)).copy()
+    assert np.isnan(pool[:, :, pos:].astype(np.float32)).all()
+    qkv = load(d, "pl_qkv_in", np.float16, (NL, QKV))
+    c, s = oracle.rope_table(MAX_SEQ, HD, THETA)
+    got_qkv = load(d, "pl_qkv_out", np.uint16, (NL, QKV))
+    got_attn = load(d, "pl_attn", np.float16, (NL, Q_DIM))
+    for layer in range(NL):
+        k, v = pool[layer, 0], pool[layer, 1]  # views: rope_append writes row pos in place
+        roped = oracle.rope_append(qkv[layer], k, v, c, s, pos, NQ, NKV, HD)
+        assert np.array_equal(got_qkv[layer], roped.view(np.uint16)), layer
+        ref = oracle.cached_attention_f64(roped[:Q_DIM], k, v, pos + 1, NQ, NKV, HD)
+        assert_attn_close(got_attn[layer], ref, what=f"pooled layer {layer}")
+    got_pool = load(d, "pl_pool_out", np.uint16, (NL, 2, MAX_SEQ, KV_DIM))
+    assert np.array_equal(got_pool, pool.view(np.uint16))
