@@ -45,6 +45,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx8k_pmc.txt")
 PAGED_PMC_SUMMARY = os.path.join(ROOT, "profiles", "paged_attn_pmc.txt")
+PMC_SUMMARY_32K = os.path.join(ROOT, "profiles", "decode_attn_c2_ctx32k_pmc.txt")
 METRIC = "decode-attn KV-read GB/s (% of 8 TB/s HBM) + us/layer-step at ctx 8k"
 
 
@@ -66,7 +67,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--no-serving", action="store_true", help="skip the continuous-batching step")
-    ap.add_argument("--no-weights", action="store_true", help="skip the .bin load measurement")
+    ap.add_argument("--weights", action="store_true",
+                    help="also time writing and loading a 4.9 GiB Llama-3.2-3B-shaped .bin")
+    ap.add_argument("--no-weights", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-matrix", action="store_true",
+                    help="skip the per-config matrix (configs[1] ctx 1k/32k, configs[2..4])")
     ap.add_argument("--fanout-only", action="store_true",
                     help="run only the fan-out decode measurement and print its JSON object")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -84,10 +89,30 @@ def read_traffic(path=PMC_SUMMARY, key="traffic_bytes_per_launch:"):
     return None
 
 
-def cpu_baseline(ctx):
-    """One 28-layer decode step (append + attention) on the scalar C++ oracle, timed with
-    1 thread and with one thread per query head up to the host cores this process may use
-    (at most 16, the GPU box's share per GPU). The threaded figure is the reported value."""
+def host_cpu():
+    """CPU model, logical cores on the host, and the cores this process may run on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1, len(os.sched_getaffinity(0))
+
+
+def cpu_threads():
+    """Worker threads for the CPU baselines: the cores this process may use, at most 16
+    (the GPU box's CPU share per GPU)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_baseline(ctx, runs_threaded=5, runs_single=3):
+    """One 28-layer decode step (append + attention) on the scalar C++ oracle: the
+    median of `runs_threaded` runs with one thread per query head (up to the cores this
+    process may use, at most 16) is the value; the median of `runs_single` one-thread
+    runs is reported beside it."""
     import oracle
 
     L = ctx + 1
@@ -98,7 +123,7 @@ def cpu_baseline(ctx):
     v[:ctx] = r.standard_normal((ctx, KV_DIM)).astype(np.float16)
     cos, sin = oracle.rope_table(L, HD, THETA)
     qkv = r.standard_normal((LAYERS, QKV)).astype(np.float16)
-    threads = max(1, min(16, NQ, len(os.sched_getaffinity(0))))
+    threads = min(cpu_threads(), NQ)
 
     def step(nt):
         t0 = time.perf_counter()
@@ -107,40 +132,126 @@ def cpu_baseline(ctx):
             oracle.cached_attention(rq[:Q_DIM], k, v, L, NQ, NKV, HD, threads=nt)
         return time.perf_counter() - t0
 
-    dt1 = step(1)
-    dtn = step(threads) if threads > 1 else dt1
+    tn = [step(threads) for _ in range(runs_threaded)]
+    t1 = [step(1) for _ in range(runs_single)]
+    dtn, dt1 = float(np.median(tn)), float(np.median(t1))
     gbs = lambda dt: LAYERS * L * KV_DIM * 2 * 2 / dt / 1e9
+    model, host_cores, allowed = host_cpu()
     return {"value": round(gbs(dtn), 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one 28-layer decode step at ctx {ctx} (RoPE+append + attention over "
-                      f"{L} tokens per layer) on the C++ oracle, {threads} threads over query "
-                      f"heads: {dtn:.2f} s; 1 thread: {dt1:.2f} s",
-            "ms_per_step": round(dtn * 1e3, 1), "single_thread_gbs": round(gbs(dt1), 3),
-            "single_thread_ms_per_step": round(dt1 * 1e3, 1)}
+                      f"{L} tokens per layer) on the C++ oracle; value = median of "
+                      f"{runs_threaded} runs with {threads} threads over query heads "
+                      f"({dtn:.3f} s); 1 thread: median of {runs_single} runs ({dt1:.2f} s)",
+            "ms_per_step": round(dtn * 1e3, 1), "runs": runs_threaded,
+            "single_thread_gbs": round(gbs(dt1), 3),
+            "single_thread_ms_per_step": round(dt1 * 1e3, 1), "single_thread_runs": runs_single,
+            "cpu_model": model, "host_logical_cores": host_cores, "cores_allowed": allowed}
+
+
+def cpu_baseline_paged(cfg, host, runs=3):
+    """The oracle's paged attention (ok_paged_attention_f16 / _fp8) over one layer of
+    BASELINE configs[cfg - 1] with the GPU run's block tables and lengths, on host
+    data of the same layout: every sequence for configs[2] and [3], 8 sequences
+    (the first 8 of the batch) for configs[4]. Sequences run in parallel on
+    cpu_threads() threads (ctypes releases the GIL); value = median of `runs` runs,
+    one single-thread run beside it."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    lens, bs, fp8 = host["lens"], host["bs"], host["fp8"]
+    B = len(lens) if cfg != 5 else 8
+    r = np.random.Generator(np.random.PCG64(0xA70F10 + 40 + cfg))
+    # The blocks the sampled sequences name, renumbered in random order into compact
+    # host slabs (shared blocks stay shared): the same rows per sequence and a
+    # scattered block order, as on the GPU.
+    nblk = [(int(lens[b]) + bs - 1) // bs for b in range(B)]
+    used = np.unique(np.concatenate([host["tables"][b, :nblk[b]] for b in range(B)]))
+    remap = np.full(int(used.max()) + 1, -1, np.int64)
+    remap[used] = r.permutation(len(used))
+    tables = [remap[host["tables"][b, :nblk[b]]].astype(np.int32) for b in range(B)]
+    rows = len(used) * bs
+    # timing only: values are fp16 bit patterns of magnitude in [2^-7, 4) or E4M3 codes
+    if fp8:
+        kslab = r.integers(0, 0x7F, (rows, KV_DIM), dtype=np.uint8)
+        vslab = r.integers(0, 0x7F, (rows, KV_DIM), dtype=np.uint8)
+        sc = np.full(NKV, 5.0 / 448.0, np.float32)
+    else:
+        kslab = r.integers(0x2000, 0x4400, (rows, KV_DIM), dtype=np.uint16).view(np.float16)
+        vslab = r.integers(0x2000, 0x4400, (rows, KV_DIM), dtype=np.uint16).view(np.float16)
+    q = r.standard_normal((B, Q_DIM), dtype=np.float32).astype(np.float16)
+
+    def one(b):
+        if fp8:
+            oracle.paged_attention_fp8(q[b], kslab, vslab, sc, sc, tables[b], int(lens[b]), bs,
+                                       NQ, NKV, HD)
+        else:
+            oracle.paged_attention_f16(q[b], kslab, vslab, tables[b], int(lens[b]), bs, NQ, NKV,
+                                       HD)
+
+    threads = cpu_threads()
+
+    def layer(nt):
+        t0 = time.perf_counter()
+        if nt == 1:
+            for b in range(B):
+                one(b)
+        else:
+            with ThreadPoolExecutor(nt) as ex:
+                list(ex.map(one, range(B)))
+        return time.perf_counter() - t0
+
+    tn = [layer(threads) for _ in range(runs)]
+    t1 = layer(1)
+    dtn = float(np.median(tn))
+    esz = 1 if fp8 else 2
+    nbytes = int(sum(int(lens[b]) for b in range(B))) * KV_DIM * esz * 2
+    model, host_cores, allowed = host_cpu()
+    return {"value": round(nbytes / dtn / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"one layer of configs[{cfg - 1}]: paged attention of {B} sequences "
+                      f"({nbytes} KV bytes attended) on the C++ oracle, the GPU run's block "
+                      f"tables; value = median of {runs} runs on {threads} threads "
+                      f"({dtn:.3f} s); 1 thread: one run ({t1:.2f} s)",
+            "runs": runs, "single_thread_gbs": round(nbytes / t1 / 1e9, 3),
+            "cpu_model": model, "host_logical_cores": host_cores, "cores_allowed": allowed}
 
 
 class Timer:
+    """Times graph replays with one HIP event pair per replay, on the replay stream
+    (the reference's own timing takes the median of graph replays, main.cu:125-150).
+    graph_ms returns the median; mean_ms holds the mean of the same replays."""
+
     def __init__(self, dev, stream, warmup):
         self.dev, self.stream, self.warmup = dev, stream, warmup
-        self.e0, self.e1 = dev.Event(), dev.Event()
+        self.events = []
+        self.mean_ms = None
 
     def graph_ms(self, graph, reps):
-        """Mean ms per replay of `graph`, HIP events on the replay stream."""
+        """Median ms per replay of `graph` over `reps` replays (after the warmup)."""
         for _ in range(self.warmup):
             graph.launch(self.stream)
         self.dev.synchronize()
-        self.e0.record(self.stream)
-        for _ in range(reps):
+        while len(self.events) < reps + 1:
+            self.events.append(self.dev.Event())
+        ev = self.events
+        for i in range(reps):
+            ev[i].record(self.stream)
             graph.launch(self.stream)
-        self.e1.record(self.stream)
-        self.e1.sync()
+        ev[reps].record(self.stream)
+        ev[reps].sync()
         self.dev.synchronize()
-        return self.e0.elapsed_ms(self.e1) / reps
+        t = [ev[i].elapsed_ms(ev[i + 1]) for i in range(reps)]
+        self.mean_ms = float(np.mean(t))
+        return float(np.median(t))
 
 
-def bench_contiguous(args, dev, kv, lib, info):
+def bench_contiguous(args, dev, kv, lib, info, ctx=None, lean=False):
+    """configs[1] at one context length. lean: the fused step, the two-launch step
+    and the attention kernel only (the matrix entries); otherwise also the QKV
+    projection and the prefill / serving / GEMV legs."""
     import atomflow_amd
 
-    ctx = args.ctx
+    ctx = args.ctx if ctx is None else ctx
     L = ctx + 1
     max_seq = (L + 127) // 128 * 128
     slab = max_seq * KV_DIM * 2
@@ -158,14 +269,16 @@ def bench_contiguous(args, dev, kv, lib, info):
     ws = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
     # The projection either side of the path: FP8 E4M3 QKV weights [QKV, HIDDEN]
     # with fp16 per-128 group scales and an fp16 activation row, per layer.
-    w_qkv = dev.DeviceBuffer(LAYERS * QKV * HIDDEN)
-    s_qkv = dev.DeviceBuffer(LAYERS * QKV * (HIDDEN // 128) * 2)
-    x_act = dev.DeviceBuffer(LAYERS * HIDDEN * 2)
-    atomflow_amd.check(lib.af_rt_fill_randn_fp8(w_qkv.ptr, LAYERS * QKV * HIDDEN, 13, 20.0,
+    proj_layers = 1 if lean else LAYERS
+    w_qkv = dev.DeviceBuffer(proj_layers * QKV * HIDDEN)
+    s_qkv = dev.DeviceBuffer(proj_layers * QKV * (HIDDEN // 128) * 2)
+    x_act = dev.DeviceBuffer(proj_layers * HIDDEN * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_fp8(w_qkv.ptr, proj_layers * QKV * HIDDEN, 13, 20.0,
                                                 stream.handle))
-    atomflow_amd.check(lib.af_rt_fill_randn_f16(s_qkv.ptr, LAYERS * QKV * (HIDDEN // 128), 17,
-                                                0.002, stream.handle))
-    atomflow_amd.check(lib.af_rt_fill_randn_f16(x_act.ptr, LAYERS * HIDDEN, 19, 1.0, stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(s_qkv.ptr, proj_layers * QKV * (HIDDEN // 128),
+                                                17, 0.002, stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(x_act.ptr, proj_layers * HIDDEN, 19, 1.0,
+                                                stream.handle))
     stream.sync()
 
     def ptrs(l):
@@ -211,28 +324,36 @@ def bench_contiguous(args, dev, kv, lib, info):
             kv.launch_qkv_rope_append(x, w, sc, HIDDEN, q, k, v, d_cos, d_sin, ctx, max_seq, NQ, NKV,
                                       HD, stream=stream)
 
-    graphs = {name: dev.Graph.capture(stream, fn) for name, fn in
-              (("step", step), ("two", step_two_launch), ("attn", attention_only),
-               ("proj_step", step_with_projection), ("proj", projection_only))}
+    legs = [("step", step), ("two", step_two_launch), ("attn", attention_only)]
+    if not lean:
+        legs += [("proj_step", step_with_projection), ("proj", projection_only)]
+    graphs = {name: dev.Graph.capture(stream, fn) for name, fn in legs}
     t = Timer(dev, stream, args.warmup)
-    log(f"splits {splits}; warmup {args.warmup}, timing {args.steps} graph replays")
+    log(f"splits {splits}; warmup {args.warmup}, timing {args.steps} graph replays (median)")
     ms_step = t.graph_ms(graphs["step"], args.steps)
+    ms_step_mean = t.mean_ms
     ms_two = t.graph_ms(graphs["two"], args.steps)
     ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
-    ms_proj_step = t.graph_ms(graphs["proj_step"], args.steps)
-    ms_proj = t.graph_ms(graphs["proj"], args.steps) / LAYERS
+    ms_proj_step = ms_proj = None
+    if not lean:
+        ms_proj_step = t.graph_ms(graphs["proj_step"], args.steps)
+        ms_proj = t.graph_ms(graphs["proj"], args.steps) / LAYERS
     log(f"step {ms_step * 1e3:.1f} us (two-launch {ms_two * 1e3:.1f} us), "
         f"attention {ms_attn * 1e3:.2f} us/launch")
     for g in graphs.values():
         g.destroy()
+    for b in (pool, qkv, out, d_cos, d_sin, w_qkv, s_qkv, x_act):
+        b.free()
 
     kv_bytes = L * KV_DIM * 2 * 2          # K and V rows attended, each byte once
     proj_bytes = QKV * HIDDEN + QKV * (HIDDEN // 128) * 2 + HIDDEN * 2 + QKV * 2
     step_gbs = LAYERS * kv_bytes / (ms_step * 1e-3) / 1e9
     attn_gbs = kv_bytes / (ms_attn * 1e-3) / 1e9
+    pmc = {8192: PMC_SUMMARY, 32768: PMC_SUMMARY_32K}.get(ctx)
     result = {
         "metric": METRIC, "value": round(step_gbs, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "ms_per_step_mean": round(ms_step_mean, 4),
         "us_per_layer_step": round(ms_step * 1e3 / LAYERS, 3),
         "pct_of_hbm_peak": round(100 * step_gbs / HBM_PEAK_GBS, 1),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -245,16 +366,19 @@ def bench_contiguous(args, dev, kv, lib, info):
                    "device": info["name"], "arch": info["arch"], "cus": info["compute_units"]},
         "kernels": {"decode_attn_us": round(ms_attn * 1e3, 3),
                     "two_launch_us_per_layer_step": round(ms_two * 1e3 / LAYERS, 3),
-                    "attn_kv_bytes_per_launch": kv_bytes,
-                    "qkv_rope_append_us": round(ms_proj * 1e3, 3),
-                    "qkv_weight_bytes_per_launch": proj_bytes,
-                    "qkv_rope_append_gbs": round(proj_bytes / (ms_proj * 1e-3) / 1e9, 1),
-                    "layer_step_with_qkv_projection_us": round(ms_proj_step * 1e3 / LAYERS, 3)},
+                    "attn_kv_bytes_per_launch": kv_bytes},
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic() if ctx == 8192 else None},
+                     "traffic": read_traffic(pmc) if pmc else None},
         "cpu_baseline": None,
     }
+    if lean:
+        return result
+    result["kernels"].update({
+        "qkv_rope_append_us": round(ms_proj * 1e3, 3),
+        "qkv_weight_bytes_per_launch": proj_bytes,
+        "qkv_rope_append_gbs": round(proj_bytes / (ms_proj * 1e-3) / 1e9, 1),
+        "layer_step_with_qkv_projection_us": round(ms_proj_step * 1e3 / LAYERS, 3)})
     if not args.no_prefill:
         log("prefill (one layer) ...")
         result["prefill"] = bench_prefill(dev, kv, lib, stream, 3, 10)
@@ -270,7 +394,7 @@ def bench_contiguous(args, dev, kv, lib, info):
         result["serving_fanout"] = bench_fanout(dev, kv, lib)
     log("projection GEMVs ...")
     result["gemv"] = bench_gemv(dev, kv, lib, args.steps, args.warmup)
-    if not args.no_weights:
+    if args.weights:
         log("weights (.bin load) ...")
         result["weights"] = bench_weights(dev)
     if args.calibrate_copy:
@@ -787,11 +911,13 @@ def bench_weights(dev, path_dir="/tmp"):
             os.remove(path)
 
 
-def bench_paged(args, dev, kv, lib, info):
+def bench_paged(args, dev, kv, lib, info, cfg=None, cpu=False):
+    """BASELINE configs[cfg - 1] (cfg 3, 4, 5) through the BlockManager. cpu: also the
+    oracle's time on a bounded sample of the same layer (cpu_baseline_paged)."""
     import atomflow_amd
     from atomflow_amd import AF_KV_FP16, AF_KV_FP8_E4M3
 
-    cfg = args.config
+    cfg = args.config if cfg is None else cfg
     r = np.random.Generator(np.random.PCG64(0xA70F10 + cfg))
     if cfg == 3:
         bs, fp8 = 16, False
@@ -910,11 +1036,13 @@ def bench_paged(args, dev, kv, lib, info):
         graphs["attn_sp"] = dev.Graph.capture(stream, attention_sp)
     t = Timer(dev, stream, args.warmup)
     ms_step = t.graph_ms(graphs["step"], args.steps)
+    ms_step_mean = t.mean_ms
     ms_attn = t.graph_ms(graphs["attn"], args.steps) / LAYERS
     ms_step_plain = ms_attn_plain = None
     if cfg == 4:
         ms_step_plain, ms_attn_plain = ms_step, ms_attn
         ms_step = t.graph_ms(graphs["step_sp"], args.steps)
+        ms_step_mean = t.mean_ms
         ms_attn = t.graph_ms(graphs["attn_sp"], args.steps) / LAYERS
     for g in graphs.values():
         g.destroy()
@@ -928,7 +1056,8 @@ def bench_paged(args, dev, kv, lib, info):
     result = {
         "metric": METRIC + f" [paged configs[{cfg - 1}]]", "value": round(step_gbs, 1),
         "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4), "us_per_layer_step": round(ms_step * 1e3 / LAYERS, 3),
+        "ms_per_step": round(ms_step, 4), "ms_per_step_mean": round(ms_step_mean, 4),
+        "us_per_layer_step": round(ms_step * 1e3 / LAYERS, 3),
         "pct_of_hbm_peak": round(100 * step_gbs / HBM_PEAK_GBS, 1), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": ("fp8 e4m3" if fp8 else "f16") + " KV, fp32 softmax/accumulate",
@@ -957,8 +1086,32 @@ def bench_paged(args, dev, kv, lib, info):
             "plain_us_per_layer_step": round(ms_step_plain * 1e3 / LAYERS, 3),
             "plain_step_gbs_logical": round(LAYERS * logical / (ms_step_plain * 1e-3) / 1e9, 1)})
         result["kernels"].update(cow_copy_timing(dev, kv, bm, prefix, B, stream, desc))
+        # The same algorithmic bytes as the shared-prefix path (the answer needs
+        # every unique row once); the plain kernel re-reads the prefix per fork,
+        # mostly from L2/MALL, which logical_gbs shows.
+        plain_gbs = algo_bytes / (ms_attn_plain * 1e-3) / 1e9
+        result["plain"] = {
+            "us_per_layer_step": round(ms_step_plain * 1e3 / LAYERS, 3),
+            "attn_us": round(ms_attn_plain * 1e3, 3),
+            "logical_gbs": round(logical / (ms_attn_plain * 1e-3) / 1e9, 1),
+            "roofline": {"bound": "hbm", "achieved": round(plain_gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(plain_gbs / HBM_PEAK_GBS, 4),
+                         "bytes": "unique KV rows (shared prefix once)",
+                         "traffic": read_traffic(PAGED_PMC_SUMMARY,
+                                                 "traffic_bytes_per_launch configs[3] plain:")}}
     if args.calibrate_copy:
         calibrate_copy(dev, kv, stream)
+    if cpu:
+        host = {"tables": tables, "lens": lens_after, "bs": bs, "fp8": fp8,
+                "total_blocks": total_blocks, "unique_rows": unique_tokens}
+    bm.close()
+    pool.free()
+    for b in (qkv, out, d_tables, d_lens, d_slots, d_pos, d_cos, d_sin):
+        b.free()
+    if cpu:
+        log(f"configs[{cfg - 1}] cpu baseline (oracle on a sample of one layer) ...")
+        result["cpu_baseline"] = cpu_baseline_paged(cfg, host)
     return result
 
 
@@ -996,6 +1149,47 @@ def calibrate_copy(dev, kv, stream, mib=256, reps=3):
     log(f"copy calibration: {reps} x paged_gather of {2 * rows * KV_DIM * 2} B read + same written")
 
 
+def matrix_entry(res, name, attn_key="paged_attn_us"):
+    """The per-workload summary kept in the default run's `matrix` object."""
+    k = res["kernels"]
+    return {"workload": name, "us_per_layer_step": res["us_per_layer_step"],
+            "attn_us_per_launch": k.get(attn_key),
+            "attn_gbs": res["roofline"]["achieved"], "roofline": res["roofline"],
+            "ms_per_step": res["ms_per_step"], "config": res["config"],
+            "cpu_baseline": res.get("cpu_baseline")}
+
+
+def bench_matrix(args, dev, kv, lib, info, headline):
+    """Every BASELINE config point on the GPU, in the default run: configs[1] at ctx
+    1024 / 8192 / 32768, configs[2] (paged fp16), configs[3] (64 forks of a shared
+    prefix: the shared-prefix path and the plain paged kernel), configs[4] (paged
+    FP8, ~93 GiB pool). Paged entries carry an oracle CPU baseline on a sample."""
+    cpu = not args.no_cpu
+    m = {"configs[1] ctx 8192": matrix_entry(headline, "configs[1] ctx 8192", "decode_attn_us")}
+    m["configs[1] ctx 8192"]["cpu_baseline"] = headline.get("cpu_baseline")
+    for ctx in (1024, 32768):
+        log(f"matrix: configs[1] ctx {ctx} ...")
+        r = bench_contiguous(args, dev, kv, lib, info, ctx=ctx, lean=True)
+        m[f"configs[1] ctx {ctx}"] = matrix_entry(r, f"configs[1] ctx {ctx}", "decode_attn_us")
+    for cfg in (3, 4, 5):
+        log(f"matrix: configs[{cfg - 1}] ...")
+        r = bench_paged(args, dev, kv, lib, info, cfg=cfg, cpu=cpu)
+        if cfg == 4:
+            m["configs[3] shared-prefix path"] = matrix_entry(r, "configs[3] shared-prefix path "
+                                                             "(af_paged_attention_shared_prefix)")
+            p = r["plain"]
+            m["configs[3] plain paged kernel"] = {
+                "workload": "configs[3] through af_paged_attention (each fork reads the prefix)",
+                "us_per_layer_step": p["us_per_layer_step"], "attn_us_per_launch": p["attn_us"],
+                "attn_gbs": p["roofline"]["achieved"], "logical_gbs": p["logical_gbs"],
+                "roofline": p["roofline"],
+                "cpu_baseline": r.get("cpu_baseline")}
+        else:
+            name = {3: "configs[2] paged fp16", 5: "configs[4] paged fp8"}[cfg]
+            m[name] = matrix_entry(r, name)
+    return m
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1018,6 +1212,8 @@ def main():
         if not args.no_cpu:
             log("cpu baseline (C++ oracle, threaded and 1 thread) ...")
             result["cpu_baseline"] = cpu_baseline(args.ctx)
+        if not args.no_matrix and args.ctx == 8192:
+            result["matrix"] = bench_matrix(args, dev, kv, lib, info, result)
     else:
         result = bench_paged(args, dev, kv, lib, info)
     print(json.dumps(result), flush=True)
