@@ -8,6 +8,14 @@
 
 #include "af_kv.h"
 
+// Every kernel here is written for gfx950 (CDNA4) alone: wave64 reductions,
+// its MFMA / transpose-load / FP8-convert forms, and the gfx9 memory-counter
+// rules the split-K combine of decode_attention.hip depends on. Another device
+// target must fail to build rather than compile into something subtly wrong.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "atomflow_amd kernels target gfx950 only: build with --offload-arch=gfx950"
+#endif
+
 #define AF_TRY_HIP(expr)                              \
     do {                                              \
         hipError_t af_e_ = (expr);                    \

@@ -213,10 +213,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // Balanced partition of rows [t_lo, L) in whole workgroup steps
     // (kStepTokens rows): C steps use n = min(num_splits, ceil(C / span)) splits
     // and split s owns steps [s*C/n, (s+1)*C/n). t_lo = row_start, the first row
-    // after a shared prefix (0 without one). A sequence no longer than the
+    // after a shared prefix (0 without one). A sequence exactly as long as the
     // prefix gets one split over its last row with every row masked (an empty
-    // partial), so the combine still runs over the prefix records.
-    const int t_lo = min(a.row_start, L - 1);
+    // partial), so the combine still runs over the prefix records. A sequence
+    // shorter than the prefix attends its own rows [0, L) through its table
+    // and its combine leaves the prefix records out (they cover rows >= L).
+    const bool below_prefix = L < a.row_start;
+    const int pre_used = below_prefix ? 0 : a.pre_records;  // prefix records this (b, h) merges
+    const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
     const int total_steps = (L - t_lo + kStepTokens - 1) / kStepTokens;
     const int span_steps = max(1, a.span_tokens / kStepTokens);
     const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
@@ -225,9 +229,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     const int step_end = int(int64_t(split + 1) * total_steps / n_active);
     const int t_begin = t_lo + step_begin * kStepTokens;
     const int t_end = min(L, t_lo + step_end * kStepTokens);
-    const int t_valid = L > a.row_start ? t_end : t_begin;  // rows below t_valid are scored
+    const int t_valid = L == a.row_start ? t_begin : t_end;  // rows below t_valid are scored
     const int n_steps = step_end - step_begin;  // >= 1
-    const bool direct = n_active == 1 && a.pre_records == 0;  // no combine: write the output
+    const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -619,12 +623,28 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     }
 
     // ---- arrival: the last split of (b, h) to finish combines --------------
-    // Partials are agent-scope atomic stores (written through to the level
-    // where every XCD sees them); each wave waits until its stores are
-    // performed before the barrier, then one relaxed agent-scope increment
-    // publishes the split. The last arrival reads the partials with
-    // agent-scope atomic loads. This replaces a device-wide fence, whose L2
-    // write-back + invalidate per workgroup costs far more than the kernel.
+    // No release/acquire fence: a device-wide fence costs an L2 write-back and
+    // invalidate per workgroup, more than the kernel itself. Correctness rests
+    // instead on these gfx950 (gfx9-family) rules, which the language-level
+    // model does not promise for relaxed atomics:
+    //  1. An agent-scope relaxed store lowers to `global_store ... sc1`. The
+    //     scope bits make it write through the CU's L1 and this XCD's L2 to the
+    //     memory side every XCD reads (MALL / HBM).
+    //  2. On gfx9 the vmcnt counter covers stores as well as loads (there is
+    //     no separate store counter as on gfx10+), and a store retires from it
+    //     only once acknowledged at its scope. So `s_waitcnt vmcnt(0)` below
+    //     returns only after this wave's partials are visible device-wide.
+    //  3. `s_barrier` after that wait orders the four waves. The counter's
+    //     `global_atomic_add` (agent scope, returning) is issued by thread 0
+    //     after the barrier, so after every wave's partials are visible.
+    //     Device atomics are performed at the memory side, one total order.
+    //  4. The last arrival reads partials with agent-scope relaxed loads
+    //     (`global_load ... sc1`, served from the memory side, not a stale
+    //     L1/L2 line). They sit behind the __syncthreads that publishes
+    //     s_last, a workgroup-scope fence no atomic load is hoisted above, and
+    //     the hardware issues them in program order after the branch.
+    // tests/test_combine_isa.py compiles this file and checks the emitted
+    // order of these instructions; af_common.h rejects any other target.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -646,10 +666,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // flight.
     constexpr int CB = 16;  // splits per batch
     constexpr int MLPT = (2 * GROUP * kMaxSplits + kThreads - 1) / kThreads;
-    const int n_rec = a.pre_records + n_active;  // shared-prefix records, then the splits'
+    const int n_rec = pre_used + n_active;  // shared-prefix records, then the splits'
     const int n_ml = n_rec * 2 * GROUP;
-    const float* ml = a.part_ml + rec * 2 * GROUP;
-    const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + rec * GHD);
+    const size_t rec0 = rec + (a.pre_records - pre_used);  // first record merged
+    const float* ml = a.part_ml + rec0 * 2 * GROUP;
+    const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + rec0 * GHD);
     float mlv[MLPT];
 #pragma unroll
     for (int r = 0; r < MLPT; ++r) {
@@ -1090,9 +1111,11 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     }
     if (batch == 0) return AF_OK;
     if (int64_t(batch) * nkv > kMaxCounters) return AF_ERR_UNSUPPORTED;
-    // The splits cover the rows after the prefix (at least one row each).
+    // The splits cover the rows after the prefix (at least one row each), or
+    // all rows [0, L) of a sequence shorter than the prefix: each split's
+    // block-table window must fit the LDS copy for either.
     const int suffix_max = std::max(max_seq_len - prefix.len, 1);
-    const int min_sp = min_splits_for_table(suffix_max, bs);
+    const int min_sp = min_splits_for_table(std::max(suffix_max, std::min(prefix.len, max_seq_len)), bs);
     int span = kMinSpan;
     if (num_splits <= 0) {
         num_splits = std::max(default_splits(suffix_max, batch, nkv), min_sp);

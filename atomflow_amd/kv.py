@@ -508,15 +508,21 @@ class Scheduler:
         }
 
 
-def decode_share_segments(groups, rows, min_members=2, min_saved_rows=0):
+# Rows a share group must save per launch, (members - 1) x shared rows, before
+# its own launch pair pays: the prefix launch and the second decode cost about
+# as much as reading 10-12k KV rows of 8 heads x 128 on MI355X.
+SHARE_MIN_SAVED_ROWS = 10240
+
+
+def decode_share_segments(groups, rows, min_members=2, min_saved_rows=SHARE_MIN_SAVED_ROWS):
     """Orders a decode batch by share group (Scheduler.step's decode_share_groups /
     decode_share_rows) for one attention launch per segment.
 
     A group qualifies with at least ``min_members`` entries this step whose
     shared rows are read ``(members - 1) * rows >= min_saved_rows`` fewer times
-    when attended once (a group's own launches cost about as much as reading
-    10-12k KV rows of 8 heads x 128 on MI355X, so smaller groups run faster in
-    the batch's plain launch).
+    when attended once (default SHARE_MIN_SAVED_ROWS: smaller groups run faster
+    in the batch's plain launch; 0 sends every group of ``min_members`` through
+    its own launch pair).
 
     Returns (order, segments): ``order`` permutes the decode entries so that
     entries without a qualifying group come first, then each group's entries
@@ -530,21 +536,20 @@ def decode_share_segments(groups, rows, min_members=2, min_saved_rows=0):
     if len(groups) != len(rows):
         raise ValueError("groups and rows differ in length")
     ids, counts = np.unique(groups[groups >= 0], return_counts=True)
-    big = set()
+    big = {}
     for g, c in zip(ids, counts):
-        shared = int(rows[groups == g][0])
-        if c >= min_members and (c - 1) * shared >= min_saved_rows:
-            big.add(int(g))
+        shared = np.unique(rows[groups == g])
+        if len(shared) != 1:
+            raise ValueError(f"group {g} has differing shared rows {shared.tolist()}")
+        if c >= min_members and (c - 1) * int(shared[0]) >= min_saved_rows:
+            big[int(g)] = int(shared[0])
     solo = [i for i, g in enumerate(groups) if int(g) not in big]
     order, segments = list(solo), []
     if solo:
         segments.append((0, len(solo), 0))
     for g in sorted(big):
         members = [i for i, x in enumerate(groups) if int(x) == g]
-        shared = {int(rows[i]) for i in members}
-        if len(shared) != 1:
-            raise ValueError(f"group {g} has differing shared rows {sorted(shared)}")
-        segments.append((len(order), len(members), shared.pop()))
+        segments.append((len(order), len(members), big[g]))
         order += members
     return np.array(order, np.int64), segments
 
@@ -556,6 +561,7 @@ def _nonneg(r, what):
 
 
 __all__ = [
+    "SHARE_MIN_SAVED_ROWS",
     "AF_KV_FP16", "AF_KV_FP8_E4M3", "AttentionWorkspace", "BlockManager", "build_rope_cache",
     "decode_share_segments", "default_splits", "fp8_quantize", "kv_copy_blocks", "launch_cached_attention",
     "launch_cached_attention_ex", "launch_decode_attention_fused", "launch_paged_attention",

@@ -508,8 +508,9 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
     With shared_prefix > 0 every arriving prompt starts with the same shared_prefix
     tokens and the scheduler's prefix cache is on (4 entries). With group_decode the
     decode batch is ordered by the plan's share groups (kv.decode_share_segments) and
-    each group of two or more sequences is attended through the shared-prefix entry
-    (its prompt prefix read once per layer), the other sequences by one plain launch."""
+    each group that saves at least kv.SHARE_MIN_SAVED_ROWS row reads is attended
+    through the shared-prefix entry (its prompt prefix read once per layer), the
+    other sequences by one plain launch."""
     import atomflow_amd
     r = np.random.Generator(np.random.PCG64(0xA70F10 + 6))
     bs, chunk, budget, max_running = 16, 512, 2048, 64

@@ -226,7 +226,10 @@ int af_paged_decode_fused(void* qkv_out, int batch, const af_kv_pool* pool, int 
  * The prefix is attended once for the whole batch on the matrix cores (one
  * launch, prefix_splits key ranges; 0 = default), the per-sequence rows
  * [prefix_len, L) by the split-K decode kernel, whose combine merges both.
- * head_dim 128. A sequence with L <= prefix_len attends the prefix only.
+ * head_dim 128. A sequence with L == prefix_len attends the prefix records
+ * alone; one with L < prefix_len attends its own rows [0, L) through its table
+ * and leaves the prefix records out, so every L gets af_paged_attention's
+ * result (rows [0, L) of its table must then hold the prefix's first L rows).
  * Workspace: af_attention_workspace_size(batch, ..., num_splits +
  * prefix_splits); one sized with num_splits = 0 (the maximum) always fits.
  * No counterpart entry in the reference (an optimisation of the same op). */

@@ -177,7 +177,8 @@ def test_scheduler_prefix_cache_drives_paged_kernels(gpu):
             # the same batch grouped by the plan's share groups: each group's prefix
             # through the shared-prefix entry (lone members too on odd steps)
             order, segs = kv.decode_share_segments(a["decode_share_groups"],
-                                                   a["decode_share_rows"], 1 + steps % 2)
+                                                   a["decode_share_rows"], 1 + steps % 2,
+                                                   min_saved_rows=0)
             q_perm = up(d_qkv.download(np.float16, (nd, QKV))[order])
             t_perm, l_perm = up(tables[order]), up(lens[order])
             d_g = dev.DeviceBuffer(nd * Q_DIM * 2)

@@ -251,6 +251,40 @@ def test_shared_prefix_configs3_shape(gpu):
         assert_attn_close(got[i], ref, what=f"seq {i} L={lens[i]}")
 
 
+@pytest.mark.parametrize("fp8,splits", [(False, 0), (False, 1), (False, 3), (True, 0)])
+def test_shared_prefix_lengths_below_prefix(gpu, fp8, splits):
+    """Sequences no longer than prefix_len (a stale or too-long prefix_len): one
+    with L < prefix_len attends its own rows [0, L) and leaves the prefix records
+    out; L == prefix_len attends the prefix records alone. Each equals the oracle
+    on its table and length, and af_paged_attention on the same inputs."""
+    say(f"shared prefix, lengths below the prefix, fp8={fp8} splits={splits}")
+    prefix = 640
+    P, bm, seqs, tables, lens_all, max_blocks = forked_batch(
+        prefix, [0, 5, 100, 400, 0, 1, 2, 3, 4], 16, 2, fp8, 0x6100 + splits)
+    lens = np.array([1, 645, 17, 1040, 639, 640, 300, 64, 65], np.int32)
+    assert np.all(lens <= lens_all)  # every row attended is mapped by the table
+    B = len(seqs)
+    q = randn_f16((B, Q_DIM), 0x6101 + splits)
+    d_q, d_t, d_l, d_root = up(q), up(tables), up(lens), up(tables[0])
+    o_c, o_p = dev.DeviceBuffer(B * Q_DIM * 2), dev.DeviceBuffer(B * Q_DIM * 2)
+    ws = kv.AttentionWorkspace(B, NQ, NKV, HD, 0)
+    max_len = int(lens.max())
+    kw = {"atol": ATOL_FP8, "rtol": RTOL_FP8} if fp8 else {}  # the oracle bar for FP8 KV
+    for layer in range(2):
+        kv.launch_paged_attention_shared_prefix(d_q, Q_DIM, P.desc, layer, d_root, prefix, d_t,
+                                                max_blocks, d_l, B, max_len, o_c, Q_DIM, NQ, ws,
+                                                num_splits=splits)
+        kv.launch_paged_attention(d_q, Q_DIM, P.desc, layer, d_t, max_blocks, d_l, B, max_len,
+                                  o_p, Q_DIM, NQ, ws)
+        got = o_c.download(np.float16, (B, Q_DIM))
+        plain = o_p.download(np.float16, (B, Q_DIM))
+        for b in range(B):
+            ref = P.reference(q[b], layer, tables[b], int(lens[b]))
+            assert_attn_close(got[b], ref, what=f"layer {layer} seq {b} L={lens[b]}", **kw)
+            assert_attn_close(got[b], plain[b].astype(np.float64),
+                              what=f"vs af_paged_attention, layer {layer} seq {b}")
+
+
 def test_shared_prefix_graph_replays(gpu):
     """Both launches captured in one hipGraph: three replays equal the eager call."""
     say("shared prefix under graph replay")

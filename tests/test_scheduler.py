@@ -242,13 +242,19 @@ def test_decode_share_segments():
     group or a lone member first (plain attention), then each group together."""
     groups = [-1, 3, 5, 3, -1, 7, 3, 5]
     rows = [0, 40, 100, 40, 0, 9, 40, 100]
-    order, segs = kv.decode_share_segments(groups, rows)
+    order, segs = kv.decode_share_segments(groups, rows, min_saved_rows=0)
     assert list(order) == [0, 4, 5, 1, 3, 6, 2, 7]
     assert segs == [(0, 3, 0), (3, 3, 40), (6, 2, 100)]
-    order, segs = kv.decode_share_segments(groups, rows, min_members=3)
+    order, segs = kv.decode_share_segments(groups, rows, min_members=3, min_saved_rows=0)
     assert list(order) == [0, 2, 4, 5, 7, 1, 3, 6] and segs == [(0, 5, 0), (5, 3, 40)]
-    order, segs = kv.decode_share_segments([2, 2], [16, 16])
+    order, segs = kv.decode_share_segments([2, 2], [16, 16], min_saved_rows=0)
     assert list(order) == [0, 1] and segs == [(0, 2, 16)]
+    # the default threshold keeps small groups in the plain launch
+    order, segs = kv.decode_share_segments([2, 2], [16, 16])
+    assert list(order) == [0, 1] and segs == [(0, 2, 0)]
+    order, segs = kv.decode_share_segments([4] * 64, [4096] * 64)
+    assert segs == [(0, 64, 4096)]
+    assert kv.SHARE_MIN_SAVED_ROWS == 10240
     assert kv.decode_share_segments([], [])[1] == []
     # only groups that save enough row reads: group 3 saves 2 x 40, group 5 1 x 100
     order, segs = kv.decode_share_segments(groups, rows, min_saved_rows=81)
