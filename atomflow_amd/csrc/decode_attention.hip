@@ -15,7 +15,10 @@
 //    dealt round-robin over the 8 XCDs): the partials a head's combine reads
 //    were written through the same L2.
 //  * A token row of one head is 8 lanes x 16 B (fp16: two loads per lane, fp8:
-//    one): every load instruction reads whole 128-B lines. QK partial dots are
+//    one): every load instruction reads whole 128-B lines. FP8 workgroups take
+//    a pair of KV heads (lanes 0-7 of a 16-lane row one head, 8-15 the next),
+//    so each row read is 256 contiguous bytes: 128-B pieces 1 KB apart stream
+//    at ~0.66 of HBM peak on MI355X, 256-B pieces at ~0.75. QK partial dots are
 //    summed across the 8 lanes with three DPP adds; the softmax max is made
 //    wave-uniform per chunk so the accumulator rescale is a uniform branch.
 //  * fp32 online softmax (exp2 with log2(e) folded into the score scale), fp32
@@ -44,7 +47,7 @@ constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kThreads = kWaves * 64;  // 256
 constexpr int kLanesPerRow = 8;        // lanes that share one token row of one head
 constexpr int kRowsPerStep = 64 / kLanesPerRow;      // 8 tokens per wave row-step
-constexpr int kStepTokens = kWaves * kRowsPerStep;   // 64 tokens per workgroup step
+constexpr int kStepTokens = kWaves * kRowsPerStep;   // 32 tokens per workgroup step (one KV head)
 constexpr int kMaxTableLds = 1024;     // block-table entries staged per split
 constexpr int kRingBudget = 126;       // VGPRs shared by the row ring and the accumulators
 constexpr float kLazyLog2 = 8.0f;      // running-max slack before a rescale (log2 units)
@@ -159,44 +162,56 @@ __device__ __forceinline__ uint64_t load_agent_u64(const float* p) {
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One workgroup = (sequence b, KV head h, split). See the file comment.
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED>
-__global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a) {
+// One workgroup = (sequence b, KV head h, split), or with PAIR (sequence b,
+// KV heads 2hw and 2hw+1, split): then GQ = 2 GROUP query heads share the
+// workgroup's records, merge and combine. See the file comment.
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
+__device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
     constexpr int EPL = LY::kEpl;
-    constexpr int GHD = GROUP * HD;
+    constexpr int KVH = PAIR ? 2 : 1;          // KV heads per workgroup
+    constexpr int GQ = GROUP * KVH;            // query heads per workgroup
+    constexpr int GHD = GQ * HD;               // output / record width of the workgroup
+    constexpr int LANES_ROW = kLanesPerRow * KVH;
+    constexpr int ROWS_WAVE = 64 / LANES_ROW;  // token rows per wave row-step
+    constexpr int STEP = kWaves * ROWS_WAVE;   // token rows per workgroup step
+    constexpr int kParts = PAIR ? kWaves : 4 * kWaves;  // partials per head staged in LDS
+    constexpr int V16 = LY::kRowBytes / 16;    // 16-B pieces of one head's row
     // Row-steps in flight per lane: as many as fit beside the accumulators.
     constexpr int kRowRegs = 2 * LOADS * 4;
     constexpr int kFree = kRingBudget - GROUP * (EPL + EPL / 2 + 2);
     constexpr int NB = kFree / kRowRegs < 2 ? 2 : (kFree / kRowRegs > 8 ? 8 : kFree / kRowRegs);
 
-    __shared__ __align__(16) float s_acc[4 * kWaves][GHD];  // per-row partial o of every wave
-    __shared__ float s_pm[4 * kWaves][GROUP];
-    __shared__ float s_pl[4 * kWaves][GROUP];
+    __shared__ __align__(16) float s_acc[kParts][GHD];  // partial o of every row group / wave
+    __shared__ float s_pm[kParts][GQ];
+    __shared__ float s_pl[kParts][GQ];
     __shared__ int32_t s_tab[PAGED ? kMaxTableLds : 1];
-    __shared__ float s_ml[2 * GROUP * kMaxSplits];  // (m, l) of every split
-    __shared__ __align__(16) float s_wt[GROUP][kMaxSplits];
+    __shared__ float s_ml[2 * GQ * kMaxSplits];  // (m, l) of every split
+    __shared__ __align__(16) float s_wt[GQ][kMaxSplits];
     __shared__ uint16_t s_q[FUSED ? GHD : 1];
-    __shared__ uint4 s_new[FUSED ? 2 * LY::kRowBytes / 16 : 1];  // new token's K then V row (head h)
+    __shared__ uint4 s_new[FUSED ? KVH * 2 * V16 : 1];  // new token's K then V row, per KV head
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 3, j = lane & 7;
+    const int g = lane / LANES_ROW, j = lane & 7;
+    const int sub = PAIR ? (lane >> 3) & 1 : 0;  // which KV head of the pair this lane reads
+    const int nkv = a.n_kv_heads;
+    const int nhw = nkv / KVH;  // workgroups per (sequence, split)
     int id = blockIdx.x;
-    const int h = id % a.n_kv_heads;
-    id /= a.n_kv_heads;
+    const int hw = id % nhw;
+    id /= nhw;
     const int split = id % a.num_splits;
     const int b = id / a.num_splits;
-    const int nkv = a.n_kv_heads;
+    const int h = hw * KVH + sub;  // this lane's KV head
 
     int L, pos = 0;
     if constexpr (FUSED) {
         pos = a.positions ? a.positions[b] : a.pos_host;
         const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
         if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
-            if (tid == 0 && split == 0 && h == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
+            if (tid == 0 && split == 0 && hw == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
             return;  // out-of-range append: nothing is written
         }
         L = pos + 1;
@@ -204,14 +219,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
         L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
         L = min(L, a.max_seq_len);
     }
-    uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(h) * GHD;
+    uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
     if (L <= 0) {  // empty sequence: defined as a zero output
         if (split == 0)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
     // Balanced partition of rows [t_lo, L) in whole workgroup steps
-    // (kStepTokens rows): C steps use n = min(num_splits, ceil(C / span)) splits
+    // (STEP rows): C steps use n = min(num_splits, ceil(C / span)) splits
     // and split s owns steps [s*C/n, (s+1)*C/n). t_lo = row_start, the first row
     // after a shared prefix (0 without one). A sequence exactly as long as the
     // prefix gets one split over its last row with every row masked (an empty
@@ -221,14 +236,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     const bool below_prefix = L < a.row_start;
     const int pre_used = below_prefix ? 0 : a.pre_records;  // prefix records this (b, h) merges
     const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
-    const int total_steps = (L - t_lo + kStepTokens - 1) / kStepTokens;
-    const int span_steps = max(1, a.span_tokens / kStepTokens);
+    const int total_steps = (L - t_lo + STEP - 1) / STEP;
+    const int span_steps = max(1, a.span_tokens / STEP);
     const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
     if (split >= n_active) return;
     const int step_begin = int(int64_t(split) * total_steps / n_active);
     const int step_end = int(int64_t(split + 1) * total_steps / n_active);
-    const int t_begin = t_lo + step_begin * kStepTokens;
-    const int t_end = min(L, t_lo + step_end * kStepTokens);
+    const int t_begin = t_lo + step_begin * STEP;
+    const int t_end = min(L, t_lo + step_end * STEP);
     const int t_valid = L == a.row_start ? t_begin : t_end;  // rows below t_valid are scored
     const int n_steps = step_end - step_begin;  // >= 1
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
@@ -257,7 +272,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // row clamp never leaves the split's staged block-table window.
     const int last_row = FUSED ? max(L - 2, t_begin) : L - 1;
     // Token of this lane in step s: waves interleave 8-row slices of each step.
-    const int lane_t0 = t_begin + wave * kRowsPerStep + g;
+    const int lane_t0 = t_begin + wave * ROWS_WAVE + g;
 
     struct Row {
         uint4 k[LOADS];
@@ -276,7 +291,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     };
 
     auto load_row = [&](Row& r, int step) {
-        const int64_t off = row_offset(lane_t0 + step * kStepTokens);
+        const int64_t off = row_offset(lane_t0 + step * STEP);
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             r.k[i] = *reinterpret_cast<const uint4*>(kbase + off + i * 128);
@@ -289,7 +304,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // set-up waits for is issued before the ring prologue, so that wait does
     // not also wait for the KV rows.
     constexpr int kQLoads = LOADS * (LY::kElemsPerLoad / 8);  // 16-B query loads per head
-    constexpr int kRopeItems = (GROUP + 1) * (HD / 2);        // Q pairs, then K pairs
+    constexpr int kHeadItems = (GROUP + 1) * (HD / 2);        // per KV head: Q pairs, then K pairs
+    constexpr int kRopeItems = KVH * kHeadItems;
     constexpr int RIT = (kRopeItems + kThreads - 1) / kThreads;
     uint16_t rx[RIT], ry[RIT];
     float rc[RIT], rs[RIT];
@@ -304,20 +320,21 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 #pragma unroll
         for (int r = 0; r < RIT; ++r) {
             const int it = tid + r * kThreads;
-            const int gh = it / half, d = it % half;
+            const int hh = hw * KVH + it / kHeadItems;  // the item's KV head
+            const int gh = (it % kHeadItems) / half, d = it % half;
             rx[r] = ry[r] = 0;
             rc[r] = rs[r] = 0.f;
             if (it < kRopeItems && (gh < GROUP || owner)) {
-                const uint16_t* src = qkv + size_t(gh < GROUP ? h * GROUP + gh : nq + h) * HD;
+                const uint16_t* src = qkv + size_t(gh < GROUP ? hh * GROUP + gh : nq + hh) * HD;
                 rx[r] = src[d];
                 ry[r] = src[d + half];
                 rc[r] = crow[d];
                 rs[r] = srow[d];
             }
         }
-        if (owner && tid < HD) vnew = qkv[size_t(nq + nkv + h) * HD + tid];
+        if (owner && tid < KVH * HD) vnew = qkv[size_t(nq + nkv + hw * KVH) * HD + tid];
     } else {
-        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
+        const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GROUP * HD;
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh)
 #pragma unroll
@@ -353,43 +370,45 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 #pragma unroll
         for (int r = 0; r < RIT; ++r) {
             const int it = tid + r * kThreads;
-            const int gh = it / half, d = it % half;
+            const int kv = it / kHeadItems, hh = hw * KVH + kv;
+            const int gh = (it % kHeadItems) / half, d = it % half;
             if (it >= kRopeItems || !(gh < GROUP || owner)) continue;
             uint16_t xo, yo;
             rope_rotate(rx[r], ry[r], rc[r], rs[r], xo, yo);
             if (gh < GROUP) {
-                s_q[gh * HD + d] = xo;
-                s_q[gh * HD + d + half] = yo;
+                s_q[(kv * GROUP + gh) * HD + d] = xo;
+                s_q[(kv * GROUP + gh) * HD + d + half] = yo;
             } else {
-                uint16_t* kh = a.q + size_t(b) * a.q_stride + size_t(nq + h) * HD;
-                kh[d] = xo;  // K is rotated in place (only this workgroup reads K head h)
+                uint16_t* kh = a.q + size_t(b) * a.q_stride + size_t(nq + hh) * HD;
+                kh[d] = xo;  // K is rotated in place (only this workgroup reads K head hh)
                 kh[d + half] = yo;
                 if constexpr (FP8) {
-                    uint8_t* kn = reinterpret_cast<uint8_t*>(s_new);
-                    kn[d] = uint8_t(quantize_fp8_dev(xo, a.scales[h]));
-                    kn[d + half] = uint8_t(quantize_fp8_dev(yo, a.scales[h]));
+                    uint8_t* kn = reinterpret_cast<uint8_t*>(s_new + kv * 2 * V16);
+                    kn[d] = uint8_t(quantize_fp8_dev(xo, a.scales[hh]));
+                    kn[d + half] = uint8_t(quantize_fp8_dev(yo, a.scales[hh]));
                 } else {
-                    uint16_t* kn = reinterpret_cast<uint16_t*>(s_new);
+                    uint16_t* kn = reinterpret_cast<uint16_t*>(s_new + kv * 2 * V16);
                     kn[d] = xo;
                     kn[d + half] = yo;
                 }
             }
         }
-        if (owner && tid < HD) {
+        if (owner && tid < KVH * HD) {
+            const int kv = tid / HD, e = tid % HD;
             if constexpr (FP8) {
-                reinterpret_cast<uint8_t*>(s_new)[LY::kRowBytes + tid] =
-                    uint8_t(quantize_fp8_dev(vnew, a.scales[nkv + h]));
+                reinterpret_cast<uint8_t*>(s_new + kv * 2 * V16)[LY::kRowBytes + e] =
+                    uint8_t(quantize_fp8_dev(vnew, a.scales[nkv + hw * KVH + kv]));
             } else {
-                reinterpret_cast<uint16_t*>(s_new)[HD + tid] = vnew;
+                reinterpret_cast<uint16_t*>(s_new + kv * 2 * V16)[HD + e] = vnew;
             }
         }
         __syncthreads();
-        if (owner) {  // append: K/V row of head h to the destination row
+        if (owner) {  // append: the K/V rows of the workgroup's heads to the destination row
             const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
-            constexpr int V16 = LY::kRowBytes / 16;
-            if (tid < 2 * V16) {
-                uint8_t* dst = (tid < V16 ? a.k : a.v) + row * a.row_bytes +
-                               size_t(h) * LY::kRowBytes + (tid % V16) * 16;
+            if (tid < KVH * 2 * V16) {
+                const int kv = tid / (2 * V16), r = tid % (2 * V16);
+                uint8_t* dst = (r < V16 ? a.k : a.v) + row * a.row_bytes +
+                               size_t(hw * KVH + kv) * LY::kRowBytes + (r % V16) * 16;
                 *reinterpret_cast<uint4*>(dst) = s_new[tid];
             }
         }
@@ -398,8 +417,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 #pragma unroll
             for (int sl = 0; sl < kQLoads; ++sl) {
                 const int i = sl / (LY::kElemsPerLoad / 8), w = sl % (LY::kElemsPerLoad / 8);
-                unpack_q(gh, sl,
-                         *reinterpret_cast<const uint4*>(&s_q[gh * HD + LY::dim(i, j, 0) + w * 8]));
+                unpack_q(gh, sl, *reinterpret_cast<const uint4*>(
+                                     &s_q[(sub * GROUP + gh) * HD + LY::dim(i, j, 0) + w * 8]));
             }
     } else {
 #pragma unroll
@@ -409,11 +428,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     }
 
     float qk_scale = a.qk_scale;
-    float v_scale = 1.0f;
-    if constexpr (FP8) {
-        qk_scale *= a.scales[h];
-        v_scale = a.scales[nkv + h];
-    }
+    if constexpr (FP8) qk_scale *= a.scales[h];
 
     float m_run[GROUP], l_run[GROUP], acc[GROUP][EPL];
 #pragma unroll
@@ -425,14 +440,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     }
 
     auto process_row = [&](Row& r, int step) {
-        const int t = lane_t0 + step * kStepTokens;
+        const int t = lane_t0 + step * STEP;
         if constexpr (FUSED) {
             // The new token (and padding past it) takes the appended row from LDS.
             if (t >= L - 1) {
 #pragma unroll
                 for (int i = 0; i < LOADS; ++i) {
-                    r.k[i] = s_new[(i * 128 + j * 16) / 16];
-                    r.v[i] = s_new[LY::kRowBytes / 16 + (i * 128 + j * 16) / 16];
+                    r.k[i] = s_new[sub * 2 * V16 + (i * 128 + j * 16) / 16];
+                    r.v[i] = s_new[sub * 2 * V16 + V16 + (i * 128 + j * 16) / 16];
                 }
             }
         }
@@ -539,42 +554,72 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             if (i < rem) process_row(ring[i], n_full * NB + i);
     }
 
-    // ---- merge: token-group pairs in registers, then the workgroup in LDS ---
-    // Lanes i and i+8 of a 16-lane row hold token groups g, g^1 with the same
-    // head-dim slice; one row_ror:8 DPP add merges the pair onto its larger
-    // reference. Lanes 0..7 of each row then hold one partial (m, l, o[]) and
-    // the kParts = 4 * kWaves partials per head are summed through LDS.
-    constexpr int kParts = 4 * kWaves;
+    // ---- merge: token groups in registers, then the workgroup in LDS -------
+    if constexpr (!PAIR) {
+        // Lanes i and i+8 of a 16-lane row hold token groups g, g^1 with the
+        // same head-dim slice; one row_ror:8 DPP add merges the pair onto its
+        // larger reference. Lanes 0..7 of each row then hold one partial
+        // (m, l, o[]) and the kParts = 4 * kWaves partials per head are summed
+        // through LDS.
 #pragma unroll
-    for (int gh = 0; gh < GROUP; ++gh) {
-        const float mp = fmaxf(m_run[gh], dpp<0x128>(m_run[gh]));
-        const float f = fast_exp2(m_run[gh] - mp);  // groups that saw no row hold l = acc = 0
-        const float l = l_run[gh] * f;
-        l_run[gh] = l + dpp<0x128>(l);
+        for (int gh = 0; gh < GROUP; ++gh) {
+            const float mp = fmaxf(m_run[gh], dpp<0x128>(m_run[gh]));
+            const float f = fast_exp2(m_run[gh] - mp);  // groups that saw no row hold l = acc = 0
+            const float l = l_run[gh] * f;
+            l_run[gh] = l + dpp<0x128>(l);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const float x = acc[gh][e] * f;
-            acc[gh][e] = x + dpp<0x128>(x);
+            for (int e = 0; e < EPL; ++e) {
+                const float x = acc[gh][e] * f;
+                acc[gh][e] = x + dpp<0x128>(x);
+            }
+            m_run[gh] = mp;
         }
-        m_run[gh] = mp;
-    }
-    {
-        const int part = wave * 4 + (lane >> 4);
-        if ((lane & 15) < kLanesPerRow) {
+    } else {
+        // The four 16-lane rows hold token groups 0..3 of both heads (lanes
+        // 0-7 / 8-15 of each row): merge rows 0+1 and 2+3 (v_permlane16_swap),
+        // then the halves (v_permlane32_swap). Every lane ends with the wave's
+        // partial for its head and head-dim slice.
+        auto merge_rows = [&](auto swap) {
 #pragma unroll
             for (int gh = 0; gh < GROUP; ++gh) {
+                uint32_t ma = __builtin_bit_cast(uint32_t, m_run[gh]), mb = ma;
+                swap(ma, mb);
+                const float m0 = __builtin_bit_cast(float, ma), m1 = __builtin_bit_cast(float, mb);
+                const float mp = fmaxf(m0, m1);
+                const float f0 = fast_exp2(m0 - mp), f1 = fast_exp2(m1 - mp);
+                uint32_t la = __builtin_bit_cast(uint32_t, l_run[gh]), lb = la;
+                swap(la, lb);
+                l_run[gh] = __builtin_bit_cast(float, la) * f0 + __builtin_bit_cast(float, lb) * f1;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    uint32_t xa = __builtin_bit_cast(uint32_t, acc[gh][e]), xb = xa;
+                    swap(xa, xb);
+                    acc[gh][e] = __builtin_bit_cast(float, xa) * f0 + __builtin_bit_cast(float, xb) * f1;
+                }
+                m_run[gh] = mp;
+            }
+        };
+        merge_rows([](uint32_t& x, uint32_t& y) { swap16(x, y); });
+        merge_rows([](uint32_t& x, uint32_t& y) { swap32(x, y); });
+    }
+    {
+        const int part = PAIR ? wave : wave * 4 + (lane >> 4);
+        if (PAIR ? lane < 16 : (lane & 15) < kLanesPerRow) {
+#pragma unroll
+            for (int gh = 0; gh < GROUP; ++gh) {
+                const int qh = sub * GROUP + gh;  // the workgroup's query head
 #pragma unroll
                 for (int i = 0; i < LOADS; ++i)
 #pragma unroll
                     for (int u = 0; u < LY::kElemsPerLoad; u += 4)
-                        *reinterpret_cast<float4*>(&s_acc[part][gh * HD + LY::dim(i, j, u)]) =
+                        *reinterpret_cast<float4*>(&s_acc[part][qh * HD + LY::dim(i, j, u)]) =
                             make_float4(acc[gh][i * LY::kElemsPerLoad + u],
                                         acc[gh][i * LY::kElemsPerLoad + u + 1],
                                         acc[gh][i * LY::kElemsPerLoad + u + 2],
                                         acc[gh][i * LY::kElemsPerLoad + u + 3]);
                 if (j == 0) {
-                    s_pm[part][gh] = m_run[gh];
-                    s_pl[part][gh] = l_run[gh];
+                    s_pm[part][qh] = m_run[gh];
+                    s_pl[part][qh] = l_run[gh];
                 }
             }
         }
@@ -583,10 +628,13 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 
     // ---- merge the partials: the output, or this split's partial ------------
     // Thread t owns head-dim pair (2t, 2t+1).
-    const size_t rec = (size_t(b) * nkv + h) * a.rec_stride;  // first record of (b, h)
+    const size_t rec = (size_t(b) * nhw + hw) * a.rec_stride;  // first record of (b, hw)
     const size_t own = rec + a.pre_records + split;            // this split's record
     for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
         const int gh = (2 * q2) / HD;
+        // V scale of the KV head that query head gh reads (not this lane's head:
+        // with pairs, thread t may merge the other head's output)
+        const float v_scale = FP8 ? a.scales[nkv + hw * KVH + gh / GROUP] : 1.0f;
         float M = -INFINITY;
 #pragma unroll
         for (int p = 0; p < kParts; ++p) M = fmaxf(M, s_pm[p][gh]);
@@ -609,14 +657,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
             __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_o + own * GHD) + q2, v,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if ((2 * q2) % HD == 0) {
-                store_agent(a.part_ml + own * 2 * GROUP + gh, M);
-                store_agent(a.part_ml + own * 2 * GROUP + GROUP + gh, lsum);
+                store_agent(a.part_ml + own * 2 * GQ + gh, M);
+                store_agent(a.part_ml + own * 2 * GQ + GQ + gh, lsum);
             }
         }
     }
     if (direct) {
-        if constexpr (FUSED) {  // the only reader of Q heads h*GROUP.. : rotate in place now
-            uint16_t* qd = a.q + size_t(b) * a.q_stride + size_t(h) * GHD;
+        if constexpr (FUSED) {  // the only reader of these Q heads: rotate in place now
+            uint16_t* qd = a.q + size_t(b) * a.q_stride + size_t(hw) * GHD;
             for (int o = tid; o < GHD; o += kThreads) qd[o] = s_q[o];
         }
         return;
@@ -648,7 +696,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        uint32_t* ctr = a.counters + size_t(b) * nkv + h;
+        uint32_t* ctr = a.counters + size_t(b) * nhw + hw;
         const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         const int last = prev == uint32_t(n_active - 1);
@@ -665,11 +713,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     // waits on them; the split weights are computed while the batch is in
     // flight.
     constexpr int CB = 16;  // splits per batch
-    constexpr int MLPT = (2 * GROUP * kMaxSplits + kThreads - 1) / kThreads;
+    constexpr int MLPT = (2 * GQ * kMaxSplits + kThreads - 1) / kThreads;
     const int n_rec = pre_used + n_active;  // shared-prefix records, then the splits'
-    const int n_ml = n_rec * 2 * GROUP;
+    const int n_ml = n_rec * 2 * GQ;
     const size_t rec0 = rec + (a.pre_records - pre_used);  // first record merged
-    const float* ml = a.part_ml + rec0 * 2 * GROUP;
+    const float* ml = a.part_ml + rec0 * 2 * GQ;
     const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + rec0 * GHD);
     float mlv[MLPT];
 #pragma unroll
@@ -692,16 +740,16 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
     }
     __syncthreads();
     // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s, one wave per head
-    for (int gh = wave; gh < GROUP; gh += kWaves) {
+    for (int gh = wave; gh < GQ; gh += kWaves) {
         float mx = -INFINITY;
-        for (int sp = lane; sp < n_rec; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GROUP + gh]);
+        for (int sp = lane; sp < n_rec; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GQ + gh]);
         mx = wave_max(mx);
         float ls = 0.f;
         for (int sp = lane; sp < n_rec; sp += 64)
-            ls += fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * s_ml[sp * 2 * GROUP + GROUP + gh];
+            ls += fast_exp2(s_ml[sp * 2 * GQ + gh] - mx) * s_ml[sp * 2 * GQ + GQ + gh];
         const float inv = 1.0f / wave_sum(ls);
         for (int sp = lane; sp < n_rec; sp += 64)
-            s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GROUP + gh] - mx) * inv;
+            s_wt[gh][sp] = fast_exp2(s_ml[sp * 2 * GQ + gh] - mx) * inv;
     }
     __syncthreads();
     for (int q2 = tid; q2 < GHD / 2; q2 += kThreads) {
@@ -727,9 +775,22 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
                               (uint32_t(__builtin_bit_cast(uint16_t, f16(r1))) << 16);
         *reinterpret_cast<uint32_t*>(out_b + 2 * q2) = pair;
         if constexpr (FUSED)
-            *reinterpret_cast<uint32_t*>(a.q + size_t(b) * a.q_stride + size_t(h) * GHD + 2 * q2) =
+            *reinterpret_cast<uint32_t*>(a.q + size_t(b) * a.q_stride + size_t(hw) * GHD + 2 * q2) =
                 *reinterpret_cast<const uint32_t*>(&s_q[2 * q2]);
     }
+}
+
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
+__global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a) {
+    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR>(a);
+}
+
+// The fused pair form holds the RoPE inputs of two KV heads across the ring
+// prologue; asking for three workgroups per CU keeps it at 3 waves per SIMD
+// (168 VGPRs, no spills for GROUP <= 4) where it would otherwise take 178.
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
+__global__ __launch_bounds__(kThreads, 3) void decode_attn_kernel_3wg(const AttnArgs a) {
+    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR>(a);
 }
 
 }  // namespace
@@ -741,23 +802,33 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 namespace af {
 namespace {
 
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED>
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR = false>
 hipError_t launch_attn(const AttnArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED, FUSED>), dim3(grid),
-                       dim3(kThreads), 0, s, a);
+    if constexpr (FUSED && PAIR && GROUP <= 4)
+        hipLaunchKernelGGL((decode_attn_kernel_3wg<HD, GROUP, FP8, PAGED, FUSED, PAIR>), dim3(grid),
+                           dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED, FUSED, PAIR>), dim3(grid),
+                           dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
-template <int HD, bool FP8, bool PAGED, bool FUSED>
+template <int HD, bool FP8, bool PAGED, bool FUSED, bool PAIR = false>
 int dispatch_group(const AttnArgs& a, int group, int grid, hipStream_t s) {
     switch (group) {
-        case 1: return int(launch_attn<HD, 1, FP8, PAGED, FUSED>(a, grid, s));
-        case 2: return int(launch_attn<HD, 2, FP8, PAGED, FUSED>(a, grid, s));
-        case 3: return int(launch_attn<HD, 3, FP8, PAGED, FUSED>(a, grid, s));
-        case 4: return int(launch_attn<HD, 4, FP8, PAGED, FUSED>(a, grid, s));
-        case 8: return int(launch_attn<HD, 8, FP8, PAGED, FUSED>(a, grid, s));
+        case 1: return int(launch_attn<HD, 1, FP8, PAGED, FUSED, PAIR>(a, grid, s));
+        case 2: return int(launch_attn<HD, 2, FP8, PAGED, FUSED, PAIR>(a, grid, s));
+        case 3: return int(launch_attn<HD, 3, FP8, PAGED, FUSED, PAIR>(a, grid, s));
+        case 4: return int(launch_attn<HD, 4, FP8, PAGED, FUSED, PAIR>(a, grid, s));
+        case 8: return int(launch_attn<HD, 8, FP8, PAGED, FUSED, PAIR>(a, grid, s));
         default: return AF_ERR_UNSUPPORTED;
     }
+}
+
+// FP8 launches without shared-prefix records take KV heads in pairs (the
+// prefix launch writes records per single KV head).
+bool pair_heads(bool fp8, const AttnArgs& a) {
+    return fp8 && a.pre_records == 0 && a.n_kv_heads % 2 == 0;
 }
 
 template <bool FUSED>
@@ -765,6 +836,7 @@ int dispatch_fused(const AttnArgs& a, int head_dim, int group, bool fp8, bool pa
                    hipStream_t s) {
     if (fp8) {
         if (!paged || head_dim != 128) return AF_ERR_UNSUPPORTED;
+        if (pair_heads(fp8, a)) return dispatch_group<128, true, true, FUSED, true>(a, group, grid / 2, s);
         return dispatch_group<128, true, true, FUSED>(a, group, grid, s);
     }
     if (head_dim == 128)

@@ -1,0 +1,117 @@
+// read_probe.hip — streaming-read probes for gfx950: HBM read rates with no
+// compute and no stores, the per-launch ceiling the attention kernels are
+// measured against. Two access patterns:
+//  * read_contiguous: workgroup w reads one contiguous chunk (the best case);
+//  * read_head_rows<SEG>: the decode-attention kernel's pattern without its
+//    arithmetic. Two slabs (K, V) of rows of row_bytes; workgroup (split s,
+//    segment g) reads bytes [g*SEG, (g+1)*SEG) of rows [s*span, (s+1)*span) of
+//    both slabs, 8 lanes x 16 B per 128 B, 8 rows per wave and 32 rows per
+//    workgroup step, as decode_attn_kernel does for one KV head (SEG 256: fp16,
+//    SEG 128: FP8, head_dim 128).
+// Each lane folds what it loads into one word and writes it to the sink only
+// when it equals a fixed constant, so the compiler keeps every load; the sink
+// is a valid device word either way.
+#include "af_common.h"
+#include "af_runtime.h"
+
+namespace af {
+namespace {
+
+constexpr int kProbeThreads = 256;
+constexpr int kProbeDepth = 4;  // 16-B loads per lane in flight
+constexpr uint32_t kNever = 0x9E3779B9u;
+
+__device__ __forceinline__ uint32_t fold(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+
+__global__ __launch_bounds__(kProbeThreads) void read_contiguous(const uint4* __restrict__ p,
+                                                                 size_t n16, size_t chunk,
+                                                                 uint32_t* sink) {
+    const size_t b = size_t(blockIdx.x) * chunk;
+    const size_t e = min(n16, b + chunk);
+    uint32_t x = 0;
+    for (size_t i = b + threadIdx.x; i < e; i += size_t(kProbeThreads) * kProbeDepth) {
+        uint4 a[kProbeDepth];
+#pragma unroll
+        for (int k = 0; k < kProbeDepth; ++k) a[k] = p[min(i + size_t(k) * kProbeThreads, e - 1)];
+#pragma unroll
+        for (int k = 0; k < kProbeDepth; ++k) x ^= fold(a[k]);
+    }
+    if (x == kNever) sink[0] = x;
+}
+
+template <int SEG>
+__global__ __launch_bounds__(kProbeThreads) void read_head_rows(const uint8_t* __restrict__ k_slab,
+                                                                const uint8_t* __restrict__ v_slab,
+                                                                int rows, int row_bytes,
+                                                                int n_seg, int splits,
+                                                                uint32_t* sink) {
+    constexpr int kPieces = SEG / 128;  // 128-B pieces per head row (8 lanes x 16 B each)
+    const int g = blockIdx.x % n_seg;
+    const int s = blockIdx.x / n_seg;
+    const int span = (rows + splits - 1) / splits;
+    const int t0 = s * span;
+    const int t1 = min(rows, t0 + span);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t off = size_t(g) * SEG + (lane & 7) * 16;
+    const int row_in_step = wave * 8 + (lane >> 3);
+    uint32_t x = 0;
+    for (int base = t0; base < t1; base += 32 * kProbeDepth) {
+        uint4 a[kProbeDepth][2 * kPieces];
+#pragma unroll
+        for (int k = 0; k < kProbeDepth; ++k) {
+            const int t = min(base + 32 * k + row_in_step, t1 - 1);
+            const uint8_t* kr = k_slab + size_t(t) * row_bytes + off;
+            const uint8_t* vr = v_slab + size_t(t) * row_bytes + off;
+#pragma unroll
+            for (int p = 0; p < kPieces; ++p) {
+                a[k][p] = *reinterpret_cast<const uint4*>(kr + 128 * p);
+                a[k][kPieces + p] = *reinterpret_cast<const uint4*>(vr + 128 * p);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kProbeDepth; ++k)
+#pragma unroll
+            for (int p = 0; p < 2 * kPieces; ++p) x ^= fold(a[k][p]);
+    }
+    if (x == kNever) sink[0] = x;
+}
+
+}  // namespace
+}  // namespace af
+
+using namespace af;
+
+extern "C" int af_rt_read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
+                                int row_bytes, uint32_t* d_sink, af_stream_t stream) {
+    if (!src || !d_sink || workgroups <= 0 || bytes == 0) return AF_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(src) & 15u) return AF_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (segment_bytes == 0) {
+        if (bytes % 16) return AF_ERR_INVALID_ARG;
+        const size_t n16 = bytes / 16;
+        const size_t chunk = (n16 + workgroups - 1) / size_t(workgroups);
+        hipLaunchKernelGGL(read_contiguous, dim3(workgroups), dim3(kProbeThreads), 0, s,
+                           static_cast<const uint4*>(src), n16, chunk, d_sink);
+        AF_TRY_LAUNCH();
+        return AF_OK;
+    }
+    if (segment_bytes != 128 && segment_bytes != 256) return AF_ERR_UNSUPPORTED;
+    if (row_bytes <= 0 || row_bytes % segment_bytes) return AF_ERR_INVALID_ARG;
+    const size_t slab = bytes / 2;
+    if (bytes % 2 || slab % size_t(row_bytes)) return AF_ERR_INVALID_ARG;
+    if (slab / size_t(row_bytes) > size_t(INT32_MAX - 32 * kProbeDepth)) return AF_ERR_UNSUPPORTED;
+    const int rows = int(slab / size_t(row_bytes));
+    const int n_seg = row_bytes / segment_bytes;
+    if (workgroups % n_seg) return AF_ERR_INVALID_ARG;
+    const int splits = workgroups / n_seg;
+    const uint8_t* k = static_cast<const uint8_t*>(src);
+    const uint8_t* v = k + slab;
+    if (segment_bytes == 256)
+        hipLaunchKernelGGL(read_head_rows<256>, dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
+                           rows, row_bytes, n_seg, splits, d_sink);
+    else
+        hipLaunchKernelGGL(read_head_rows<128>, dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
+                           rows, row_bytes, n_seg, splits, d_sink);
+    AF_TRY_LAUNCH();
+    return AF_OK;
+}

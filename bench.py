@@ -76,6 +76,9 @@ def parse():
                     help="run only the fan-out decode measurement and print its JSON object")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="run only the streaming-read probes (per-launch read ceilings of each "
+                         "workload's bytes) and print their JSON object")
     return ap.parse_args()
 
 
@@ -1191,6 +1194,60 @@ def bench_matrix(args, dev, kv, lib, info, headline):
     return m
 
 
+# (name, bytes per launch, layers rotated, head-row bytes, segment bytes): the
+# attention kernel's bytes per launch for each BASELINE workload, rotated over
+# enough layers that the 256 MB MALL does not serve re-reads.
+READ_PROBE_WORKLOADS = [
+    ("configs[1] ctx 8192", 8193 * 2 * 2048, 28, 2048, 256),
+    ("configs[1] ctx 32768", 32769 * 2 * 2048, 12, 2048, 256),
+    ("configs[2] (549 MB)", 134104 * 2 * 2048, 4, 2048, 256),
+    ("configs[4] (3.25 GB, FP8 rows)", 1585518 * 2 * 1024, 2, 1024, 128),
+]
+
+
+def bench_read_probe(args, dev):
+    """Streaming-read ceilings (af_rt_read_probe): for each workload's bytes per
+    launch, the median time of a launch that only reads them, over a sweep of
+    workgroup counts, for contiguous chunks and for the decode kernel's head-row
+    access pattern. Times are per launch from graphs of `layers` launches, each
+    on its own region."""
+    stream = dev.Stream()
+    sink = dev.DeviceBuffer(256)
+    t = Timer(dev, stream, args.warmup)
+    out = {}
+    for name, nbytes, layers, row_bytes, seg in READ_PROBE_WORKLOADS:
+        log(f"read probe: {name}, {nbytes} B per launch x {layers} regions ...")
+        buf = dev.DeviceBuffer(nbytes * layers)
+        buf.fill_u32(0x3C003C00, stream)
+        n_seg = row_bytes // seg
+        entry = {"bytes_per_launch": nbytes, "regions": layers, "contiguous_us": {},
+                 "head_rows_us": {}, "head_row_bytes": row_bytes, "segment_bytes": seg}
+        for kind, grid in (("contiguous_us", (256, 512, 1024, 2048, 4096, 8192)),
+                           ("head_rows_us", tuple(n_seg * sp for sp in (24, 32, 64, 128, 256, 512)))):
+            for g in grid:
+                def launches(g=g, kind=kind):
+                    for l in range(layers):
+                        if kind == "contiguous_us":
+                            dev.read_probe(buf.ptr + l * nbytes, nbytes, g, sink.ptr, stream=stream)
+                        else:
+                            dev.read_probe(buf.ptr + l * nbytes, nbytes, g, sink.ptr, seg,
+                                           row_bytes, stream=stream)
+                graph = dev.Graph.capture(stream, launches)
+                us = t.graph_ms(graph, args.steps) * 1e3 / layers
+                graph.destroy()
+                entry[kind][str(g)] = round(us, 3)
+        for kind in ("contiguous_us", "head_rows_us"):
+            g, us = min(entry[kind].items(), key=lambda kv_: kv_[1])
+            gbs = nbytes / (us * 1e-6) / 1e9
+            entry["best_" + kind[:-3]] = {"workgroups": int(g), "us": us, "gbs": round(gbs, 1),
+                                         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        out[name] = entry
+        buf.free()
+    sink.free()
+    stream.destroy()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1207,6 +1264,9 @@ def main():
     log(f"device {info}")
     if args.fanout_only:
         print(json.dumps({"serving_fanout": bench_fanout(dev, kv, lib)}), flush=True)
+        return
+    if args.read_probe:
+        print(json.dumps({"read_probe": bench_read_probe(args, dev)}), flush=True)
         return
     if args.config == 2:
         result = bench_contiguous(args, dev, kv, lib, info)

@@ -48,6 +48,16 @@ int af_rt_fill_randn_f16(void* dst, size_t n, uint64_t seed, float stddev, af_st
 /* Synthetic FP8 E4M3 codes of N(0,1)/scale values (bench-scale inputs). */
 int af_rt_fill_randn_fp8(uint8_t* dst, size_t n, uint64_t seed, float inv_scale, af_stream_t stream);
 
+/* Streaming-read probe, a measurement aid: reads `bytes` at src once (16-B
+ * loads, no compute) and writes at most one word of d_sink. segment_bytes 0:
+ * `workgroups` contiguous chunks (the read ceiling for a launch of this size).
+ * segment_bytes 256 (fp16) or 128 (FP8): the decode-attention kernel's access
+ * pattern for head_dim 128 without its arithmetic. src holds two equal slabs
+ * (K then V) of rows of row_bytes; workgroups = splits x (row_bytes /
+ * segment_bytes), each reading one head segment of one split's rows. */
+int af_rt_read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
+                     int row_bytes, uint32_t* d_sink, af_stream_t stream);
+
 int af_rt_stream_create(af_stream_t* stream);
 int af_rt_stream_destroy(af_stream_t stream);
 int af_rt_stream_sync(af_stream_t stream);
