@@ -1202,6 +1202,8 @@ READ_PROBE_WORKLOADS = [
     ("configs[1] ctx 32768", 32769 * 2 * 2048, 12, 2048, 256),
     ("configs[2] (549 MB)", 134104 * 2 * 2048, 4, 2048, 256),
     ("configs[4] (3.25 GB, FP8 rows)", 1585518 * 2 * 1024, 2, 1024, 128),
+    # the same rows read as 256-B pieces: two KV heads per workgroup (the FP8 pair form)
+    ("configs[4] (3.25 GB, FP8 rows, KV-head pairs)", 1585518 * 2 * 1024, 2, 1024, 256),
 ]
 
 
