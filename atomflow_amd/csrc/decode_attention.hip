@@ -181,7 +181,11 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     // Row-steps in flight per lane: as many as fit beside the accumulators.
     constexpr int kRowRegs = 2 * LOADS * 4;
     constexpr int kFree = kRingBudget - GROUP * (EPL + EPL / 2 + 2);
-    constexpr int NB = kFree / kRowRegs < 2 ? 2 : (kFree / kRowRegs > 8 ? 8 : kFree / kRowRegs);
+    constexpr int NB_FIT = kFree / kRowRegs < 2 ? 2 : (kFree / kRowRegs > 8 ? 8 : kFree / kRowRegs);
+    // FP8 consumes slots in pairs and is VALU-bound: 4 slots keep the paired
+    // fused form within 3 waves per SIMD. Fused and unfused kernels use the
+    // same NB, so both process the same rows in pairs (bit-identical results).
+    constexpr int NB = FP8 ? (NB_FIT > 4 ? 4 : NB_FIT) : NB_FIT;
 
     __shared__ __align__(16) float s_acc[kParts][GHD];  // partial o of every row group / wave
     __shared__ float s_pm[kParts][GQ];
@@ -439,7 +443,9 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         for (int e = 0; e < EPL; ++e) acc[gh][e] = 0.f;
     }
 
-    auto process_row = [&](Row& r, int step) {
+    // Scores of one row-step for the GROUP query heads (log2 units, masked rows
+    // -inf); the fused kernel first substitutes the appended row from LDS.
+    auto score_row = [&](Row& r, int step, float (&s)[GROUP]) {
         const int t = lane_t0 + step * STEP;
         if constexpr (FUSED) {
             // The new token (and padding past it) takes the appended row from LDS.
@@ -451,7 +457,6 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
                 }
             }
         }
-        float s[GROUP];
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh) s[gh] = 0.f;
 #pragma unroll
@@ -483,6 +488,11 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
             const float x = group8_sum(s[gh]) * qk_scale;
             s[gh] = valid ? x : -INFINITY;
         }
+    };
+
+    auto process_row = [&](Row& r, int step) {
+        float s[GROUP];
+        score_row(r, step, s);
         // Per-lane running max with a lazy rescale: the reference point only
         // moves when a score exceeds it by more than 2^kLazyLog2, so p <= 2^8
         // and the (rare) accumulator rescale replaces a cross-lane max per row.
@@ -532,6 +542,57 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         }
     };
 
+    // FP8: two row-steps at once. One lazy-max check covers both rows (the
+    // reference point still only moves past 2^kLazyLog2, so p <= 2^8), and P.V
+    // runs on v_dot2_f32_f16 across the two rows: a byte permute puts dimension
+    // e of both rows' V codes side by side, the FP8 -> f16 conversion is exact,
+    // and (p0, p1) are rounded to f16 (relative 2^-11). 72 VALU instructions
+    // per pair for V where two single rows take 112.
+    auto process_pair = [&](Row& r0, int step0, Row& r1, int step1) {
+        float s0[GROUP], s1[GROUP];
+        score_row(r0, step0, s0);
+        __builtin_amdgcn_sched_barrier(0);  // one row's K temporaries live at a time
+        score_row(r1, step1, s1);
+        __builtin_amdgcn_sched_barrier(0);
+        half2_t pp[GROUP];
+#pragma unroll
+        for (int gh = 0; gh < GROUP; ++gh) {
+            const float sm = fmaxf(s0[gh], s1[gh]);
+            if (sm > m_run[gh] + kLazyLog2) {
+                const float alpha = fast_exp2(m_run[gh] - sm);
+                l_run[gh] *= alpha;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[gh][e] *= alpha;
+                m_run[gh] = sm;
+            }
+            const float p0 = fast_exp2(s0[gh] - m_run[gh]);
+            const float p1 = fast_exp2(s1[gh] - m_run[gh]);
+            l_run[gh] += p0 + p1;
+            pp[gh] = half2_t{f16(p0), f16(p1)};
+        }
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t a4[4] = {r0.v[i].x, r0.v[i].y, r0.v[i].z, r0.v[i].w};
+            const uint32_t b4[4] = {r1.v[i].x, r1.v[i].y, r1.v[i].z, r1.v[i].w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                // bytes (r0.b0, r1.b0, r0.b1, r1.b1) and (r0.b2, r1.b2, r0.b3, r1.b3)
+                const uint32_t lo = __builtin_amdgcn_perm(a4[w], b4[w], 0x01050004u);
+                const uint32_t hi = __builtin_amdgcn_perm(a4[w], b4[w], 0x03070206u);
+                const half2_t d[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(lo), 1.0f, false),
+                                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(lo), 1.0f, true),
+                                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(hi), 1.0f, false),
+                                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(int(hi), 1.0f, true)};
+                const int e = i * 16 + w * 4;
+#pragma unroll
+                for (int gh = 0; gh < GROUP; ++gh)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        acc[gh][e + u] = __builtin_amdgcn_fdot2(pp[gh], d[u], acc[gh][e + u], false);
+            }
+        }
+    };
+
     // ---- main loop: a ring of NB row-steps per lane -------------------------
     // Each slot is consumed and refilled with the step NB ahead (past the end
     // the refill re-reads the split's last step, a cache hit). Whole rounds
@@ -539,15 +600,30 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     // the compiler waits only for the slot being consumed; the last partial
     // round is drained without refills.
     const int n_full = n_steps / NB;
-    for (int round = 0; round < n_full; ++round) {
+    if constexpr (FP8) {  // slots consumed and refilled two at a time
+        static_assert(NB % 2 == 0, "FP8 ring pairs slots");
+        for (int round = 0; round < n_full; ++round) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const int step = round * NB + i;
-            process_row(ring[i], step);
-            load_row(ring[i], min(step + NB, n_steps - 1));
+            for (int i = 0; i < NB; i += 2) {
+                const int step = round * NB + i;
+                process_pair(ring[i], step, ring[i + 1], step + 1);
+                load_row(ring[i], min(step + NB, n_steps - 1));
+                load_row(ring[i + 1], min(step + 1 + NB, n_steps - 1));
+            }
         }
-    }
-    {
+        const int rem = n_steps - n_full * NB;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)  // the drain row by row (a paired drain costs ~30 VGPRs)
+            if (i < rem) process_row(ring[i], n_full * NB + i);
+    } else {
+        for (int round = 0; round < n_full; ++round) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int step = round * NB + i;
+                process_row(ring[i], step);
+                load_row(ring[i], min(step + NB, n_steps - 1));
+            }
+        }
         const int rem = n_steps - n_full * NB;
 #pragma unroll
         for (int i = 0; i < NB; ++i)
