@@ -344,3 +344,68 @@ def test_paged_fused_equals_append_then_attention(gpu, fp8):
         assert np.array_equal(o1.download(np.uint16), o2.download(np.uint16)), layer
     assert np.array_equal(q1.download(np.uint16), q2.download(np.uint16))
     assert np.array_equal(P1.download().view(np.uint8), P2.download().view(np.uint8))
+
+
+@pytest.mark.parametrize("nq,nkv", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (6, 2), (9, 3),
+                                    (8, 1)])
+def test_paged_fp8_gqa_shapes(gpu, nq, nkv):
+    """FP8 attention over every supported GQA ratio (1, 2, 3, 4, 8): even KV-head counts run
+    the KV-head-pair kernel (GQ = 2 x GROUP query heads per workgroup), odd ones the single
+    head kernel. Each sequence against the oracle at the FP8 and the fp16 bar, and the
+    fused RoPE + append + attention kernel against append then attention bit for bit."""
+    say(f"paged fp8 gqa nq={nq} nkv={nkv}")
+    bs, layers = 32, 2
+    kv_dim, q_dim = nkv * HD, nq * HD
+    qkv_w = q_dim + 2 * kv_dim
+    lengths = [1, 32, 33, 200, 1500, 4000]
+    B = len(lengths)
+    total = sum(n // bs + 2 for n in lengths) + 3
+    bm = kv.BlockManager(total, bs, layers, dtype=AF_KV_FP8_E4M3)
+    ids = [bm.allocate_block() for _ in range(total)]
+    for blk in rng(790 + nq + nkv).permutation(ids):
+        bm.free_block(int(blk))
+    seqs = _sequences(bm, lengths)
+    r = rng(791 + nq)
+    shape = (layers, 2, total * bs, kv_dim)
+    host = r.integers(0, 256, shape, dtype=np.uint8)
+    host[(host & 0x7F) == 0x7F] = 0x00
+    scales = r.uniform(0.004, 0.02, (layers, 2, nkv)).astype(np.float32)
+    d_sc = up(scales)
+    bufs = [up(host), up(host)]
+    descs = [kv.make_pool(b, AF_KV_FP8_E4M3, bs, layers, nkv, HD, total, d_sc) for b in bufs]
+    max_blocks = max((n + 1 + bs - 1) // bs for n in lengths)
+    # attention over the current lengths, against the oracle
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    q = randn_f16((B, q_dim), 792 + nkv)
+    d_q, d_t, d_l = up(q), up(tables), up(lens)
+    d_o = dev.DeviceBuffer(B * q_dim * 2)
+    ws = kv.AttentionWorkspace(B, nq, nkv, HD, 0)
+    for layer in range(layers):
+        kv.launch_paged_attention(d_q, q_dim, descs[0], layer, d_t, max_blocks, d_l, B,
+                                  int(lens.max()), d_o, q_dim, nq, ws)
+        got = d_o.download(np.float16, (B, q_dim))
+        for b in range(B):
+            ref = oracle.paged_attention_fp8(q[b], host[layer, 0], host[layer, 1],
+                                             scales[layer, 0], scales[layer, 1], tables[b],
+                                             int(lens[b]), bs, nq, nkv, HD)
+            assert_attn_close(got[b], ref, ATOL_FP8, RTOL_FP8, what=f"layer {layer} seq {b}")
+            assert_attn_close(got[b], ref, what=f"layer {layer} seq {b} (fp16 bar)")
+    # one decode step: fused == paged append + attention, bit for bit
+    slots, positions, _ = bm.plan_decode(seqs)
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    max_pos = 4096
+    c, s = oracle.rope_table(max_pos, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    qkv = randn_f16((B, qkv_w), 793 + nq)
+    q1, q2 = up(qkv), up(qkv)
+    d_t, d_l, d_sl, d_p = up(tables), up(lens), up(slots), up(positions)
+    o1, o2 = dev.DeviceBuffer(B * q_dim * 2), dev.DeviceBuffer(B * q_dim * 2)
+    for layer in range(layers):
+        kv.launch_paged_rope_append(q1, B, descs[0], layer, d_sl, d_p, d_c, d_s, max_pos, nq)
+        kv.launch_paged_attention(q1, qkv_w, descs[0], layer, d_t, max_blocks, d_l, B,
+                                  int(lens.max()), o1, q_dim, nq, ws)
+        kv.launch_paged_decode_fused(q2, B, descs[1], layer, d_sl, d_p, d_c, d_s, max_pos, d_t,
+                                     max_blocks, int(lens.max()), o2, q_dim, nq, ws)
+        assert np.array_equal(o1.download(np.uint16), o2.download(np.uint16)), layer
+    assert np.array_equal(q1.download(np.uint16), q2.download(np.uint16))
+    assert np.array_equal(bufs[0].download(np.uint8), bufs[1].download(np.uint8))
