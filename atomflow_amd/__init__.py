@@ -26,6 +26,7 @@ AF_ERR_BAD_BLOCK = -5
 AF_ERR_WORKSPACE = -6
 AF_ERR_BAD_SEQUENCE = -7
 AF_ERR_BAD_FILE = -9
+AF_ERR_TIMEOUT = -10
 AF_KV_FP16 = 1
 AF_KV_FP8_E4M3 = 3
 

@@ -46,9 +46,12 @@ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Split-K buffers of the decode-attention kernels. Layout of a workspace:
-//   [0, kCounterBytes)           arrival counters, one per (sequence, KV head),
-//                                zero between launches (each launch re-zeroes
-//                                the counters it used)
+//   [0, kCounterBytes)           words [0, kMaxCounters): arrival counters, one
+//                                per (sequence, KV head); words [kFlagBase,
+//                                kFlagBase + kCombMaxGroups * kCombSplits):
+//                                ready flags of the dedicated-combiner form, one
+//                                per (sequence, KV head, split). All zero between
+//                                launches (each launch re-zeroes what it used)
 //   [kCounterBytes, ...)         part_ml [batch][n_kv_heads][splits][2 * group]
 //                                (group = n_q_heads / n_kv_heads: max..., sum...)
 //   then                         part_o  [batch][n_kv_heads][splits][group * head_dim]
@@ -56,10 +59,20 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // launches (each launch re-zeroes the counters it used), so one workspace
 // serves launches of any batch / split count without re-initialisation.
 constexpr size_t kCounterBytes = 64 * 1024;
-constexpr int kMaxCounters = int(kCounterBytes / sizeof(uint32_t));
+constexpr int kMaxCounters = int(kCounterBytes / sizeof(uint32_t)) / 2;
+constexpr int kFlagBase = kMaxCounters;
+// Dedicated-combiner form: the most splits per (sequence, KV head), and the
+// most (sequence, KV head) pairs of one launch (combiners are one workgroup
+// each, dispatched after every split, and stay few enough that they could never
+// hold every workgroup slot of the device).
+constexpr int kCombSplits = 32;
+constexpr int kCombMaxGroups = 16;
+static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= int(kCounterBytes / sizeof(uint32_t)),
+              "ready flags exceed the counter region");
 
 struct AttnWorkspace {
     uint32_t* counters;
+    uint32_t* flags;
     float* part_ml;
     float* part_o;
 };
@@ -74,6 +87,7 @@ inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, 
     char* p = static_cast<char*>(base);
     AttnWorkspace w;
     w.counters = reinterpret_cast<uint32_t*>(p);
+    w.flags = w.counters + kFlagBase;
     p += kCounterBytes;
     w.part_ml = reinterpret_cast<float*>(p);
     p += align_up(size_t(batch) * n_q_heads * num_splits * 2 * sizeof(float), 256);

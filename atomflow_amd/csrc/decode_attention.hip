@@ -119,6 +119,11 @@ struct AttnArgs {
     float* part_o;        // [batch][n_kv_heads][rec_stride][GROUP * head_dim]
     float* part_ml;       // [batch][n_kv_heads][rec_stride][2 * GROUP]  (m..., l...)
     uint32_t* counters;   // [batch][n_kv_heads]
+    // Dedicated-combiner form: workgroups [0, split_wgs) are splits, the next
+    // batch * n_kv_heads are one combiner per (sequence, KV head) that waits on
+    // its splits' ready flags ([batch * n_kv_heads][kCombSplits]).
+    uint32_t* flags;
+    int32_t split_wgs;
     // Shared prefix: rows [0, row_start) of every sequence are covered by
     // pre_records partials already in records 0 .. pre_records-1 (written by an
     // earlier launch); the splits cover rows [row_start, L) and write records
@@ -162,10 +167,131 @@ __device__ __forceinline__ uint64_t load_agent_u64(const float* p) {
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Polls of a dedicated combiner before it gives up (each waits one memory
+// round trip, ~0.5 us: about a second). Reached only if a split never
+// publishes; the output is then NaN and *d_status (if given) AF_ERR_TIMEOUT.
+constexpr int kCombMaxPolls = 1 << 21;
+
+// Split-K merge weights over records held one per lane (lane s: record s of a
+// query head; lanes past the last record hold m = -inf, l = 0): the max M, then
+// w_s = exp2(m_s - M) / sum_s exp2(m_s - M) l_s in lane s. Both merges (the
+// last-arrival combine and combine_dedicated) use it, so they agree bit for bit.
+__device__ __forceinline__ float merge_weight(float m, float l) {
+    const float mx = wave_max(m);
+    const float e = fast_exp2(m - mx);  // 0 for lanes without a record
+    float ls = 0.f;
+    ls += e * l;
+    return e * (1.0f / wave_sum(ls));
+}
+
+// Dedicated combiner of (sequence b, KV head hw), contiguous fp16, head_dim 128:
+// wave w serves query head w (64 lanes x 2 outputs; GROUP <= 4, host-checked).
+// Every wave polls the n_active <= kCombSplits ready flags (lane s: split s),
+// and loads a split's record as soon as its flag is set, so the records of
+// splits that finish early are in registers before the last one arrives: lane s
+// keeps split s's (m, l), every lane its two outputs of each split. A split sets
+// its flag after its partial stores are acknowledged at agent scope (the store
+// / vmcnt rules of the arrival counter below), and the flag and record loads are
+// agent-scope, so a set flag means the record is readable.
+template <int HD, int GROUP, bool FUSED>
+__device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int hw, int n_active,
+                                                  int pos) {
+    static_assert(HD == 128 && GROUP <= kWaves, "one query head per combiner wave");
+    constexpr int GQ = GROUP, GHD = GROUP * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool act = wave < GROUP;
+    const int gh = act ? wave : 0;
+    const int e = gh * HD + 2 * lane;  // the lane's outputs e, e + 1
+    const size_t grp = size_t(b) * a.n_kv_heads + hw;
+    const float* ml = a.part_ml + grp * a.rec_stride * 2 * GQ;
+    const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + grp * a.rec_stride * GHD);
+    uint32_t* flags = a.flags + grp * kCombSplits;
+
+    // The query heads are stored back rotated, as the last-arrival combine does
+    // (every split has read them once the records are complete). Their inputs
+    // are read now; a rotation pairs dims (d, d + HD/2), held by two lanes.
+    constexpr int half = HD / 2;
+    uint16_t* qh = a.q + size_t(b) * a.q_stride + size_t(hw) * GHD + size_t(gh) * HD;
+    const int d = 2 * lane, dd = d % half;
+    uint32_t qx = 0, qy = 0;
+    float2 cs = make_float2(0.f, 0.f), sn = make_float2(0.f, 0.f);
+    if constexpr (FUSED) {
+        if (act) {
+            qx = *reinterpret_cast<const uint32_t*>(qh + dd);
+            qy = *reinterpret_cast<const uint32_t*>(qh + dd + half);
+            cs = *reinterpret_cast<const float2*>(a.cos_t + size_t(pos) * half + dd);
+            sn = *reinterpret_cast<const float2*>(a.sin_t + size_t(pos) * half + dd);
+        }
+    }
+
+    const uint32_t all = n_active >= 32 ? ~0u : ((1u << n_active) - 1u);
+    uint32_t have = 0;
+    float mv = -INFINITY, lv = 0.f;  // lane s: split s
+    uint64_t ov[kCombSplits];
+#pragma unroll
+    for (int sp = 0; sp < kCombSplits; ++sp) ov[sp] = 0;
+    if (act) {
+        for (int polls = 0; have != all && polls < kCombMaxPolls; ++polls) {
+            const uint32_t f = lane < n_active ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT)
+                                               : 0u;
+            const uint32_t fresh = uint32_t(__builtin_amdgcn_ballot_w64(f != 0u)) & all & ~have;
+            if (lane < kCombSplits && ((fresh >> lane) & 1u)) {
+                mv = load_agent(ml + lane * 2 * GQ + gh);
+                lv = load_agent(ml + lane * 2 * GQ + GQ + gh);
+            }
+#pragma unroll
+            for (int sp = 0; sp < kCombSplits; ++sp)
+                if ((fresh >> sp) & 1u)
+                    ov[sp] = __hip_atomic_load(po + size_t(sp) * (GHD / 2) + e / 2,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            have |= fresh;
+        }
+    }
+    const bool timed_out = act && have != all;
+
+    const float w = merge_weight(mv, lv);  // lane s: split s's weight
+    float r0 = 0.f, r1 = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kCombSplits; ++sp) {
+        if (sp < n_active) {
+            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                           __builtin_bit_cast(uint32_t, w), sp));
+            r0 = fmaf(ws, __builtin_bit_cast(float, uint32_t(ov[sp])), r0);
+            r1 = fmaf(ws, __builtin_bit_cast(float, uint32_t(ov[sp] >> 32)), r1);
+        }
+    }
+    if (timed_out) r0 = r1 = __builtin_nanf("");
+    uint32_t qrot = 0;
+    if (act) {
+        uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
+        const uint32_t pair = uint32_t(__builtin_bit_cast(uint16_t, f16(r0))) |
+                              (uint32_t(__builtin_bit_cast(uint16_t, f16(r1))) << 16);
+        *reinterpret_cast<uint32_t*>(out_b + e) = pair;
+        if constexpr (FUSED) {
+            const float cc[2] = {cs.x, cs.y}, ss[2] = {sn.x, sn.y};
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                uint16_t xo, yo;
+                rope_rotate(uint16_t(qx >> (16 * u)), uint16_t(qy >> (16 * u)), cc[u], ss[u], xo, yo);
+                qrot |= uint32_t(d < half ? xo : yo) << (16 * u);
+            }
+        }
+    }
+    if (timed_out && lane == 0 && a.d_status) *a.d_status = AF_ERR_TIMEOUT;
+    // Every wave has read Q and finished polling past this barrier: the flags
+    // return to zero for the next launch and the rotated Q is stored.
+    __syncthreads();
+    if (tid < n_active)
+        __hip_atomic_store(flags + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (FUSED)
+        if (act) *reinterpret_cast<uint32_t*>(qh + d) = qrot;
+}
+
 // One workgroup = (sequence b, KV head h, split), or with PAIR (sequence b,
 // KV heads 2hw and 2hw+1, split): then GQ = 2 GROUP query heads share the
 // workgroup's records, merge and combine. See the file comment.
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB>
 __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
@@ -204,6 +330,12 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     const int nkv = a.n_kv_heads;
     const int nhw = nkv / KVH;  // workgroups per (sequence, split)
     int id = blockIdx.x;
+    // A dedicated combiner decodes as split 0 of its (sequence, KV head).
+    const bool comb = COMB && id >= a.split_wgs;
+    if (comb) {
+        const int c = id - a.split_wgs;
+        id = (c / nhw) * a.num_splits * nhw + c % nhw;
+    }
     const int hw = id % nhw;
     id /= nhw;
     const int split = id % a.num_splits;
@@ -215,7 +347,8 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         pos = a.positions ? a.positions[b] : a.pos_host;
         const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
         if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
-            if (tid == 0 && split == 0 && hw == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
+            if (tid == 0 && split == 0 && hw == 0 && !comb && a.d_status)
+                *a.d_status = AF_ERR_OUT_OF_RANGE;
             return;  // out-of-range append: nothing is written
         }
         L = pos + 1;
@@ -225,7 +358,7 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     }
     uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
     if (L <= 0) {  // empty sequence: defined as a zero output
-        if (split == 0)
+        if (split == 0 && !comb)
             for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
         return;
     }
@@ -252,6 +385,12 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     const int n_steps = step_end - step_begin;  // >= 1
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
+    if constexpr (COMB) {
+        if (comb) {
+            if (!direct) combine_dedicated<HD, GROUP, FUSED>(a, b, hw, n_active, pos);
+            return;
+        }
+    }
 
     // ---- stage this split's block-table entries (paged) --------------------
     int tab_base = 0;
@@ -771,6 +910,12 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     // order of these instructions; af_common.h rejects any other target.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if constexpr (COMB) {  // the dedicated combiner reads the partial once the flag is set
+        if (tid == 0)
+            __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     if (tid == 0) {
         uint32_t* ctr = a.counters + size_t(b) * nhw + hw;
         const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
@@ -816,7 +961,16 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     }
     __syncthreads();
     // split weights w = exp2(m - M) / sum_s exp2(m_s - M) l_s, one wave per head
+    // (up to 64 records: lane s holds record s, as in combine_dedicated, so the
+    // two merges give the same bits)
     for (int gh = wave; gh < GQ; gh += kWaves) {
+        if (n_rec <= 64) {
+            const bool has = lane < n_rec;
+            const float w = merge_weight(has ? s_ml[lane * 2 * GQ + gh] : -INFINITY,
+                                         has ? s_ml[lane * 2 * GQ + GQ + gh] : 0.f);
+            if (has) s_wt[gh][lane] = w;
+            continue;
+        }
         float mx = -INFINITY;
         for (int sp = lane; sp < n_rec; sp += 64) mx = fmaxf(mx, s_ml[sp * 2 * GQ + gh]);
         mx = wave_max(mx);
@@ -856,9 +1010,9 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     }
 }
 
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a) {
-    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR>(a);
+    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>(a);
 }
 
 // The fused pair form holds the RoPE inputs of two KV heads across the ring
@@ -866,7 +1020,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a)
 // (168 VGPRs, no spills for GROUP <= 4) where it would otherwise take 178.
 template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR>
 __global__ __launch_bounds__(kThreads, 3) void decode_attn_kernel_3wg(const AttnArgs a) {
-    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR>(a);
+    decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR, false>(a);
 }
 
 }  // namespace
@@ -878,27 +1032,40 @@ __global__ __launch_bounds__(kThreads, 3) void decode_attn_kernel_3wg(const Attn
 namespace af {
 namespace {
 
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR = false>
-hipError_t launch_attn(const AttnArgs& a, int grid, hipStream_t s) {
-    if constexpr (FUSED && PAIR && GROUP <= 4)
-        hipLaunchKernelGGL((decode_attn_kernel_3wg<HD, GROUP, FP8, PAGED, FUSED, PAIR>), dim3(grid),
-                           dim3(kThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED, FUSED, PAIR>), dim3(grid),
-                           dim3(kThreads), 0, s, a);
-    return hipGetLastError();
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR = false, bool COMB = false>
+int launch_attn(const AttnArgs& a, int grid, hipStream_t s) {
+    if constexpr (COMB && (HD != 128 || GROUP > kWaves)) {
+        return AF_ERR_UNSUPPORTED;  // the combiner's waves serve one query head each
+    } else {
+        if constexpr (FUSED && PAIR && GROUP <= 4)
+            hipLaunchKernelGGL((decode_attn_kernel_3wg<HD, GROUP, FP8, PAGED, FUSED, PAIR>),
+                               dim3(grid), dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_attn_kernel<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>),
+                               dim3(grid), dim3(kThreads), 0, s, a);
+        return int(hipGetLastError());
+    }
 }
 
-template <int HD, bool FP8, bool PAGED, bool FUSED, bool PAIR = false>
+template <int HD, bool FP8, bool PAGED, bool FUSED, bool PAIR = false, bool COMB = false>
 int dispatch_group(const AttnArgs& a, int group, int grid, hipStream_t s) {
     switch (group) {
-        case 1: return int(launch_attn<HD, 1, FP8, PAGED, FUSED, PAIR>(a, grid, s));
-        case 2: return int(launch_attn<HD, 2, FP8, PAGED, FUSED, PAIR>(a, grid, s));
-        case 3: return int(launch_attn<HD, 3, FP8, PAGED, FUSED, PAIR>(a, grid, s));
-        case 4: return int(launch_attn<HD, 4, FP8, PAGED, FUSED, PAIR>(a, grid, s));
-        case 8: return int(launch_attn<HD, 8, FP8, PAGED, FUSED, PAIR>(a, grid, s));
+        case 1: return launch_attn<HD, 1, FP8, PAGED, FUSED, PAIR, COMB>(a, grid, s);
+        case 2: return launch_attn<HD, 2, FP8, PAGED, FUSED, PAIR, COMB>(a, grid, s);
+        case 3: return launch_attn<HD, 3, FP8, PAGED, FUSED, PAIR, COMB>(a, grid, s);
+        case 4: return launch_attn<HD, 4, FP8, PAGED, FUSED, PAIR, COMB>(a, grid, s);
+        case 8: return launch_attn<HD, 8, FP8, PAGED, FUSED, PAIR, COMB>(a, grid, s);
         default: return AF_ERR_UNSUPPORTED;
     }
+}
+
+// The fp16 kernels; contiguous launches may take the dedicated-combiner form
+// (AttnArgs::split_wgs > 0).
+template <int HD, bool PAGED, bool FUSED>
+int dispatch_fp16(const AttnArgs& a, int group, int grid, hipStream_t s) {
+    if constexpr (!PAGED)
+        if (a.split_wgs > 0) return dispatch_group<HD, false, PAGED, FUSED, false, true>(a, group, grid, s);
+    return dispatch_group<HD, false, PAGED, FUSED>(a, group, grid, s);
 }
 
 // FP8 launches without shared-prefix records take KV heads in pairs (the
@@ -916,11 +1083,11 @@ int dispatch_fused(const AttnArgs& a, int head_dim, int group, bool fp8, bool pa
         return dispatch_group<128, true, true, FUSED>(a, group, grid, s);
     }
     if (head_dim == 128)
-        return paged ? dispatch_group<128, false, true, FUSED>(a, group, grid, s)
-                     : dispatch_group<128, false, false, FUSED>(a, group, grid, s);
+        return paged ? dispatch_fp16<128, true, FUSED>(a, group, grid, s)
+                     : dispatch_fp16<128, false, FUSED>(a, group, grid, s);
     if (head_dim == 64)
-        return paged ? dispatch_group<64, false, true, FUSED>(a, group, grid, s)
-                     : dispatch_group<64, false, false, FUSED>(a, group, grid, s);
+        return paged ? dispatch_fp16<64, true, FUSED>(a, group, grid, s)
+                     : dispatch_fp16<64, false, FUSED>(a, group, grid, s);
     return AF_ERR_UNSUPPORTED;
 }
 
@@ -932,9 +1099,18 @@ int dispatch(const AttnArgs& a, int head_dim, int group, bool fp8, bool paged, b
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Launches whose split-K tail goes through dedicated combiners instead of the
+// last-arriving split: few (sequence, KV head) pairs (combiners are one
+// workgroup each, dispatched after every split), at most kCombSplits splits,
+// and one output pair per combiner thread.
+bool use_combiner(int batch, int n_kv_heads, int num_splits, int group, int head_dim) {
+    return num_splits >= 2 && num_splits <= kCombSplits && head_dim == 128 && group <= kWaves &&
+           int64_t(batch) * n_kv_heads <= kCombMaxGroups;
+}
+
 float qk_scale_for(int head_dim) { return float(1.4426950408889634 / std::sqrt(double(head_dim))); }
 
-// Zero arrival counters (the state each launch leaves behind).
+// Zero arrival counters and ready flags (the state each launch leaves behind).
 int init_workspace(void* ws, size_t bytes, hipStream_t stream) {
     (void)bytes;
     return fill_u32(ws, 0u, kCounterBytes / 4, stream);
@@ -1105,8 +1281,13 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     a.part_ml = w.part_ml;
     a.counters = w.counters;
     a.rec_stride = num_splits;
-    return dispatch(a, head_dim, n_q_heads / n_kv_heads, false, false, fused,
-                    num_splits * n_kv_heads, stream);
+    int grid = num_splits * n_kv_heads;
+    if (use_combiner(1, n_kv_heads, num_splits, n_q_heads / n_kv_heads, head_dim)) {
+        a.flags = w.flags;
+        a.split_wgs = grid;
+        grid += n_kv_heads;  // one combiner per KV head, dispatched after every split
+    }
+    return dispatch(a, head_dim, n_q_heads / n_kv_heads, false, false, fused, grid, stream);
 }
 
 extern "C" int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache,

@@ -20,6 +20,7 @@ extern "C" const char* af_status_string(int status) {
         case AF_ERR_BAD_SEQUENCE: return "unknown sequence id";
         case AF_ERR_NOT_BUILT: return "device code not built";
         case AF_ERR_BAD_FILE: return "bad or truncated weight file";
+        case AF_ERR_TIMEOUT: return "decode attention: a split never published its partial";
         default: break;
     }
     if (status > 0) return hipGetErrorString(hipError_t(status));

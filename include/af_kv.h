@@ -43,6 +43,7 @@ extern "C" {
 #define AF_ERR_BAD_SEQUENCE (-7)    /* unknown sequence id                            */
 #define AF_ERR_NOT_BUILT (-8)       /* library built without a device code object     */
 #define AF_ERR_BAD_FILE (-9)        /* weight file missing, not AtomFlow, or truncated */
+#define AF_ERR_TIMEOUT (-10)        /* a decode-attention split never published (output NaN) */
 
 typedef void* af_stream_t; /* hipStream_t; NULL = the default stream */
 

@@ -45,9 +45,11 @@ def test_ctypes_prototypes_cover_the_headers():
 def test_library_loads_and_reports_status_strings():
     lib = atomflow_amd.lib()
     assert lib.af_version() > 0
-    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10):
         assert lib.af_status_string(code)
+        assert lib.af_status_string(code).decode() != "unknown status", code
     assert lib.af_status_string(-1).decode() == "block pool exhausted"
+    assert atomflow_amd.AF_ERR_TIMEOUT == -10
 
 
 def test_host_only_entry_points_without_gpu():
