@@ -50,8 +50,10 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 //                                per (sequence, KV head); words [kFlagBase,
 //                                kFlagBase + kCombMaxGroups * kCombSplits):
 //                                ready flags of the dedicated-combiner form, one
-//                                per (sequence, KV head, split). All zero between
-//                                launches (each launch re-zeroes what it used)
+//                                per (sequence, KV head, split); the last two
+//                                words: the persistent form's item counters. All
+//                                zero between launches (each launch re-zeroes
+//                                what it used)
 //   [kCounterBytes, ...)         part_ml [batch][n_kv_heads][splits][2 * group]
 //                                (group = n_q_heads / n_kv_heads: max..., sum...)
 //   then                         part_o  [batch][n_kv_heads][splits][group * head_dim]
@@ -69,6 +71,11 @@ constexpr int kCombSplits = 32;
 constexpr int kCombMaxGroups = 16;
 static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= int(kCounterBytes / sizeof(uint32_t)),
               "ready flags exceed the counter region");
+// Item and finished-workgroup counters of the persistent decode form (the last
+// two words of the counter region).
+constexpr int kItemCounter = int(kCounterBytes / sizeof(uint32_t)) - 2;
+constexpr int kDoneCounter = kItemCounter + 1;
+static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= kItemCounter, "counter words overlap");
 
 struct AttnWorkspace {
     uint32_t* counters;

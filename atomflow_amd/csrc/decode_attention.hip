@@ -124,6 +124,9 @@ struct AttnArgs {
     // its splits' ready flags ([batch * n_kv_heads][kCombSplits]).
     uint32_t* flags;
     int32_t split_wgs;
+    int32_t batch;       // sequences (the persistent form claims items over their rows)
+    int32_t item_big;    // persistent form: row-steps of a big / small item
+    int32_t item_small;
     // Shared prefix: rows [0, row_start) of every sequence are covered by
     // pre_records partials already in records 0 .. pre_records-1 (written by an
     // earlier launch); the splits cover rows [row_start, L) and write records
@@ -288,11 +291,19 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
         if (act) *reinterpret_cast<uint32_t*>(qh + d) = qrot;
 }
 
-// One workgroup = (sequence b, KV head h, split), or with PAIR (sequence b,
-// KV heads 2hw and 2hw+1, split): then GQ = 2 GROUP query heads share the
-// workgroup's records, merge and combine. See the file comment.
-template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB>
-__device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
+// One decode-attention work item: rows [t_begin, t_end) of (sequence b, KV
+// head group hw), split `split` of n_active (record slot pre_used + split).
+struct Seg {
+    int b, hw, split, n_active, pre_used;
+    int L, pos;                 // attended rows; the appended row's position (fused)
+    int t_begin, t_end, t_valid, n_steps;
+};
+
+// Streams one work item and publishes its partial (or the output when it is
+// the item's only split); the last split of (b, hw) to publish merges them.
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB,
+          bool PERSIST = false>
+__device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg) {
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
     constexpr int EPL = LY::kEpl;
@@ -323,74 +334,23 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     __shared__ uint4 s_new[FUSED ? KVH * 2 * V16 : 1];  // new token's K then V row, per KV head
     __shared__ int s_last;
 
-    const int tid = threadIdx.x;
+    int tid = threadIdx.x;
+    // The persistent form runs items in a loop: an opaque thread id keeps the
+    // compiler from hoisting per-lane values out of it (they would stay live
+    // across every item, past the register budget of 3 workgroups per CU).
+    if constexpr (PERSIST) asm volatile("" : "+v"(tid));
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane / LANES_ROW, j = lane & 7;
     const int sub = PAIR ? (lane >> 3) & 1 : 0;  // which KV head of the pair this lane reads
     const int nkv = a.n_kv_heads;
     const int nhw = nkv / KVH;  // workgroups per (sequence, split)
-    int id = blockIdx.x;
-    // A dedicated combiner decodes as split 0 of its (sequence, KV head).
-    const bool comb = COMB && id >= a.split_wgs;
-    if (comb) {
-        const int c = id - a.split_wgs;
-        id = (c / nhw) * a.num_splits * nhw + c % nhw;
-    }
-    const int hw = id % nhw;
-    id /= nhw;
-    const int split = id % a.num_splits;
-    const int b = id / a.num_splits;
+    const int b = sg.b, hw = sg.hw, split = sg.split, n_active = sg.n_active;
+    const int pre_used = sg.pre_used, L = sg.L, pos = sg.pos;
+    const int t_begin = sg.t_begin, t_end = sg.t_end, t_valid = sg.t_valid, n_steps = sg.n_steps;
     const int h = hw * KVH + sub;  // this lane's KV head
-
-    int L, pos = 0;
-    if constexpr (FUSED) {
-        pos = a.positions ? a.positions[b] : a.pos_host;
-        const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
-        if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
-            if (tid == 0 && split == 0 && hw == 0 && !comb && a.d_status)
-                *a.d_status = AF_ERR_OUT_OF_RANGE;
-            return;  // out-of-range append: nothing is written
-        }
-        L = pos + 1;
-    } else {
-        L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
-        L = min(L, a.max_seq_len);
-    }
     uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
-    if (L <= 0) {  // empty sequence: defined as a zero output
-        if (split == 0 && !comb)
-            for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
-        return;
-    }
-    // Balanced partition of rows [t_lo, L) in whole workgroup steps
-    // (STEP rows): C steps use n = min(num_splits, ceil(C / span)) splits
-    // and split s owns steps [s*C/n, (s+1)*C/n). t_lo = row_start, the first row
-    // after a shared prefix (0 without one). A sequence exactly as long as the
-    // prefix gets one split over its last row with every row masked (an empty
-    // partial), so the combine still runs over the prefix records. A sequence
-    // shorter than the prefix attends its own rows [0, L) through its table
-    // and its combine leaves the prefix records out (they cover rows >= L).
-    const bool below_prefix = L < a.row_start;
-    const int pre_used = below_prefix ? 0 : a.pre_records;  // prefix records this (b, h) merges
-    const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
-    const int total_steps = (L - t_lo + STEP - 1) / STEP;
-    const int span_steps = max(1, a.span_tokens / STEP);
-    const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
-    if (split >= n_active) return;
-    const int step_begin = int(int64_t(split) * total_steps / n_active);
-    const int step_end = int(int64_t(split + 1) * total_steps / n_active);
-    const int t_begin = t_lo + step_begin * STEP;
-    const int t_end = min(L, t_lo + step_end * STEP);
-    const int t_valid = L == a.row_start ? t_begin : t_end;  // rows below t_valid are scored
-    const int n_steps = step_end - step_begin;  // >= 1
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
-    if constexpr (COMB) {
-        if (comb) {
-            if (!direct) combine_dedicated<HD, GROUP, FUSED>(a, b, hw, n_active, pos);
-            return;
-        }
-    }
 
     // ---- stage this split's block-table entries (paged) --------------------
     int tab_base = 0;
@@ -1010,6 +970,83 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     }
 }
 
+// One workgroup = (sequence b, KV head h, split), or with PAIR (sequence b,
+// KV heads 2hw and 2hw+1, split): then GQ = 2 GROUP query heads share the
+// workgroup's records, merge and combine. See the file comment.
+template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB>
+__device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
+    constexpr int KVH = PAIR ? 2 : 1;          // KV heads per workgroup
+    constexpr int GHD = GROUP * KVH * HD;      // output width of the workgroup
+    constexpr int STEP = kWaves * (64 / (kLanesPerRow * KVH));  // token rows per workgroup step
+
+    const int tid = threadIdx.x;
+    const int nkv = a.n_kv_heads;
+    const int nhw = nkv / KVH;  // workgroups per (sequence, split)
+    int id = blockIdx.x;
+    // A dedicated combiner decodes as split 0 of its (sequence, KV head).
+    const bool comb = COMB && id >= a.split_wgs;
+    if (comb) {
+        const int c = id - a.split_wgs;
+        id = (c / nhw) * a.num_splits * nhw + c % nhw;
+    }
+    const int hw = id % nhw;
+    id /= nhw;
+    const int split = id % a.num_splits;
+    const int b = id / a.num_splits;
+
+    int L, pos = 0;
+    if constexpr (FUSED) {
+        pos = a.positions ? a.positions[b] : a.pos_host;
+        const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
+        if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
+            if (tid == 0 && split == 0 && hw == 0 && !comb && a.d_status)
+                *a.d_status = AF_ERR_OUT_OF_RANGE;
+            return;  // out-of-range append: nothing is written
+        }
+        L = pos + 1;
+    } else {
+        L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
+        L = min(L, a.max_seq_len);
+    }
+    uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
+    if (L <= 0) {  // empty sequence: defined as a zero output
+        if (split == 0 && !comb)
+            for (int o = tid; o < GHD; o += kThreads) out_b[o] = 0;
+        return;
+    }
+    // Balanced partition of rows [t_lo, L) in whole workgroup steps
+    // (STEP rows): C steps use n = min(num_splits, ceil(C / span)) splits
+    // and split s owns steps [s*C/n, (s+1)*C/n). t_lo = row_start, the first row
+    // after a shared prefix (0 without one). A sequence exactly as long as the
+    // prefix gets one split over its last row with every row masked (an empty
+    // partial), so the combine still runs over the prefix records. A sequence
+    // shorter than the prefix attends its own rows [0, L) through its table
+    // and its combine leaves the prefix records out (they cover rows >= L).
+    const bool below_prefix = L < a.row_start;
+    const int pre_used = below_prefix ? 0 : a.pre_records;  // prefix records this (b, h) merges
+    const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
+    const int total_steps = (L - t_lo + STEP - 1) / STEP;
+    const int span_steps = max(1, a.span_tokens / STEP);
+    const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
+    if (split >= n_active) return;
+    const int step_begin = int(int64_t(split) * total_steps / n_active);
+    const int step_end = int(int64_t(split + 1) * total_steps / n_active);
+    const int t_begin = t_lo + step_begin * STEP;
+    const int t_end = min(L, t_lo + step_end * STEP);
+    const int t_valid = L == a.row_start ? t_begin : t_end;  // rows below t_valid are scored
+    const int n_steps = step_end - step_begin;  // >= 1
+    const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
+    if constexpr (COMB) {
+        if (comb) {
+            if (!direct) combine_dedicated<HD, GROUP, FUSED>(a, b, hw, n_active, pos);
+            return;
+        }
+    }
+    const Seg sg{b, hw, split, n_active, pre_used, L, pos, t_begin, t_end, t_valid, n_steps};
+    decode_attn_seg<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>(a, sg);
+}
+
+
 template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(const AttnArgs a) {
     decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>(a);
@@ -1023,6 +1060,172 @@ __global__ __launch_bounds__(kThreads, 3) void decode_attn_kernel_3wg(const Attn
     decode_attn_body<HD, GROUP, FP8, PAGED, FUSED, PAIR, false>(a);
 }
 
+
+// ---- persistent form for batched launches ---------------------------------
+// Sequences of the persistent form (their row-step counts are scanned in LDS).
+constexpr int kMaxPersistBatch = 256;
+
+// Workgroup-uniform values read from LDS, moved to scalar registers.
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni64(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(x)));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(x) >> 32));
+    return int64_t((uint64_t(hi) << 32) | lo);
+}
+
+// Exclusive prefix sums of v[0, n) into pre[0, n] (pre[n] = total), n <=
+// 4 * kThreads, by the whole workgroup.
+__device__ __forceinline__ void block_exclusive_scan(const int32_t* v, int64_t* pre, int n) {
+    __shared__ int64_t s_wave[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int64_t x[4];
+    int64_t own = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid * 4 + u;
+        x[u] = i < n ? v[i] : 0;
+        own += x[u];
+    }
+    int64_t inc = own;  // inclusive scan over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t y = __shfl_up(inc, d);
+        if (lane >= d) inc += y;
+    }
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int64_t base = 0;
+    for (int w = 0; w < wave; ++w) base += s_wave[w];
+    int64_t run = base + inc - own;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid * 4 + u;
+        if (i < n) pre[i] = run;
+        run += x[u];
+    }
+    if (tid == kThreads - 1) pre[n] = run;
+    __syncthreads();
+}
+
+// Batched paged decode as a persistent grid (one launch of as many workgroups
+// as the device holds at once) that claims work items from a device counter,
+// so workgroups on faster CUs (or favoured within a CU) take more of them and
+// all finish within about one small item of each other. Every (sequence, KV
+// head group) with n row-steps is cut into n / C1 big items of C1 steps and
+// then ceil((n mod C1) / C2) small items of C2 steps (C2 < C1, both set by the
+// host so a group has at most rec_stride items); all big items are handed out
+// first, then the small ones, so the last items claimed are short. An item is
+// a split: its record slot is its index within its group and the last of the
+// group's items to publish merges them (the arrival counter of the grid form).
+// Claims go through item_ctr; each workgroup requests its next item before
+// streaming the current one, so the claim's round trip is hidden. The last
+// workgroup to run out of items (done_ctr) re-zeroes both counters.
+template <int HD, int GROUP, bool FP8, bool FUSED, bool PAIR>
+__global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_persistent(const AttnArgs a) {
+    constexpr int KVH = PAIR ? 2 : 1;
+    constexpr int GHD = GROUP * KVH * HD;
+    constexpr int STEP = kWaves * (64 / (kLanesPerRow * KVH));
+    __shared__ int32_t s_len[kMaxPersistBatch];
+    __shared__ int32_t s_cnt[kMaxPersistBatch];     // big items, then small items, of sequence b
+    __shared__ int64_t s_pre[kMaxPersistBatch + 1];  // exclusive prefix of s_cnt
+    __shared__ int32_t s_item;
+    const int tid = threadIdx.x;
+    const int B = a.batch;
+    const int nhw = a.n_kv_heads / KVH;
+    const int C1 = a.item_big, C2 = a.item_small;
+    uint32_t* item_ctr = a.counters + kItemCounter;
+    uint32_t* done_ctr = a.counters + kDoneCounter;
+    if (tid == 0)  // the first claim is in flight while the item list is built
+        s_item = int(__hip_atomic_fetch_add(item_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    // big-item counts of every sequence, then their prefix
+    for (int bb = tid; bb < B; bb += kThreads) {
+        int L;
+        if constexpr (FUSED) {
+            const int pos = a.positions[bb];
+            const int64_t row = a.slots[bb];
+            const bool ok = pos >= 0 && pos < a.max_pos && pos < a.max_seq_len && row >= 0 &&
+                            row < a.max_rows;
+            if (!ok && blockIdx.x == 0 && a.d_status) *a.d_status = AF_ERR_OUT_OF_RANGE;
+            L = ok ? pos + 1 : 0;  // out-of-range append: nothing is written
+        } else {
+            L = min(a.seq_lens[bb], a.max_seq_len);
+        }
+        s_len[bb] = L;
+        const int n = L > 0 ? (L + STEP - 1) / STEP : 0;
+        s_cnt[bb] = n / C1;
+    }
+    __syncthreads();
+    block_exclusive_scan(s_cnt, s_pre, B);
+    const int64_t T1 = uni64(int64_t(nhw) * s_pre[B]);  // big items in all
+    __shared__ int64_t s_pre2[kMaxPersistBatch + 1];    // exclusive prefix of small-item counts
+    __shared__ int32_t s_big[kMaxPersistBatch];
+    for (int bb = tid; bb < B; bb += kThreads) {
+        const int L = s_len[bb];
+        const int n = L > 0 ? (L + STEP - 1) / STEP : 0;
+        s_big[bb] = n / C1;
+        s_cnt[bb] = (n - (n / C1) * C1 + C2 - 1) / C2;
+    }
+    __syncthreads();
+    block_exclusive_scan(s_cnt, s_pre2, B);
+    const int64_t T = T1 + uni64(int64_t(nhw) * s_pre2[B]);
+    // Empty sequences (unfused, L <= 0) are defined as a zero output.
+    if constexpr (!FUSED) {
+        for (int p = blockIdx.x; p < B * nhw; p += gridDim.x) {
+            if (s_len[p / nhw] > 0) continue;
+            uint16_t* o = a.out + size_t(p / nhw) * a.out_stride + size_t(p % nhw) * GHD;
+            for (int e = tid; e < GHD; e += kThreads) o[e] = 0;
+        }
+    }
+    int64_t item = uni(s_item);
+    while (item < T) {
+        uint32_t next = 0;  // the following claim, issued before this item streams
+        if (tid == 0)
+            next = __hip_atomic_fetch_add(item_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool big = item < T1;
+        const int64_t* pre = big ? s_pre : s_pre2;
+        const int64_t i = big ? item : item - T1;
+        // the sequence of item i: the last b with nhw * pre[b] <= i
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) / 2;
+            if (int64_t(nhw) * pre[mid] <= i) lo = mid; else hi = mid - 1;
+        }
+        const int b = uni(lo);
+        const int nbig = uni(s_big[b]);
+        const int cnt = big ? nbig : uni(s_cnt[b]);
+        const int64_t r = i - uni64(int64_t(nhw) * pre[b]);
+        const int hw = uni(int(r / cnt));
+        const int k = uni(int(r % cnt));  // the item's index among its group's big / small items
+        const int L = uni(s_len[b]);
+        const int nsmall = uni(s_cnt[b]);
+        const int step0 = big ? k * C1 : nbig * C1 + k * C2;
+        const int steps = big ? C1 : C2;
+        Seg sg;
+        sg.b = b;
+        sg.hw = hw;
+        sg.split = big ? k : nbig + k;
+        sg.n_active = nbig + nsmall;
+        sg.pre_used = 0;
+        sg.L = L;
+        sg.pos = L - 1;
+        sg.t_begin = step0 * STEP;
+        sg.t_end = min(L, (step0 + steps) * STEP);
+        sg.t_valid = sg.t_end;
+        sg.n_steps = (sg.t_end - sg.t_begin + STEP - 1) / STEP;
+        decode_attn_seg<HD, GROUP, FP8, true, FUSED, PAIR, false, true>(a, sg);
+        if (tid == 0) s_item = int(next);
+        __syncthreads();  // the item's LDS (block table, partials) is reused by the next
+        item = uni(s_item);
+    }
+    if (tid == 0) {  // out of items: the last workgroup re-arms the counters
+        const uint32_t prev = __hip_atomic_fetch_add(done_ctr, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == gridDim.x - 1) {
+            __hip_atomic_store(item_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
 }  // namespace
 }  // namespace af
 
@@ -1098,6 +1301,70 @@ int dispatch(const AttnArgs& a, int head_dim, int group, bool fp8, bool paged, b
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Persistent form: rows of a big item (before the cap on items per group) and
+// small items per big one.
+constexpr int kBigItemRows = 1024;
+constexpr int kSmallItems = 8;
+
+// Workgroups of a persistent launch: as many as the device holds at once
+// (occupancy x CUs), looked up once per device for each kernel.
+template <int HD, int GROUP, bool FP8, bool FUSED, bool PAIR>
+int persistent_grid() {
+    static std::mutex mu;
+    static std::vector<int> grid;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (int(grid.size()) <= dev) grid.resize(size_t(dev) + 1, 0);
+    if (!grid[size_t(dev)]) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void*>(&decode_attn_persistent<HD, GROUP, FP8, FUSED, PAIR>),
+                kThreads, 0) != hipSuccess)
+            return 0;
+        grid[size_t(dev)] = std::max(1, per_cu) * device_compute_units();
+    }
+    return grid[size_t(dev)];
+}
+
+template <int HD, int GROUP, bool FP8, bool FUSED, bool PAIR>
+int launch_persistent(const AttnArgs& a, int grid, hipStream_t s) {
+    hipLaunchKernelGGL((decode_attn_persistent<HD, GROUP, FP8, FUSED, PAIR>), dim3(grid),
+                       dim3(kThreads), 0, s, a);
+    return int(hipGetLastError());
+}
+
+// The persistent form's kernel for (head_dim, group, dtype, fused): `grid` = 0
+// returns its grid size; otherwise launches it over `grid` workgroups.
+template <bool FP8, bool FUSED, bool PAIR>
+int persistent_group(const AttnArgs& a, int group, int grid, hipStream_t s) {
+#define AF_PERSIST_CASE(G)                                                             \
+    case G:                                                                            \
+        return grid ? launch_persistent<128, G, FP8, FUSED, PAIR>(a, grid, s)          \
+                    : persistent_grid<128, G, FP8, FUSED, PAIR>();
+    switch (group) {
+        AF_PERSIST_CASE(1)
+        AF_PERSIST_CASE(2)
+        AF_PERSIST_CASE(3)
+        AF_PERSIST_CASE(4)
+        AF_PERSIST_CASE(8)
+        default: return grid ? AF_ERR_UNSUPPORTED : 0;
+    }
+#undef AF_PERSIST_CASE
+}
+
+int persistent_dispatch(const AttnArgs& a, int group, bool fp8, bool fused, int grid, hipStream_t s) {
+    const bool pair = pair_heads(fp8, a);
+    if (fp8) {
+        if (pair) return fused ? persistent_group<true, true, true>(a, group, grid, s)
+                               : persistent_group<true, false, true>(a, group, grid, s);
+        return fused ? persistent_group<true, true, false>(a, group, grid, s)
+                     : persistent_group<true, false, false>(a, group, grid, s);
+    }
+    return fused ? persistent_group<false, true, false>(a, group, grid, s)
+                 : persistent_group<false, false, false>(a, group, grid, s);
+}
 
 // Launches whose split-K tail goes through dedicated combiners instead of the
 // last-arriving split: few (sequence, KV head) pairs (combiners are one
@@ -1446,9 +1713,15 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     const int suffix_max = std::max(max_seq_len - prefix.len, 1);
     const int min_sp = min_splits_for_table(std::max(suffix_max, std::min(prefix.len, max_seq_len)), bs);
     int span = kMinSpan;
+    bool persistent_ok = false;  // the default partition of a batch may run persistent
     if (num_splits <= 0) {
         num_splits = std::max(default_splits(suffix_max, batch, nkv), min_sp);
         span = default_span(batch, nkv);
+        // (FP8 pools; the fp16 kernel streams faster than its per-item
+        // set-up and merge let a persistent workgroup overlap, so fp16 batches
+        // keep the grid form)
+        persistent_ok = fp8 && span == kBatchSpan && prefix.len == 0 && hd == 128 &&
+                        batch <= kMaxPersistBatch;
         if (prefix.len > 0 && span == kBatchSpan) {
             // Batched suffixes behind a shared prefix are short: splits of up to
             // ~256 rows (measured best on MI355X for 64 forks of a 2048-row
@@ -1510,6 +1783,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     a.row_start = prefix.len;
     a.pre_records = pre;
     a.rec_stride = rec_stride;
+    a.batch = batch;
     const int64_t grid = int64_t(batch) * num_splits * nkv;
     if (grid > INT32_MAX) return AF_ERR_UNSUPPORTED;
     if (pre > 0) {  // the prefix's partials first: records 0 .. pre-1
@@ -1538,6 +1812,23 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
             pp.max_pos = max_pos;
         }
         if (int st = launch_prefix_partials(pp, stream)) return st;
+    }
+    if (persistent_ok && rec_stride > kSmallItems) {
+        // head_dim 128 batches without a shared prefix, default split count: the
+        // persistent form. Big items of about kBigItemRows rows, more when a
+        // group would otherwise exceed rec_stride items (at most n / C1 big and
+        // kSmallItems small ones); small items C1 / kSmallItems steps.
+        const int group = n_q_heads / nkv;
+        const int pgrid = persistent_dispatch(a, group, fp8, fused, 0, stream);
+        const int kvh = pair_heads(fp8, a) ? 2 : 1;
+        const int step = kWaves * (64 / (kLanesPerRow * kvh));
+        const int n_max = ceil_div(max_seq_len, step);
+        int c1 = std::max(kBigItemRows / step, ceil_div(n_max, rec_stride - kSmallItems));
+        c1 = ceil_div(c1, kSmallItems) * kSmallItems;
+        a.item_big = c1;
+        a.item_small = c1 / kSmallItems;
+        if (pgrid > 0 && (c1 * step) / bs + 2 <= kMaxTableLds)
+            return persistent_dispatch(a, group, fp8, fused, pgrid, stream);
     }
     return dispatch(a, hd, n_q_heads / nkv, fp8, true, fused, int(grid), stream);
 }
