@@ -142,7 +142,11 @@ int af_attention_default_splits(int max_seq_len, int batch, int n_kv_heads);
 
 /* Explicit-workspace form. seq_len: used when d_seq_len == NULL; otherwise the
  * length is read on the device (graph replay). num_splits <= 0 picks the
- * default for max_seq_len. k/v row stride is n_kv_heads*head_dim. */
+ * default for max_seq_len. k/v row stride is n_kv_heads*head_dim. With 2..32
+ * splits, n_kv_heads <= 16, head_dim 128 and up to 4 query heads per KV head,
+ * one combiner workgroup per KV head merges the splits' partials as they are
+ * published (a combiner that waits about a second for a split that never
+ * publishes writes NaN; the fused form then stores AF_ERR_TIMEOUT). */
 int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache, void* out,
                            int seq_len, const int32_t* d_seq_len, int max_seq_len, int head_dim,
                            int n_q_heads, int n_kv_heads, int num_splits, void* workspace,
@@ -199,7 +203,10 @@ int af_paged_rope_append(void* qkv_out, int batch, const af_kv_pool* pool, int l
  * q: [batch, q_stride] fp16 (head h at q + b*q_stride + h*head_dim),
  * d_block_tables: [batch, max_blocks_per_seq] int32, d_seq_lens: [batch] int32,
  * out: [batch, out_stride] fp16. max_seq_len bounds every d_seq_lens[b] and sizes
- * the split grid. Workspace from af_attention_workspace_size(batch, ...). */
+ * the split grid. Workspace from af_attention_workspace_size(batch, ...).
+ * With num_splits = 0, batches of FP8 pools (batch * n_kv_heads * 2 >= CUs,
+ * batch <= 256, head_dim 128) run as one persistent launch whose workgroups
+ * claim row ranges from a counter in the workspace (re-armed by the launch). */
 int af_paged_attention(const void* q, int q_stride, const af_kv_pool* pool, int layer,
                        const int32_t* d_block_tables, int max_blocks_per_seq,
                        const int32_t* d_seq_lens, int batch, int max_seq_len, void* out,

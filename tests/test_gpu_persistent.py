@@ -88,7 +88,7 @@ def test_persistent_fp8_vs_oracle(gpu, B):
 
 def test_persistent_fused_equals_unfused_and_appends(gpu):
     """Fused decode (RoPE + append + attention) == append, then the unfused kernel."""
-    B = 40
+    B = 96  # several items per workgroup, so item set-up overlaps the previous tail
     lengths = _lengths(940, B)
     lengths[0] = 5  # fused decode appends to every sequence
     say(f"persistent fused vs unfused B={B}")
