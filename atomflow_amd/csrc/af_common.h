@@ -144,6 +144,32 @@ struct PrefixPartialArgs {
     const int32_t* positions;
     int max_pos;
 };
+// The single-token QKV projection + RoPE + KV append (gemv.hip), for the
+// contiguous cache (rows = positions, max_rows = max_pos) and for one token of
+// the paged pool (row = *d_slot, fp16 or FP8 with the layer's per-head scales).
+enum { kQkvContiguous = 0, kQkvPagedFp16 = 1, kQkvPagedFp8 = 2 };
+struct QkvSingleArgs {
+    const uint8_t* w;        // [n_q + 2 n_kv heads][head_dim] x k E4M3 weights
+    const uint16_t* x;       // k fp16 activations
+    const uint16_t* scales;  // fp16 group scales
+    int k, group_size;
+    uint16_t* qkv;           // the projection (rotated Q and K)
+    uint8_t* k_dst;          // K / V destination rows (fp16 or fp8 elements)
+    uint8_t* v_dst;
+    const float* cos_t;      // [max_pos][head_dim / 2]
+    const float* sin_t;
+    int pos_host;            // position when d_pos is NULL
+    const int32_t* d_pos;
+    int max_pos;
+    const int64_t* d_slot;   // paged: the destination row
+    int64_t max_rows;
+    const float* k_scales;   // FP8: [n_kv_heads] each
+    const float* v_scales;
+    int n_q_heads, n_kv_heads, head_dim;
+    int32_t* d_status;
+};
+void launch_qkv_single(const QkvSingleArgs& a, int dest, hipStream_t stream);
+
 // Workgroups of the partial launch per key split.
 int prefix_partial_tiles(int batch, int group, int n_kv_heads);
 int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream);

@@ -366,6 +366,9 @@ extern "C" int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, con
     if (int st = check_batched(x, x_stride, m, weight, scales, n, k, group_size)) return st;
     if (!y || y_stride < n) return AF_ERR_INVALID_ARG;
     if (m == 0) return AF_OK;
+    // One token: the single-token GEMV streams the weights faster than one
+    // 16-token MFMA tile that is 15/16 padding.
+    if (m == 1) return af_w8a16_gemv(x, weight, scales, y, n, k, group_size, stream);
     BatchedArgs a{};
     fill_common(a, x, x_stride, m, weight, scales, n, k, group_size);
     a.y = static_cast<uint16_t*>(y);
@@ -399,6 +402,34 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
     const int kv_dim = pool->n_kv_heads * hd;
     const size_t slab = size_t(pool->total_blocks) * pool->block_size * kv_dim * esz;
     uint8_t* base = static_cast<uint8_t*>(pool->base);
+    if (m == 1) {  // one token: the GEMV form, as af_w8a16_gemm_batched at m = 1
+        QkvSingleArgs q{};
+        q.w = w_qkv;
+        q.x = static_cast<const uint16_t*>(x);
+        q.scales = static_cast<const uint16_t*>(scales);
+        q.k = k;
+        q.group_size = group_size;
+        q.qkv = static_cast<uint16_t*>(qkv_out);
+        q.k_dst = base + size_t(2 * layer) * slab;
+        q.v_dst = base + size_t(2 * layer + 1) * slab;
+        q.cos_t = cos_table;
+        q.sin_t = sin_table;
+        q.d_pos = d_positions;
+        q.max_pos = max_pos;
+        q.d_slot = d_slots;
+        q.max_rows = int64_t(pool->total_blocks) * pool->block_size;
+        if (fp8) {
+            q.k_scales = pool->scales + size_t(layer) * 2 * pool->n_kv_heads;
+            q.v_scales = q.k_scales + pool->n_kv_heads;
+        }
+        q.n_q_heads = n_q_heads;
+        q.n_kv_heads = pool->n_kv_heads;
+        q.head_dim = hd;
+        q.d_status = d_status;
+        launch_qkv_single(q, fp8 ? kQkvPagedFp8 : kQkvPagedFp16, static_cast<hipStream_t>(stream));
+        AF_TRY_LAUNCH();
+        return AF_OK;
+    }
     BatchedArgs a{};
     fill_common(a, x, x_stride, m, w_qkv, scales, n, k, group_size);
     a.y = static_cast<uint16_t*>(qkv_out);

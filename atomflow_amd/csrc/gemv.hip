@@ -6,8 +6,9 @@
 // output. M = 1: every weight byte is read once, so the roofline is HBM.
 //
 // Design:
-//  * One wave owns RPW (2..5) rows, chosen so the waves make a whole number of
-//    rounds of one wave per SIMD. A weight row is read in 1 KB chunks, 16
+//  * One wave owns RPW (1..5) rows: one row per wave up to four waves per SIMD
+//    of the device, two up to sixteen (more waves in flight beat sharing the
+//    activation loads over more rows). A weight row is read in 1 KB chunks, 16
 //    bytes per lane (global_load_dwordx4); the activation slice of a chunk is
 //    loaded once and shared by the wave's rows. All of a pass's loads (NCH
 //    chunks x RPW rows; one pass for K up to 8 KB) are issued before any is used.
@@ -15,11 +16,13 @@
 //    two fp16 values is exact in fp32, so each 16-element slice is summed with
 //    v_dot2c_f32_f16 in fp32 and scaled once by its group scale.
 //  * Lane partials are summed with DPP and v_permlane16/32_swap (no LDS).
-//  * The fused QKV kernel gives each wave two rotation pairs (d, d+HD/2) and
-//    (d+1, d+1+HD/2) of one head, so RoPE and the KV append run on the rounded
-//    fp16 results in registers: the output equals af_w8a16_gemv followed by
-//    af_rope_append bit for bit (a row's arithmetic does not depend on which
-//    wave computes it or on the chunks per pass).
+//  * The fused QKV kernel gives each wave one rotation pair (d, d+HD/2) of one
+//    head, so RoPE and the KV append run on the rounded fp16 results in
+//    registers: the output equals af_w8a16_gemv followed by af_rope_append bit
+//    for bit (a row's arithmetic does not depend on which wave computes it or
+//    on the chunks per pass). The position and cos / sin loads go out with the
+//    weight loads. The same kernel appends one token to a paged pool (fp16 or
+//    FP8), the single-token form of af_paged_qkv_rope_append.
 #include <algorithm>
 #include <cmath>
 
@@ -33,7 +36,8 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kGemvWaves = 4;                 // plain GEMV: waves per workgroup
 constexpr int kGemvThreads = kGemvWaves * 64;
-constexpr int kQkvWaves = 5;                  // fused QKV: 2 rotation pairs per wave
+constexpr int kQkvWaves = 5;                  // fused QKV: waves per workgroup
+constexpr int kQkvPairs = 1;                  // fused QKV: rotation pairs per wave
 constexpr int kQkvThreads = kQkvWaves * 64;
 constexpr int kChunkBytes = 64 * 16;          // one weight-row chunk per wave load
 
@@ -54,12 +58,20 @@ __device__ __forceinline__ float dot16(const uint4 w, const uint4 xa, const uint
 
 // Lane partials of rows[r] (r < RPW) over the whole K dimension, NCH chunks
 // per pass. Chunks past K are read at a clamped address and contribute 0.
-template <int RPW, int NCH>
+// `hook` runs once, right after the first pass's loads are issued: loads the
+// caller needs only after the sums (the fused kernel's position and cos / sin)
+// then travel with the weight loads instead of after them.
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+template <int RPW, int NCH, typename Hook = NoHook>
 __device__ __forceinline__ void row_partials(const uint8_t* __restrict__ w,
                                              const uint16_t* __restrict__ x,
                                              const uint16_t* __restrict__ scales,
                                              const int (&rows)[RPW], int k, int group_size,
-                                             int groups, int lane, float (&acc)[RPW]) {
+                                             int groups, int lane, float (&acc)[RPW],
+                                             const Hook& hook = Hook()) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
     for (int base = 0; base < k; base += NCH * kChunkBytes) {
@@ -79,6 +91,7 @@ __device__ __forceinline__ void row_partials(const uint8_t* __restrict__ w,
                 sc[c][r] = scales[size_t(rows[r]) * groups + kk / group_size];
             }
         }
+        if (base == 0) hook();
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
 #pragma unroll
@@ -90,8 +103,7 @@ __device__ __forceinline__ void row_partials(const uint8_t* __restrict__ w,
 }
 
 // ---- plain GEMV: wave w of block b owns rows (4b + w) * RPW .. + RPW - 1 ----
-// RPW is picked so there is about one wave per SIMD of the device, NCH so one
-// pass covers K for the usual widths.
+// RPW from rows_per_wave, NCH so one pass covers K for the usual widths.
 template <int RPW, int NCH>
 __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(
     const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,
@@ -147,58 +159,80 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_pair_kernel(
 
 // ---- fused decode QKV projection + RoPE + KV append --------------------------
 // Output rows of qkv_out = [Q heads | K heads | V heads] x head_dim. Rotation
-// pairs are numbered p = head * HD/2 + d; wave w of block b takes pairs
-// 2(b*kQkvWaves + w) and +1, i.e. rows (head, d), (head, d+1) and their
-// partners + HD/2.
-template <int NCH>
-__global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(
-    const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,
-    const uint16_t* __restrict__ scales, int k, int group_size, uint16_t* __restrict__ qkv,
-    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos_host,
-    const int32_t* __restrict__ d_pos, int max_seq, int n_q_heads, int n_kv_heads, int head_dim,
-    int32_t* __restrict__ d_status) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int half = head_dim / 2;
-    const int n_pairs = (n_q_heads + 2 * n_kv_heads) * half;
-    const int p0 = 2 * (blockIdx.x * kQkvWaves + wave);
-    if (p0 >= n_pairs) return;  // half is even, so pair p0 + 1 is in the same head
+// pairs are numbered p = head * HD/2 + d; wave w of block b takes the PPW pairs
+// PPW(b*kQkvWaves + w) .. + PPW - 1 of one head, i.e. rows (head, d .. d+PPW-1)
+// and their partners + HD/2. DEST selects where K and V go (QkvSingleArgs).
+template <int PPW, int NCH, int DEST>
+__global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(const QkvSingleArgs a) {
+    constexpr int R = 2 * PPW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hd = a.head_dim, half = hd / 2;
+    const int n_pairs = (a.n_q_heads + 2 * a.n_kv_heads) * half;
+    const int p0 = PPW * (blockIdx.x * kQkvWaves + wave);
+    if (p0 >= n_pairs) return;  // half % PPW == 0: the wave's pairs are in one head
     const int head = p0 / half;
-    const int dA = p0 % half;  // pairs (dA, dA+half), (dA+1, dA+1+half)
-    const int hrow = head * head_dim;
-    const int rows[4] = {hrow + dA, hrow + dA + 1, hrow + dA + half, hrow + dA + 1 + half};
-    float acc[4];
-    row_partials<4, NCH>(w, x, scales, rows, k, group_size, k / group_size, lane, acc);
-    uint16_t yv[4];
+    const int dA = p0 % half;  // pairs (dA + j, dA + j + half), j < PPW
+    int rows[R];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) yv[r] = f2h(wave_sum(acc[r]));
-    // The position is read once the weight loads are in flight; an
-    // out-of-range one writes nothing.
-    const int pos = d_pos ? *d_pos : pos_host;
-    if (pos < 0 || pos >= max_seq) {
-        if (blockIdx.x == 0 && threadIdx.x == 0 && d_status) *d_status = AF_ERR_OUT_OF_RANGE;
-        return;
+    for (int j = 0; j < PPW; ++j) {
+        rows[j] = head * hd + dA + j;
+        rows[PPW + j] = head * hd + dA + j + half;
     }
-    if (lane != 0) return;
-    const int kv_dim = n_kv_heads * head_dim;
-    const int kind = head < n_q_heads ? 0 : (head < n_q_heads + n_kv_heads ? 1 : 2);  // Q, K, V
-    uint16_t out[4] = {yv[0], yv[1], yv[2], yv[3]};
-    if (kind < 2) {
+    // The position, the destination row and the cos / sin are read while the
+    // weight loads are in flight (the table row clamped into the table).
+    const bool rotate = head < a.n_q_heads + a.n_kv_heads;  // Q and K rows
+    int pos = 0;
+    int64_t row = 0;
+    float cs[PPW], sn[PPW];
+    auto fetch = [&]() {
+        pos = a.d_pos ? *a.d_pos : a.pos_host;
+        row = DEST == kQkvContiguous ? int64_t(pos) : *a.d_slot;
+        const size_t at = size_t(min(max(pos, 0), a.max_pos - 1)) * half + dA;
 #pragma unroll
-        for (int p = 0; p < 2; ++p)  // the reference's rope_kernel arithmetic, rope.cu:30-45
-            rope_rotate(yv[p], yv[2 + p], cos_t[size_t(pos) * half + dA + p],
-                        sin_t[size_t(pos) * half + dA + p], out[p], out[2 + p]);
+        for (int j = 0; j < PPW; ++j) {
+            cs[j] = rotate ? a.cos_t[at + j] : 0.f;
+            sn[j] = rotate ? a.sin_t[at + j] : 0.f;
+        }
+    };
+    float acc[R];
+    row_partials<R, NCH>(a.w, a.x, a.scales, rows, a.k, a.group_size, a.k / a.group_size, lane,
+                         acc, fetch);
+    uint16_t out[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) out[r] = f2h(wave_sum(acc[r]));
+    const bool ok = pos >= 0 && pos < a.max_pos && row >= 0 && row < a.max_rows;
+    if (!ok && blockIdx.x == 0 && threadIdx.x == 0 && a.d_status)
+        *a.d_status = AF_ERR_OUT_OF_RANGE;
+    // Out of range: the contiguous form writes nothing, the paged form leaves
+    // the unrotated projection in qkv_out and nothing in the pool.
+    if ((!ok && DEST == kQkvContiguous) || lane != 0) return;
+    if (ok && rotate) {
+#pragma unroll
+        for (int j = 0; j < PPW; ++j)  // the reference's rope_kernel arithmetic, rope.cu:30-45
+            rope_rotate(out[j], out[PPW + j], cs[j], sn[j], out[j], out[PPW + j]);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) qkv[rows[r]] = out[r];
-    if (kind > 0) {
-        uint16_t* cache = kind == 1 ? k_cache : v_cache;
-        const int hk = head - n_q_heads - (kind == 2 ? n_kv_heads : 0);
-        uint16_t* dst = cache + size_t(pos) * kv_dim + size_t(hk) * head_dim;
-        dst[dA] = out[0];
-        dst[dA + 1] = out[1];
-        dst[dA + half] = out[2];
-        dst[dA + 1 + half] = out[3];
+    for (int r = 0; r < R; ++r) a.qkv[rows[r]] = out[r];
+    if (!ok || head < a.n_q_heads) return;
+    const bool is_k = head < a.n_q_heads + a.n_kv_heads;
+    const int hk = head - a.n_q_heads - (is_k ? 0 : a.n_kv_heads);
+    const size_t at = size_t(row) * (a.n_kv_heads * hd) + size_t(hk) * hd + dA;
+    if constexpr (DEST == kQkvPagedFp8) {
+        const float sc = (is_k ? a.k_scales : a.v_scales)[hk];
+        uint8_t* dst = (is_k ? a.k_dst : a.v_dst) + at;
+#pragma unroll
+        for (int j = 0; j < PPW; ++j) {
+            dst[j] = uint8_t(quantize_fp8(out[j], sc));
+            dst[j + half] = uint8_t(quantize_fp8(out[PPW + j], sc));
+        }
+    } else {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(is_k ? a.k_dst : a.v_dst) + at;
+#pragma unroll
+        for (int j = 0; j < PPW; ++j) {
+            dst[j] = out[j];
+            dst[j + half] = out[PPW + j];
+        }
     }
 }
 
@@ -234,12 +268,14 @@ void launch_gemv(int nch, hipStream_t s, const uint8_t* w, const uint16_t* x, co
                            sc, y, n, k, group_size);
 }
 
-// Rows per wave for n rows: the fewest whole rounds of one wave per SIMD with at
-// most 5 rows per wave, then rows spread evenly over those rounds (2..5).
+// Rows per wave for n rows: 1 up to four waves per SIMD, 2 up to sixteen, then
+// as many as keep eight waves per SIMD (at most 5). Measured on the Llama-3.2-3B
+// shapes (3072 / 8192 / 16384 rows): fewer rows per wave, and so more waves with
+// loads in flight, is faster until the activation loads (one per row at RPW 1)
+// cost more than the extra waves win.
 int rows_per_wave(int n) {
     const int simds = 4 * device_compute_units();
-    const int rounds = std::max(1, (n + 5 * simds - 1) / (5 * simds));
-    return std::min(5, std::max(2, (n + simds * rounds - 1) / (simds * rounds)));
+    return n <= 4 * simds ? 1 : (n <= 16 * simds ? 2 : std::min(5, (n + 8 * simds - 1) / (8 * simds)));
 }
 
 template <int RPW, int NCH>
@@ -263,7 +299,33 @@ void launch_pair(int nch, const GemvPair& p, const uint16_t* x, int k, int group
         launch_pair_nch<RPW, 4>(p, x, k, group_size, s);
 }
 
+template <int PPW, int NCH>
+void launch_qkv_nch(const QkvSingleArgs& q, int dest, hipStream_t s) {
+    const int n_pairs = (q.n_q_heads + 2 * q.n_kv_heads) * (q.head_dim / 2);
+    const dim3 grid((n_pairs + PPW * kQkvWaves - 1) / (PPW * kQkvWaves));
+    if (dest == kQkvPagedFp8)
+        hipLaunchKernelGGL((qkv_rope_append_kernel<PPW, NCH, kQkvPagedFp8>), grid,
+                           dim3(kQkvThreads), 0, s, q);
+    else if (dest == kQkvPagedFp16)
+        hipLaunchKernelGGL((qkv_rope_append_kernel<PPW, NCH, kQkvPagedFp16>), grid,
+                           dim3(kQkvThreads), 0, s, q);
+    else
+        hipLaunchKernelGGL((qkv_rope_append_kernel<PPW, NCH, kQkvContiguous>), grid,
+                           dim3(kQkvThreads), 0, s, q);
+}
+
 }  // namespace
+
+void launch_qkv_single(const QkvSingleArgs& q, int dest, hipStream_t s) {
+    const int nch = chunks_per_pass(q.k);
+    if (nch == 3)
+        launch_qkv_nch<kQkvPairs, 3>(q, dest, s);
+    else if (nch == 8)
+        launch_qkv_nch<kQkvPairs, 8>(q, dest, s);
+    else
+        launch_qkv_nch<kQkvPairs, 4>(q, dest, s);
+}
+
 }  // namespace af
 
 using namespace af;
@@ -288,6 +350,7 @@ extern "C" int af_w8a16_gemv_pair(const void* x, const uint8_t* weight0, const v
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto* xw = static_cast<const uint16_t*>(x);
     switch (rows_per_wave(n0 + n1)) {
+        case 1: launch_pair<1>(nch, p, xw, k, group_size, s); break;
         case 2: launch_pair<2>(nch, p, xw, k, group_size, s); break;
         case 3: launch_pair<3>(nch, p, xw, k, group_size, s); break;
         case 4: launch_pair<4>(nch, p, xw, k, group_size, s); break;
@@ -308,6 +371,7 @@ extern "C" int af_w8a16_gemv(const void* x, const uint8_t* weight, const void* s
     const auto* sw = static_cast<const uint16_t*>(scales);
     auto* yw = static_cast<uint16_t*>(y);
     switch (rpw) {
+        case 1: launch_gemv<1>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
         case 2: launch_gemv<2>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
         case 3: launch_gemv<3>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
         case 4: launch_gemv<4>(nch, s, weight, xw, sw, yw, n, k, group_size); break;
@@ -328,29 +392,28 @@ extern "C" int af_qkv_rope_append(const void* x, const uint8_t* w_qkv, const voi
     if (int st = check_gemv_shape(x, w_qkv, scales, n, k, group_size)) return st;
     if (!qkv_out || !k_cache || !v_cache || !cos_table || !sin_table || max_seq <= 0)
         return AF_ERR_INVALID_ARG;
-    if (head_dim % 4) return AF_ERR_UNSUPPORTED;  // two rotation pairs per wave, one head
+    if (head_dim % 2) return AF_ERR_UNSUPPORTED;  // rotation pairs (d, d + head_dim / 2)
     if (!d_pos && (pos < 0 || pos >= max_seq)) return AF_ERR_OUT_OF_RANGE;
-    const int n_pairs = n / 2;
-    const int grid = (n_pairs + 2 * kQkvWaves - 1) / (2 * kQkvWaves);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const auto* xw = static_cast<const uint16_t*>(x);
-    const auto* sw = static_cast<const uint16_t*>(scales);
-    auto* qw = static_cast<uint16_t*>(qkv_out);
-    auto* kc = static_cast<uint16_t*>(k_cache);
-    auto* vc = static_cast<uint16_t*>(v_cache);
-    const int nch = chunks_per_pass(k);
-    if (nch == 3)
-        hipLaunchKernelGGL(qkv_rope_append_kernel<3>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
-                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
-                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
-    else if (nch == 8)
-        hipLaunchKernelGGL(qkv_rope_append_kernel<8>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
-                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
-                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
-    else
-        hipLaunchKernelGGL(qkv_rope_append_kernel<4>, dim3(grid), dim3(kQkvThreads), 0, s, w_qkv,
-                           xw, sw, k, group_size, qw, kc, vc, cos_table, sin_table, pos, d_pos,
-                           max_seq, n_q_heads, n_kv_heads, head_dim, d_status);
+    QkvSingleArgs q{};
+    q.w = w_qkv;
+    q.x = static_cast<const uint16_t*>(x);
+    q.scales = static_cast<const uint16_t*>(scales);
+    q.k = k;
+    q.group_size = group_size;
+    q.qkv = static_cast<uint16_t*>(qkv_out);
+    q.k_dst = static_cast<uint8_t*>(k_cache);
+    q.v_dst = static_cast<uint8_t*>(v_cache);
+    q.cos_t = cos_table;
+    q.sin_t = sin_table;
+    q.pos_host = pos;
+    q.d_pos = d_pos;
+    q.max_pos = max_seq;
+    q.max_rows = max_seq;
+    q.n_q_heads = n_q_heads;
+    q.n_kv_heads = n_kv_heads;
+    q.head_dim = head_dim;
+    q.d_status = d_status;
+    launch_qkv_single(q, kQkvContiguous, static_cast<hipStream_t>(stream));
     AF_TRY_LAUNCH();
     return AF_OK;
 }

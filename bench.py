@@ -1204,6 +1204,10 @@ READ_PROBE_WORKLOADS = [
     ("configs[4] (3.25 GB, FP8 rows)", 1585518 * 2 * 1024, 2, 1024, 128),
     # the same rows read as 256-B pieces: two KV heads per workgroup (the FP8 pair form)
     ("configs[4] (3.25 GB, FP8 rows, KV-head pairs)", 1585518 * 2 * 1024, 2, 1024, 256),
+    # the E4M3 weights of the projections either side of the path (K = 3072 rows of 3 KB)
+    # (contiguous reads only: segment 0)
+    ("QKV weights 5120 x 3072 (15.7 MB)", QKV * HIDDEN, 28, HIDDEN, 0),
+    ("o_proj weights 3072 x 3072 (9.4 MB)", HIDDEN * HIDDEN, 28, HIDDEN, 0),
 ]
 
 
@@ -1221,11 +1225,13 @@ def bench_read_probe(args, dev):
         log(f"read probe: {name}, {nbytes} B per launch x {layers} regions ...")
         buf = dev.DeviceBuffer(nbytes * layers)
         buf.fill_u32(0x3C003C00, stream)
-        n_seg = row_bytes // seg
+        n_seg = row_bytes // seg if seg else 0
         entry = {"bytes_per_launch": nbytes, "regions": layers, "contiguous_us": {},
                  "head_rows_us": {}, "head_row_bytes": row_bytes, "segment_bytes": seg}
-        for kind, grid in (("contiguous_us", (256, 512, 1024, 2048, 4096, 8192)),
-                           ("head_rows_us", tuple(n_seg * sp for sp in (24, 32, 64, 128, 256, 512)))):
+        kinds = [("contiguous_us", (256, 512, 1024, 2048, 4096, 8192))]
+        if n_seg:
+            kinds.append(("head_rows_us", tuple(n_seg * sp for sp in (24, 32, 64, 128, 256, 512))))
+        for kind, grid in kinds:
             for g in grid:
                 def launches(g=g, kind=kind):
                     for l in range(layers):
@@ -1239,6 +1245,8 @@ def bench_read_probe(args, dev):
                 graph.destroy()
                 entry[kind][str(g)] = round(us, 3)
         for kind in ("contiguous_us", "head_rows_us"):
+            if not entry[kind]:
+                continue
             g, us = min(entry[kind].items(), key=lambda kv_: kv_[1])
             gbs = nbytes / (us * 1e-6) / 1e9
             entry["best_" + kind[:-3]] = {"workgroups": int(g), "us": us, "gbs": round(gbs, 1),

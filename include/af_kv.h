@@ -304,7 +304,7 @@ int af_w8a16_gemv_pair(const void* x, const uint8_t* weight0, const void* scales
  * token per step: launch_w8a16_gemv, qkv_gemm.cu:32-152; a serving step has one
  * token per sequence). k and group_size multiples of 32; x_stride >= k and a
  * multiple of 8; x and weight 16-byte aligned. Weights are read once per 32
- * tokens. */
+ * tokens; m = 1 runs af_w8a16_gemv itself (the same bits). */
 int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, const uint8_t* weight,
                           const void* scales, void* y, int64_t y_stride, int n, int k,
                           int group_size, af_stream_t stream);
@@ -315,7 +315,9 @@ int af_w8a16_gemm_batched(const void* x, int64_t x_stride, int m, const uint8_t*
  * d_positions, ...), the same outputs bit for bit (the paged form of
  * af_qkv_rope_append). A token whose position or slot is out of range gets its
  * unrotated projection in qkv_out, nothing in the pool, and AF_ERR_OUT_OF_RANGE
- * in *d_status (if given). head_dim 128. */
+ * in *d_status (if given). head_dim 128. m = 1 runs the single-token form of
+ * af_qkv_rope_append on the pool row (the GEMV's arithmetic, which is what
+ * af_w8a16_gemm_batched computes at m = 1). */
 int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m, const uint8_t* w_qkv,
                              const void* scales, int k, int group_size, void* qkv_out,
                              const af_kv_pool* pool, int layer, const int64_t* d_slots,
@@ -329,7 +331,7 @@ int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m, const uint8
  * outputs bit for bit (src/core/engine.cu:315-355 issues the three launches).
  * Position: *d_pos when d_pos != NULL, else pos; a device position >= max_seq
  * writes nothing and stores AF_ERR_OUT_OF_RANGE into *d_status (if given).
- * head_dim a multiple of 16. */
+ * head_dim even. */
 int af_qkv_rope_append(const void* x, const uint8_t* w_qkv, const void* scales, int k,
                        int group_size, void* qkv_out, void* k_cache, void* v_cache,
                        const float* cos_table, const float* sin_table, int pos,

@@ -73,16 +73,28 @@ def test_gemm_batched_rejects_bad_shapes(gpu):
     assert call(dx.ptr, 1024, 0, dw.ptr, ds.ptr, y.ptr, 64, 64, 1024, 128, None) == 0
 
 
-@pytest.mark.parametrize("fp8,group", [(False, 128), (True, 128), (False, 32)])
-def test_paged_qkv_rope_append_equals_unfused(gpu, fp8, group):
-    say(f"paged qkv rope append, fp8 {fp8}, group {group}")
-    k_in, m, bs, total, max_pos = 3072, 19, 16, 96, 700
+@pytest.mark.parametrize("fp8,group,m,bad", [(False, 128, 19, 5), (True, 128, 19, 5),
+                                              (False, 32, 19, 5), (False, 128, 1, None),
+                                              (True, 128, 1, None), (True, 128, 1, "pos"),
+                                              (False, 128, 1, "slot")])
+def test_paged_qkv_rope_append_equals_unfused(gpu, fp8, group, m, bad):
+    """m = 1 takes the single-token GEMV form; it must still equal the batched
+    projection (itself the GEMV at m = 1) followed by the paged append."""
+    say(f"paged qkv rope append, fp8 {fp8}, group {group}, m {m}, out of range {bad}")
+    k_in, bs, total, max_pos = 3072, 16, 96, 700
     w, _, s = gemv_case(QKV, k_in, 0xA70F31, group=group)
     xs = np.random.default_rng(3).standard_normal((m, k_in)).astype(np.float16)
     r = np.random.default_rng(4)
     slots = r.permutation(total * bs)[:m].astype(np.int64)
     positions = r.integers(0, max_pos, m).astype(np.int32)
-    positions[5] = max_pos  # out of range: projection stays unrotated, nothing appended
+    # an out-of-range token: its projection stays unrotated, nothing is appended
+    bad_row = None
+    if bad == "pos" or isinstance(bad, int):
+        bad_row = bad if isinstance(bad, int) else 0
+        positions[bad_row] = max_pos
+    elif bad == "slot":
+        bad_row = 0
+        slots[0] = total * bs
     esz = 1 if fp8 else 2
     pool_bytes = 2 * 2 * total * bs * KV_DIM * esz  # two layers
     init = r.integers(0, 256, pool_bytes, dtype=np.uint8)
@@ -109,11 +121,39 @@ def test_paged_qkv_rope_append_equals_unfused(gpu, fp8, group):
     p1 = pools[0][0].download(np.uint8, (pool_bytes,))
     p2 = pools[1][0].download(np.uint8, (pool_bytes,))
     assert np.array_equal(p1, p2)
-    assert not np.array_equal(p1, init)  # something was appended
-    assert st.download(np.int32, (1,))[0] == atomflow_amd.AF_ERR_OUT_OF_RANGE
-    # the out-of-range token's projection is unrotated: equal to the plain projection
     plain = batched_gpu(w, xs, s, group)
-    assert np.array_equal(q1.download(np.uint16, (m, QKV))[5], plain[5].view(np.uint16))
+    if m == 1:  # the batched projection of one token is the GEMV, bit for bit
+        y = dev.DeviceBuffer(QKV * 2)
+        kv.launch_w8a16_gemv(dx, dw, ds, y, QKV, k_in, group)
+        assert np.array_equal(plain[0].view(np.uint16), y.download(np.uint16, (QKV,)))
+    status = st.download(np.int32, (1,))[0]
+    if bad_row is None:
+        assert status == 0
+        assert not np.array_equal(p1, init)  # something was appended
+        # the appended row matches the oracle's append of the rotated projection
+        if m == 1:
+            host = init.reshape(2, 2, total * bs, KV_DIM * esz).copy()
+            rq = oracle.rope_append(plain[0], np.zeros((1, KV_DIM), np.float16),
+                                    np.zeros((1, KV_DIM), np.float16), c[positions[0]:],
+                                    sn[positions[0]:], 0, NQ, NKV, HD)
+            assert np.array_equal(q1.download(np.uint16, (QKV,)), rq.view(np.uint16))
+            kr, vr = rq[NQ * HD:NQ * HD + KV_DIM], rq[NQ * HD + KV_DIM:]
+            if fp8:
+                hk = host[1, 0].reshape(-1, KV_DIM)
+                hv = host[1, 1].reshape(-1, KV_DIM)
+                oracle.paged_write_fp8(kr, vr, hk, hv, int(slots[0]), KV_DIM, HD,
+                                       np.full(NKV, 0.04, np.float32),
+                                       np.full(NKV, 0.04, np.float32))
+            else:
+                host[1, 0, slots[0]] = kr.view(np.uint8)
+                host[1, 1, slots[0]] = vr.view(np.uint8)
+            assert np.array_equal(p1, host.reshape(-1))
+    else:
+        assert status == atomflow_amd.AF_ERR_OUT_OF_RANGE
+        assert np.array_equal(q1.download(np.uint16, (m, QKV))[bad_row],
+                              plain[bad_row].view(np.uint16))
+        if m == 1:
+            assert np.array_equal(p1, init)  # nothing appended
 
 
 def test_paged_qkv_rope_append_graph_replays(gpu):
