@@ -297,13 +297,22 @@ struct Seg {
     int b, hw, split, n_active, pre_used;
     int L, pos;                 // attended rows; the appended row's position (fused)
     int t_begin, t_end, t_valid, n_steps;
+    // Persistent form: this item's block-table window was loaded by the
+    // previous item (thread t holds entry t).
+    int staged;
 };
 
 // Streams one work item and publishes its partial (or the output when it is
 // the item's only split); the last split of (b, hw) to publish merges them.
+struct NoNextItem {
+    __device__ bool operator()(uint32_t, int*, int*, int*) const { return false; }
+};
+
 template <int HD, int GROUP, bool FP8, bool PAGED, bool FUSED, bool PAIR, bool COMB,
-          bool PERSIST = false>
-__device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg) {
+          bool PERSIST = false, typename NextFn = NoNextItem>
+__device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg, int32_t& nx_entry,
+                                                uint32_t next_item = 0,
+                                                const NextFn& next_window = NextFn()) {
     using LY = Layout<HD, FP8>;
     constexpr int LOADS = LY::kLoads;
     constexpr int EPL = LY::kEpl;
@@ -333,6 +342,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     __shared__ uint16_t s_q[FUSED ? GHD : 1];
     __shared__ uint4 s_new[FUSED ? KVH * 2 * V16 : 1];  // new token's K then V row, per KV head
     __shared__ int s_last;
+    __shared__ uint32_t s_next;  // persistent form: the item claimed for after this one
 
     int tid = threadIdx.x;
     // The persistent form runs items in a loop: an opaque thread id keeps the
@@ -358,11 +368,17 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
         const int first = t_begin >> a.block_shift;
         const int last = (t_end - 1) >> a.block_shift;
         tab_base = first;
-        const int32_t* trow = a.tables + size_t(b) * a.max_blocks;
-        for (int e = tid; e <= last - first; e += kThreads) {
-            int blk = trow[first + e];
-            blk = min(max(blk, 0), int(a.total_blocks - 1));  // never address outside the pool
-            s_tab[e] = blk;
+        if (PERSIST && sg.staged) {
+            // the previous item loaded this window's entries (thread t holds
+            // entry t) while it merged
+            if (tid <= last - first) s_tab[tid] = min(max(nx_entry, 0), int(a.total_blocks - 1));
+        } else {
+            const int32_t* trow = a.tables + size_t(b) * a.max_blocks;
+            for (int e = tid; e <= last - first; e += kThreads) {
+                int blk = trow[first + e];
+                blk = min(max(blk, 0), int(a.total_blocks - 1));  // never address outside the pool
+                s_tab[e] = blk;
+            }
         }
         __syncthreads();
     }
@@ -729,6 +745,9 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
             if (i < rem) process_row(ring[i], n_full * NB + i);
     }
 
+    if constexpr (PERSIST)  // the claim issued at the item's start has long returned
+        if (tid == 0) s_next = next_item;
+
     // ---- merge: token groups in registers, then the workgroup in LDS -------
     if constexpr (!PAIR) {
         // Lanes i and i+8 of a 16-lane row hold token groups g, g^1 with the
@@ -800,6 +819,16 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
         }
     }
     __syncthreads();
+    if constexpr (PERSIST) {
+        // The next item's block-table window (thread t: entry t, up to kThreads
+        // entries): loaded here, it arrives while this item merges and
+        // publishes, and the next item stages it from registers.
+        int nb = 0, first = 0, count = 0;
+        if (next_window(s_next, &nb, &first, &count)) {
+            const int e = min(tid, count - 1);
+            nx_entry = a.tables[size_t(nb) * a.max_blocks + first + e];
+        }
+    }
 
     // ---- merge the partials: the output, or this split's partial ------------
     // Thread t owns head-dim pair (2t, 2t+1).
@@ -1043,7 +1072,8 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         }
     }
     const Seg sg{b, hw, split, n_active, pre_used, L, pos, t_begin, t_end, t_valid, n_steps};
-    decode_attn_seg<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>(a, sg);
+    int32_t unused = 0;
+    decode_attn_seg<HD, GROUP, FP8, PAGED, FUSED, PAIR, COMB>(a, sg, unused);
 }
 
 
@@ -1064,6 +1094,10 @@ __global__ __launch_bounds__(kThreads, 3) void decode_attn_kernel_3wg(const Attn
 // ---- persistent form for batched launches ---------------------------------
 // Sequences of the persistent form (their row-step counts are scanned in LDS).
 constexpr int kMaxPersistBatch = 256;
+
+// Big items of a group with n row-steps: its steps in whole items of c1 (the
+// remainder goes out in small items).
+__host__ __device__ inline int big_items(int n, int c1) { return n / c1; }
 
 // Workgroup-uniform values read from LDS, moved to scalar registers.
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -1111,13 +1145,16 @@ __device__ __forceinline__ void block_exclusive_scan(const int32_t* v, int64_t* 
 // as the device holds at once) that claims work items from a device counter,
 // so workgroups on faster CUs (or favoured within a CU) take more of them and
 // all finish within about one small item of each other. Every (sequence, KV
-// head group) with n row-steps is cut into n / C1 big items of C1 steps and
-// then ceil((n mod C1) / C2) small items of C2 steps (C2 < C1, both set by the
+// head group) with n row-steps is cut into big_items(n) = n / C1 items of C1
+// steps, then small items of C2 steps over the rest (C2 < C1, both set by the
 // host so a group has at most rec_stride items); all big items are handed out
-// first, then the small ones, so the last items claimed are short. An item is
-// a split: its record slot is its index within its group and the last of the
-// group's items to publish merges them (the arrival counter of the grid form).
-// Claims go through item_ctr; each workgroup requests its next item before
+// first, then the small ones, so the last items claimed are short. (Moving a
+// quarter of every group into small items cost more in per-item set-up and
+// merge than it saved at the end.) An item is a split: its record
+// slot is its index within its group and the last of the group's items to
+// publish merges them (the arrival counter of the grid form). Workgroup w
+// starts on item w; further claims go through item_ctr (item = grid size +
+// the counter's value), and each workgroup requests its next item before
 // streaming the current one, so the claim's round trip is hidden. The last
 // workgroup to run out of items (done_ctr) re-zeroes both counters.
 template <int HD, int GROUP, bool FP8, bool FUSED, bool PAIR>
@@ -1135,8 +1172,6 @@ __global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_pers
     const int C1 = a.item_big, C2 = a.item_small;
     uint32_t* item_ctr = a.counters + kItemCounter;
     uint32_t* done_ctr = a.counters + kDoneCounter;
-    if (tid == 0)  // the first claim is in flight while the item list is built
-        s_item = int(__hip_atomic_fetch_add(item_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     // big-item counts of every sequence, then their prefix
     for (int bb = tid; bb < B; bb += kThreads) {
         int L;
@@ -1152,7 +1187,7 @@ __global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_pers
         }
         s_len[bb] = L;
         const int n = L > 0 ? (L + STEP - 1) / STEP : 0;
-        s_cnt[bb] = n / C1;
+        s_cnt[bb] = big_items(n, C1);
     }
     __syncthreads();
     block_exclusive_scan(s_cnt, s_pre, B);
@@ -1162,8 +1197,9 @@ __global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_pers
     for (int bb = tid; bb < B; bb += kThreads) {
         const int L = s_len[bb];
         const int n = L > 0 ? (L + STEP - 1) / STEP : 0;
-        s_big[bb] = n / C1;
-        s_cnt[bb] = (n - (n / C1) * C1 + C2 - 1) / C2;
+        const int nb = big_items(n, C1);
+        s_big[bb] = nb;
+        s_cnt[bb] = (n - nb * C1 + C2 - 1) / C2;
     }
     __syncthreads();
     block_exclusive_scan(s_cnt, s_pre2, B);
@@ -1176,11 +1212,8 @@ __global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_pers
             for (int e = tid; e < GHD; e += kThreads) o[e] = 0;
         }
     }
-    int64_t item = uni(s_item);
-    while (item < T) {
-        uint32_t next = 0;  // the following claim, issued before this item streams
-        if (tid == 0)
-            next = __hip_atomic_fetch_add(item_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The item's split descriptor (sequence, group, row range).
+    auto make_seg = [&](int64_t item) -> Seg {
         const bool big = item < T1;
         const int64_t* pre = big ? s_pre : s_pre2;
         const int64_t i = big ? item : item - T1;
@@ -1212,10 +1245,38 @@ __global__ __launch_bounds__(kThreads, GROUP <= 4 ? 3 : 1) void decode_attn_pers
         sg.t_end = min(L, (step0 + steps) * STEP);
         sg.t_valid = sg.t_end;
         sg.n_steps = (sg.t_end - sg.t_begin + STEP - 1) / STEP;
-        decode_attn_seg<HD, GROUP, FP8, true, FUSED, PAIR, false, true>(a, sg);
+        sg.staged = 0;
+        return sg;
+    };
+    // The block-table window of item `it` (false past the last item).
+    auto window = [&](uint32_t it, int* nb, int* first, int* count) -> bool {
+        if (int64_t(it) >= T) return false;
+        const Seg nx = make_seg(it);
+        *nb = nx.b;
+        *first = nx.t_begin >> a.block_shift;
+        *count = ((nx.t_end - 1) >> a.block_shift) - *first + 1;
+        return *count <= kThreads;
+    };
+    // Workgroup w starts on item w without a claim (768 claims at once on one
+    // counter serialise at the memory side for microseconds); each further
+    // item is claimed at the start of the one before it, whose merge then
+    // loads the claimed item's block-table window.
+    int64_t item = blockIdx.x;
+    int staged = 0;
+    int32_t nx_entry = 0;  // thread t: entry t of the next item's block-table window
+    while (item < T) {
+        uint32_t next = 0;  // the following claim, issued before this item streams
+        if (tid == 0)
+            next = gridDim.x +
+                   __hip_atomic_fetch_add(item_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        Seg sg = make_seg(item);
+        sg.staged = staged;
+        decode_attn_seg<HD, GROUP, FP8, true, FUSED, PAIR, false, true>(a, sg, nx_entry, next, window);
         if (tid == 0) s_item = int(next);
         __syncthreads();  // the item's LDS (block table, partials) is reused by the next
         item = uni(s_item);
+        int nb, first, count;
+        staged = window(uint32_t(item), &nb, &first, &count);
     }
     if (tid == 0) {  // out of items: the last workgroup re-arms the counters
         const uint32_t prev = __hip_atomic_fetch_add(done_ctr, 1u, __ATOMIC_RELAXED,
@@ -1306,6 +1367,46 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // small items per big one.
 constexpr int kBigItemRows = 1024;
 constexpr int kSmallItems = 8;
+
+// Most items of a group with up to n_max row-steps, big items of c1 steps and
+// small ones of c2. The count grows with n while big_items(n) stays the same,
+// so the maximum is at n_max or just before big_items steps up.
+// (big_items(n) = k for n in [k c1, (k + 1) c1).)
+int max_items(int n_max, int c1, int c2) {
+    auto items = [&](int n) {
+        const int nb = big_items(n, c1);
+        return nb + ceil_div(n - nb * c1, c2);
+    };
+    int worst = items(n_max);
+    for (int k = 1;; ++k) {
+        const int n = c1 * k - 1;  // the last n with big_items(n) = k - 1
+        if (n > n_max) break;
+        if (n >= 1) worst = std::max(worst, items(n));
+    }
+    return worst;
+}
+
+// Item sizes of the persistent form: big items of c1_min steps and small ones
+// of c1 / kSmallItems, the small ones coarsened first (up to c1 / 2), then
+// both, until every group fits `records` items.
+bool plan_items(int n_max, int records, int c1_min, int* c1, int* c2) {
+    int a = std::max(1, c1_min), b = std::max(1, a / kSmallItems);
+    for (int guard = 0; guard < 64; ++guard) {
+        if (max_items(n_max, a, b) <= records) {
+            *c1 = a;
+            *c2 = b;
+            return true;
+        }
+        if (2 * b <= a / 2) {
+            b *= 2;
+        } else {
+            a *= 2;
+            b = std::max(b, a / kSmallItems);
+        }
+        if (a > n_max + 1 && b > n_max + 1) break;
+    }
+    return false;
+}
 
 // Workgroups of a persistent launch: as many as the device holds at once
 // (occupancy x CUs), looked up once per device for each kernel.
@@ -1813,22 +1914,22 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
         }
         if (int st = launch_prefix_partials(pp, stream)) return st;
     }
-    if (persistent_ok && rec_stride > kSmallItems) {
+    if (persistent_ok) {
         // head_dim 128 batches without a shared prefix, default split count: the
-        // persistent form. Big items of about kBigItemRows rows, more when a
-        // group would otherwise exceed rec_stride items (at most n / C1 big and
-        // kSmallItems small ones); small items C1 / kSmallItems steps.
+        // persistent form, with item sizes that keep every group within
+        // rec_stride items.
         const int group = n_q_heads / nkv;
         const int pgrid = persistent_dispatch(a, group, fp8, fused, 0, stream);
         const int kvh = pair_heads(fp8, a) ? 2 : 1;
         const int step = kWaves * (64 / (kLanesPerRow * kvh));
-        const int n_max = ceil_div(max_seq_len, step);
-        int c1 = std::max(kBigItemRows / step, ceil_div(n_max, rec_stride - kSmallItems));
-        c1 = ceil_div(c1, kSmallItems) * kSmallItems;
-        a.item_big = c1;
-        a.item_small = c1 / kSmallItems;
-        if (pgrid > 0 && (c1 * step) / bs + 2 <= kMaxTableLds)
+        int c1 = 0, c2 = 0;
+        if (pgrid > 0 && plan_items(ceil_div(max_seq_len, step), rec_stride, kBigItemRows / step,
+                                    &c1, &c2) &&
+            (c1 * step) / bs + 2 <= kMaxTableLds) {
+            a.item_big = c1;
+            a.item_small = c2;
             return persistent_dispatch(a, group, fp8, fused, pgrid, stream);
+        }
     }
     return dispatch(a, hd, n_q_heads / nkv, fp8, true, fused, int(grid), stream);
 }
