@@ -1,4 +1,4 @@
-"""GPU parity at two BASELINE config points that the smaller tests do not reach.
+"""GPU parity at BASELINE config points that the smaller tests do not reach.
 
 * configs[1] at ctx 32768: one decode step at position 32768 (L = 32769 rows,
   the library's default split count), fused and as the two separate launches,
@@ -15,6 +15,9 @@
   oracle: the rotated query and the appended K/V codes bit for bit, attention
   within the FP8 bar and the fp16 bar. The unfused paged attention over the
   updated pool must equal the fused output bit for bit.
+* configs[1] as bench.py times it: the 28-layer contiguous stack at ctx 8192,
+  every layer's fused step in one captured hipGraph, each layer against the
+  oracle.
 """
 import numpy as np
 import pytest
@@ -77,6 +80,61 @@ def test_config2_ctx32k_fused_and_unfused(gpu):
     ref32 = oracle.cached_attention(rq[:Q_DIM], k, v, L, NQ, NKV, HD, threads=8)
     assert_attn_close(got, ref64, what="ctx 32768 vs fp64 oracle")
     assert_attn_close(got, ref32, what="ctx 32768 vs fp32 oracle")
+
+
+def test_config2_28_layer_graph_ctx8k_vs_oracle(gpu):
+    """BASELINE configs[1] as bench.py times it: 28 contiguous layers, ctx 8192, one
+    fused RoPE + append + attention launch per layer (default split count) and the
+    position advance captured in one hipGraph. Two replays (positions 8192 and
+    8193), fresh QKV rows uploaded before each: every layer's rotated QKV row and
+    appended K/V row bit for bit, its attention output within the fp16 bar of the
+    float64 oracle (tiled_attention.cu:196-269 over the reference's per-layer
+    [MAX_SEQ_LEN, KV_DIM] slabs, engine.cu:187-215)."""
+    layers, pos0, steps = 28, 8192, 2
+    max_seq = pos0 + 128
+    say(f"configs[1] 28-layer graph: ctx {pos0}, max_seq {max_seq}, default splits "
+        f"{kv.default_splits(max_seq, 1, NKV)}")
+    c, s = oracle.rope_table(max_seq, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    host = [contiguous_case(max_seq, pos0, SEED_BASE + 100 + 3 * l) for l in range(layers)]
+    dev_l = [(dev.DeviceBuffer(QKV * 2), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2))
+             for (_, k, v) in host]
+    ws = kv.AttentionWorkspace(1, NQ, NKV, HD, 0)
+    d_pos = up(np.array([pos0], np.int32))
+    d_st = up(np.array([0], np.int32))
+    stream = dev.Stream()
+
+    def step():
+        for (qkv, k, v, o) in dev_l:
+            kv.launch_decode_attention_fused(qkv, k, v, d_c, d_s, -1, max_seq, o, NQ, NKV, HD, ws,
+                                             num_splits=0, d_pos=d_pos, d_status=d_st,
+                                             stream=stream)
+        dev.add_i32(d_pos.ptr, 1, 1, stream)
+
+    graph = dev.Graph.capture(stream, step)
+    try:
+        for i in range(steps):
+            pos = pos0 + i
+            rows = [np.random.default_rng(SEED_BASE + 1000 * i + l).standard_normal(QKV)
+                    .astype(np.float16) for l in range(layers)]
+            for l in range(layers):
+                dev_l[l][0].upload(rows[l])
+            graph.launch(stream)
+            stream.sync()
+            for l in range(layers):
+                _, k, v = host[l]
+                rq = oracle.rope_append(rows[l], k, v, c, s, pos, NQ, NKV, HD)  # row pos of k, v
+                qkv_d, k_d, v_d, o_d = dev_l[l]
+                assert np.array_equal(bits(qkv_d.download(np.float16)), bits(rq)), (i, l)
+                for d_cache, h_cache in ((k_d, k), (v_d, v)):
+                    got_row = d_cache.download(np.uint16, (max_seq, KV_DIM))[pos]
+                    assert np.array_equal(got_row, bits(h_cache[pos])), (i, l)
+                ref = oracle.cached_attention_f64(rq[:Q_DIM], k, v, pos + 1, NQ, NKV, HD)
+                assert_attn_close(o_d.download(np.float16), ref, what=f"step {i} layer {l}")
+        assert d_pos.download(np.int32)[0] == pos0 + steps and d_st.download(np.int32)[0] == 0
+    finally:
+        graph.destroy()
+        stream.destroy()
 
 
 def _sample(rng_, tables, lens, k):
