@@ -134,6 +134,13 @@ struct AttnArgs {
     int32_t row_start;
     int32_t pre_records;
     int32_t rec_stride;
+    // Batched grid form (up to kThreads sequences, no shared prefix): the grid
+    // is batch x heads x num_splits, but a sequence uses only the splits its
+    // length needs. Workgroups then map onto the splits that exist (sequence
+    // by sequence, heads fastest) and the surplus, at the end of the grid,
+    // exits at once, instead of idle workgroups spread through the grid each
+    // holding a slot for a length read.
+    int32_t compact;
 };
 
 template <int HD, bool FP8>
@@ -289,6 +296,40 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
         __hip_atomic_store(flags + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (FUSED)
         if (act) *reinterpret_cast<uint32_t*>(qh + d) = qrot;
+}
+
+// Exclusive prefix sums of v[0, n) into pre[0, n] (pre[n] = total), n <=
+// 4 * kThreads, by the whole workgroup.
+__device__ __forceinline__ void block_exclusive_scan(const int32_t* v, int64_t* pre, int n) {
+    __shared__ int64_t s_wave[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int64_t x[4];
+    int64_t own = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid * 4 + u;
+        x[u] = i < n ? v[i] : 0;
+        own += x[u];
+    }
+    int64_t inc = own;  // inclusive scan over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t y = __shfl_up(inc, d);
+        if (lane >= d) inc += y;
+    }
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int64_t base = 0;
+    for (int w = 0; w < wave; ++w) base += s_wave[w];
+    int64_t run = base + inc - own;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid * 4 + u;
+        if (i < n) pre[i] = run;
+        run += x[u];
+    }
+    if (tid == kThreads - 1) pre[n] = run;
+    __syncthreads();
 }
 
 // One decode-attention work item: rows [t_begin, t_end) of (sequence b, KV
@@ -1018,10 +1059,46 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         const int c = id - a.split_wgs;
         id = (c / nhw) * a.num_splits * nhw + c % nhw;
     }
-    const int hw = id % nhw;
-    id /= nhw;
-    const int split = id % a.num_splits;
-    const int b = id / a.num_splits;
+    int hw, split, b;
+    if (a.compact) {
+        __shared__ int32_t s_splits[kThreads];      // splits of each sequence
+        __shared__ int64_t s_first[kThreads + 1];   // exclusive prefix: its first split
+        const int span_steps = max(1, a.span_tokens / STEP);
+        if (tid < a.batch) {
+            int Lb;
+            if constexpr (FUSED) {  // the length the fused step attends (0: out of range)
+                const int pb = a.positions ? a.positions[tid] : a.pos_host;
+                const int64_t rb = a.slots ? a.slots[tid] : int64_t(pb);
+                const bool ok = pb >= 0 && pb < a.max_pos && pb < a.max_seq_len && rb >= 0 &&
+                                rb < a.max_rows;
+                Lb = ok ? pb + 1 : 0;
+            } else {
+                Lb = min(a.seq_lens ? a.seq_lens[tid] : a.seq_len_host, a.max_seq_len);
+            }
+            // as below (no shared prefix): n_active splits; an empty or
+            // out-of-range sequence keeps one for its zero output / status
+            const int steps = Lb > 0 ? (Lb + STEP - 1) / STEP : 0;
+            s_splits[tid] = Lb > 0 ? max(1, min(a.num_splits, (steps + span_steps - 1) / span_steps))
+                                   : 1;
+        }
+        __syncthreads();
+        block_exclusive_scan(s_splits, s_first, a.batch);
+        if (id >= s_first[a.batch] * nhw) return;
+        int lo = 0, hi = a.batch - 1;  // the last sequence whose first split is <= id
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) / 2;
+            if (s_first[mid] * nhw <= id) lo = mid; else hi = mid - 1;
+        }
+        b = lo;
+        const int r = id - int(s_first[b] * nhw);
+        hw = r % nhw;
+        split = r / nhw;
+    } else {
+        hw = id % nhw;
+        id /= nhw;
+        split = id % a.num_splits;
+        b = id / a.num_splits;
+    }
 
     int L, pos = 0;
     if constexpr (FUSED) {
@@ -1107,39 +1184,6 @@ __device__ __forceinline__ int64_t uni64(int64_t x) {
     return int64_t((uint64_t(hi) << 32) | lo);
 }
 
-// Exclusive prefix sums of v[0, n) into pre[0, n] (pre[n] = total), n <=
-// 4 * kThreads, by the whole workgroup.
-__device__ __forceinline__ void block_exclusive_scan(const int32_t* v, int64_t* pre, int n) {
-    __shared__ int64_t s_wave[kWaves];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int64_t x[4];
-    int64_t own = 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = tid * 4 + u;
-        x[u] = i < n ? v[i] : 0;
-        own += x[u];
-    }
-    int64_t inc = own;  // inclusive scan over the wave
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int64_t y = __shfl_up(inc, d);
-        if (lane >= d) inc += y;
-    }
-    if (lane == 63) s_wave[wave] = inc;
-    __syncthreads();
-    int64_t base = 0;
-    for (int w = 0; w < wave; ++w) base += s_wave[w];
-    int64_t run = base + inc - own;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = tid * 4 + u;
-        if (i < n) pre[i] = run;
-        run += x[u];
-    }
-    if (tid == kThreads - 1) pre[n] = run;
-    __syncthreads();
-}
 
 // Batched paged decode as a persistent grid (one launch of as many workgroups
 // as the device holds at once) that claims work items from a device counter,
@@ -1885,6 +1929,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     a.pre_records = pre;
     a.rec_stride = rec_stride;
     a.batch = batch;
+    a.compact = span == kBatchSpan && pre == 0 && batch <= kThreads;
     const int64_t grid = int64_t(batch) * num_splits * nkv;
     if (grid > INT32_MAX) return AF_ERR_UNSUPPORTED;
     if (pre > 0) {  // the prefix's partials first: records 0 .. pre-1
