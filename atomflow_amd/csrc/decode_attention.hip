@@ -134,9 +134,9 @@ struct AttnArgs {
     int32_t row_start;
     int32_t pre_records;
     int32_t rec_stride;
-    // Batched grid form (up to kThreads sequences, no shared prefix): the grid
-    // is batch x heads x num_splits, but a sequence uses only the splits its
-    // length needs. Workgroups then map onto the splits that exist (sequence
+    // Batched paged grid form (up to kThreads sequences, no shared prefix): the
+    // grid is batch x heads x num_splits, but a sequence uses only the splits
+    // its length needs. Workgroups then map onto the splits that exist (sequence
     // by sequence, heads fastest) and the surplus, at the end of the grid,
     // exits at once, instead of idle workgroups spread through the grid each
     // holding a slot for a length read.
@@ -330,6 +330,19 @@ __device__ __forceinline__ void block_exclusive_scan(const int32_t* v, int64_t* 
     }
     if (tid == kThreads - 1) pre[n] = run;
     __syncthreads();
+}
+
+// Splits of a sequence attending L rows in the grid form (rows of STEP per
+// workgroup step): the rows after the shared prefix (all rows [0, L) when L is
+// below it) in spans of about span_tokens, at least one and at most
+// num_splits; an empty sequence keeps one workgroup for its zero output.
+__device__ __forceinline__ int grid_splits(const AttnArgs& a, int L, int step_rows) {
+    if (L <= 0) return 1;
+    const bool below_prefix = L < a.row_start;
+    const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
+    const int total_steps = (L - t_lo + step_rows - 1) / step_rows;
+    const int span_steps = max(1, a.span_tokens / step_rows);
+    return max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
 }
 
 // One decode-attention work item: rows [t_begin, t_end) of (sequence b, KV
@@ -1063,7 +1076,6 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     if (a.compact) {
         __shared__ int32_t s_splits[kThreads];      // splits of each sequence
         __shared__ int64_t s_first[kThreads + 1];   // exclusive prefix: its first split
-        const int span_steps = max(1, a.span_tokens / STEP);
         if (tid < a.batch) {
             int Lb;
             if constexpr (FUSED) {  // the length the fused step attends (0: out of range)
@@ -1075,11 +1087,9 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
             } else {
                 Lb = min(a.seq_lens ? a.seq_lens[tid] : a.seq_len_host, a.max_seq_len);
             }
-            // as below (no shared prefix): n_active splits; an empty or
-            // out-of-range sequence keeps one for its zero output / status
-            const int steps = Lb > 0 ? (Lb + STEP - 1) / STEP : 0;
-            s_splits[tid] = Lb > 0 ? max(1, min(a.num_splits, (steps + span_steps - 1) / span_steps))
-                                   : 1;
+            // an out-of-range fused append keeps one workgroup (per head) that
+            // reports it, as an empty sequence keeps one for its zero output
+            s_splits[tid] = grid_splits(a, Lb, STEP);
         }
         __syncthreads();
         block_exclusive_scan(s_splits, s_first, a.batch);
@@ -1132,8 +1142,7 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     const int pre_used = below_prefix ? 0 : a.pre_records;  // prefix records this (b, h) merges
     const int t_lo = below_prefix ? 0 : min(a.row_start, L - 1);
     const int total_steps = (L - t_lo + STEP - 1) / STEP;
-    const int span_steps = max(1, a.span_tokens / STEP);
-    const int n_active = max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
+    const int n_active = grid_splits(a, L, STEP);
     if (split >= n_active) return;
     const int step_begin = int(int64_t(split) * total_steps / n_active);
     const int step_end = int(int64_t(split + 1) * total_steps / n_active);
@@ -1929,6 +1938,9 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     a.pre_records = pre;
     a.rec_stride = rec_stride;
     a.batch = batch;
+    // (Only batched launches without a shared prefix: the shared-prefix form's
+    // short suffix splits measured slower with the length scan, configs[3]
+    // 55.2 against 51.9 us.)
     a.compact = span == kBatchSpan && pre == 0 && batch <= kThreads;
     const int64_t grid = int64_t(batch) * num_splits * nkv;
     if (grid > INT32_MAX) return AF_ERR_UNSUPPORTED;
