@@ -69,6 +69,9 @@ PROTOTYPES = {
     "af_prefill_attention": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, P]),
     "af_tiled_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
     "af_paged_prefill_attention": (I, [P, I, P, I, P, I, I, I, I, P, I, I, P]),
+    "af_prefill_attention_ws": (I, [P, I, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ, P]),
+    "af_paged_prefill_attention_ws": (I, [P, I, P, I, P, I, I, I, I, P, I, I, I, P, SZ, P]),
+    "af_prefill_workspace_size": (SZ, [I, I, I, I, I]),
     "af_paged_prefill_attention_batched": (I, [P, I, P, I, P, I, P, P, I, P, I, I, P]),
     "af_prefill_tile_map": (I, [P, I, P, I]),
     "af_weights_open": (I, [ctypes.c_char_p, P]),

@@ -42,6 +42,13 @@
 //    XCDs, so each XCD's L2 serves one KV head when n_kv_heads divides 8), then
 //    Q head, then query tile heaviest first; waves skip key tiles that lie wholly
 //    above their queries' diagonal.
+//  * Key pieces (the _ws entry points): a causal chunk's query tiles carry
+//    unequal work (tile t attends about p0 + 128(t+1) keys), and a short prompt
+//    has too few workgroups to keep the device busy while its heaviest tiles
+//    finish. Tiles with more key tiles than their share of the device's
+//    workgroup slots are cut into up to four key ranges, one workgroup each;
+//    every piece publishes its unnormalised (o, m, l), and the last piece of the
+//    (tile, Q head) to arrive merges them in piece order.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -60,6 +67,9 @@ constexpr int kPfKeys = 64;                      // keys per LDS tile
 constexpr int kTileBytes = kPfKeys * kPfHd * 2;  // one K or V tile: 64 rows of 256 B
 constexpr float kPfSumLimit = 256.0f;  // per-lane tile row sum that forces a rescale
 constexpr float kPfEmptyMax = -1e30f;
+constexpr int kPfQueries = 32 * kPfWaves;  // queries per workgroup (query tile)
+constexpr int kPfMaxPieces = 4;            // key pieces per query tile
+constexpr int kPfMinPieceTiles = 12;       // 64-key tiles per piece, at least
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -116,6 +126,19 @@ struct PrefillArgs {
     const float* sin_t;
     const int32_t* positions;
     int32_t max_pos;
+    // Key pieces (n_pieces > 1; single chunk, no tile map, no partials): query
+    // tile t's key tiles are cut into min(n_pieces, ceil(tiles / piece_units))
+    // balanced ranges, workgroup id / (n_kv_heads * group) % n_pieces being the
+    // piece. A piece leaves its unnormalised output in
+    //   rec_o [tile][q head][piece][128 x 128] (in the lanes' register order)
+    //   rec_ml[tile][q head][piece][2][128 queries] = (m, l), m in log2 units
+    // and takes counters[tile * n_q_heads + q head]; the last arrival merges the
+    // pieces into the output and re-zeroes the counter.
+    int32_t n_pieces;
+    int32_t piece_units;
+    float* rec_o;
+    float* rec_ml;
+    uint32_t* counters;
 };
 
 // Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a K tile.
@@ -270,6 +293,129 @@ __device__ __forceinline__ float dot2_sum(const half8& h, float acc) {
 // LDS: K tiles at [0, 2*kTileBytes), V tiles after them.
 constexpr int kVBase = 2 * kTileBytes;
 
+__device__ __forceinline__ void store_agent2(uint64_t* p, float x, float y) {
+    const auto u = [](float f) { return uint64_t(__builtin_bit_cast(uint32_t, f)); };
+    __hip_atomic_store(p, u(x) | (u(y) << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 load_agent2(const uint64_t* p) {
+    const uint64_t a = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__builtin_bit_cast(float, uint32_t(a)), __builtin_bit_cast(float, uint32_t(a >> 32)));
+}
+
+// End of a key piece: publish (o, m, l) of this workgroup's queries, arrive at
+// the (tile, Q head) counter, and, in the last piece to arrive, merge every
+// piece in piece order (own piece from registers: the bits it stored) and write
+// the output. Publication relies on gfx950 rules, not on the language's
+// relaxed atomics: agent-scope stores (sc1) write through to where every XCD
+// reads; s_waitcnt vmcnt(0) covers stores on gfx9, so each wave's records are
+// acknowledged before the barrier; the barrier orders them before the one
+// returning agent-scope atomic; the merging workgroup's agent-scope loads are
+// issued after the barrier that publishes that atomic's result. Lane (col, hi)
+// holds query t0 + 32 wave + col at dims 32 db + 8 (r / 4) + 4 hi + r % 4 of
+// o[db][r], and m / l of its query (the same in lanes col and col + 32). A
+// piece's o record is kept in that register order, o[db][2i .. 2i+1] of lane l
+// of wave w at 64-bit word (w * 32 + db * 8 + i) * 64 + l, so each store and
+// load instruction covers 512 contiguous bytes; the merging workgroup's lanes
+// hold the same queries and dims.
+__device__ __forceinline__ void merge_pieces(const PrefillArgs& a, float16v (&o)[4], float m_run,
+                                          float l_run, int tile, int head, int piece, int pieces,
+                                          int t0, int wq0, bool wave_live, float v_scale) {
+    __shared__ uint32_t s_arrived;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int col = lane & 31, hi = lane >> 5;
+    const int qi = wq0 + col;
+    const bool valid = wave_live && qi < a.n;
+    const float l_sum = halves_sum(l_run);
+    const int qrow = qi - t0;  // 0 .. 127
+    const size_t grp = size_t(tile) * a.n_q_heads + head;
+    const size_t rec0 = grp * a.n_pieces;
+    constexpr size_t kRecO = size_t(kPfQueries) * kPfHd, kRecMl = 2 * kPfQueries;
+    // this lane's first 64-bit word in a piece's o record
+    const size_t lane_word = size_t(tid >> 6) * 32 * 64 + lane;
+    if (valid) {
+        uint64_t* ro = reinterpret_cast<uint64_t*>(a.rec_o + (rec0 + piece) * kRecO) + lane_word;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                store_agent2(ro + (db * 8 + i) * 64, o[db][2 * i], o[db][2 * i + 1]);
+        if (hi == 0) {
+            float* ml = a.rec_ml + (rec0 + piece) * kRecMl;
+            __hip_atomic_store(ml + qrow, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ml + kPfQueries + qrow, l_sum, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        s_arrived = __hip_atomic_fetch_add(a.counters + grp, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != uint32_t(pieces - 1)) return;
+    if (tid == 0) __hip_atomic_store(a.counters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!valid) return;
+    float mp[kPfMaxPieces], lp[kPfMaxPieces];
+#pragma unroll
+    for (int p = 0; p < kPfMaxPieces; ++p) {
+        mp[p] = kPfEmptyMax;
+        lp[p] = 0.0f;
+        if (p < pieces) {
+            if (p == piece) {
+                mp[p] = m_run;
+                lp[p] = l_sum;
+            } else {
+                const float* ml = a.rec_ml + (rec0 + p) * kRecMl;
+                mp[p] = __hip_atomic_load(ml + qrow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                lp[p] = __hip_atomic_load(ml + kPfQueries + qrow, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    float mx = mp[0];
+#pragma unroll
+    for (int p = 1; p < kPfMaxPieces; ++p) mx = fmaxf(mx, mp[p]);
+    float wp[kPfMaxPieces], lt = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kPfMaxPieces; ++p) {
+        wp[p] = p < pieces ? fast_exp2(mp[p] - mx) : 0.0f;  // 0 for a piece without keys
+        lt = fmaf(wp[p], lp[p], lt);
+    }
+    const float inv = v_scale / lt;
+    uint16_t* orow = a.out + size_t(qi) * a.out_stride + size_t(head) * kPfHd + 4 * hi;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        float16v acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kPfMaxPieces; ++p) {
+            if (p >= pieces) continue;
+            if (p == piece) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = fmaf(wp[p], o[db][r], acc[r]);
+            } else {
+                const uint64_t* src = reinterpret_cast<const uint64_t*>(a.rec_o + (rec0 + p) * kRecO) +
+                                      lane_word + db * 8 * 64;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float2 x = load_agent2(src + i * 64);
+                    acc[2 * i] = fmaf(wp[p], x.x, acc[2 * i]);
+                    acc[2 * i + 1] = fmaf(wp[p], x.y, acc[2 * i + 1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint2 w;
+            w.x = uint32_t(f2h(acc[4 * g] * inv)) | (uint32_t(f2h(acc[4 * g + 1] * inv)) << 16);
+            w.y = uint32_t(f2h(acc[4 * g + 2] * inv)) | (uint32_t(f2h(acc[4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) = w;
+        }
+    }
+}
+
 template <bool PAGED, bool FP8>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const PrefillArgs args) {
     PrefillArgs a = args;
@@ -284,7 +430,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     // heaviest first.
     const int group = a.n_q_heads / a.n_kv_heads;
     int bid = int(blockIdx.x);
-    int ks = 0;  // key split (shared-prefix partials)
+    int ks = 0;     // key split (shared-prefix partials)
+    int piece = 0;  // key piece
     if (a.part_o) {
         const int per = a.n_tiles * a.n_q_heads;
         ks = bid / per;
@@ -306,6 +453,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
         a.q += size_t(row0) * a.q_stride;
         a.out += size_t(row0) * a.out_stride;
         a.table += size_t(c) * a.max_blocks;
+    } else if (a.n_pieces > 1) {  // key pieces: the pieces of a tile are adjacent
+        const int r2 = rest / group;
+        piece = r2 % a.n_pieces;
+        tile = a.n_tiles - 1 - r2 / a.n_pieces;
     } else {
         tile = a.n_tiles - 1 - rest / group;
     }
@@ -320,6 +471,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
         const int all = n_kt;
         kt_lo = ks * all / a.key_splits;
         n_kt = (ks + 1) * all / a.key_splits;
+    }
+    int pieces = 1;  // workgroup-uniform
+    if (a.n_pieces > 1) {
+        const int all = n_kt;
+        pieces = min(a.n_pieces, (all + a.piece_units - 1) / a.piece_units);
+        if (piece >= pieces) return;  // a lighter tile needs fewer pieces
+        kt_lo = piece * all / pieces;
+        n_kt = (piece + 1) * all / pieces;
     }
     // Keys the wave needs.
     const int w_keys = wave_live ? min(a.p0 + min(wq0 + 32, a.n), a.kv_len) : 0;
@@ -548,6 +707,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     }
     if (kt < n_kt) step(kt, std::integral_constant<int, 0>{});
 
+    if (pieces > 1) {
+        merge_pieces(a, o, m_run, l_run, tile, head, piece, pieces, t0, wq0, wave_live, v_scale);
+        return;
+    }
     if (!wave_live) return;
     const int qi = wq0 + col;
     const float l_sum = halves_sum(l_run);
@@ -588,7 +751,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 int launch_prefill(PrefillArgs a, hipStream_t stream) {
     a.n_tiles = ceil_div(a.n, 32 * kPfWaves);
-    const dim3 grid(a.n_tiles * a.n_q_heads), block(kPfThreads);
+    const dim3 grid(a.n_tiles * a.n_q_heads * std::max(a.n_pieces, 1)), block(kPfThreads);
     if (a.scales)
         hipLaunchKernelGGL((prefill_attention_kernel<true, true>), grid, block, 0, stream, a);
     else if (a.table)
@@ -642,15 +805,77 @@ int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream) {
     return AF_OK;
 }
 
+// Key pieces of one chunk. Only a chunk whose plain grid (query tiles x Q heads)
+// has fewer workgroups than the device has slots (two per CU) is cut: a grid
+// that fills the device is already balanced by its heaviest-first order, and
+// cutting it only adds record traffic (MI355X: a 4096-token prompt 129 -> 143
+// us). Its work (64-key tiles x Q heads) is spread over the slots: a query tile
+// with more key tiles than one slot's share is cut into pieces of about that
+// share (at least kPfMinPieceTiles tiles each: shorter pieces cost more in
+// set-up and merge than they gain; at most max_pieces per tile). Returns the
+// most pieces of any tile (1: no cut) and the tiles per piece in *units.
+int plan_pieces(int p0, int n, int kv_len, int n_q_heads, int max_pieces, int* units) {
+    *units = 0;
+    const int nt = ceil_div(n, kPfQueries);
+    if (n <= 0 || max_pieces <= 1 || int64_t(nt) * n_q_heads > kMaxCounters) return 1;
+    int64_t work = 0;
+    int most = 0;
+    for (int t = 0; t < nt; ++t) {
+        const int keys = std::min(p0 + std::min((t + 1) * kPfQueries, n), kv_len);
+        const int u = ceil_div(std::max(keys, 1), kPfKeys);
+        work += u;
+        most = std::max(most, u);
+    }
+    work *= n_q_heads;
+    const int64_t slots = 2 * int64_t(device_compute_units());
+    if (int64_t(nt) * n_q_heads >= slots) return 1;
+    const int per = int(std::max<int64_t>(kPfMinPieceTiles, (work + slots - 1) / slots));
+    const int pieces = std::min(std::min(max_pieces, kPfMaxPieces), ceil_div(most, per));
+    if (pieces <= 1) return 1;
+    *units = per;
+    return pieces;
+}
+
+// Workspace of a key-piece launch: the counter region of the attention
+// workspaces (zero between launches), then rec_ml, then rec_o.
+size_t piece_workspace_bytes(int n, int n_q_heads, int pieces) {
+    if (pieces <= 1) return kCounterBytes;
+    const size_t recs = size_t(ceil_div(n, kPfQueries)) * n_q_heads * pieces;
+    return kCounterBytes + align_up(recs * 2 * kPfQueries * sizeof(float), 256) +
+           recs * kPfQueries * kPfHd * sizeof(float);
+}
+
+// Sets a's key pieces (key_pieces: 0 = plan_pieces' choice, 1 = none, else at
+// most that many), checking the workspace.
+int set_pieces(PrefillArgs& a, int key_pieces, void* workspace, size_t workspace_bytes) {
+    if (key_pieces < 0 || key_pieces > kPfMaxPieces) return AF_ERR_INVALID_ARG;
+    int units = 0;
+    const int pieces = plan_pieces(a.p0, a.n, a.kv_len, a.n_q_heads,
+                                   key_pieces == 0 ? kPfMaxPieces : key_pieces, &units);
+    a.n_pieces = pieces;
+    a.piece_units = units;
+    if (pieces <= 1) return AF_OK;
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) ||
+        workspace_bytes < piece_workspace_bytes(a.n, a.n_q_heads, pieces))
+        return AF_ERR_WORKSPACE;
+    char* w = static_cast<char*>(workspace);
+    const size_t recs = size_t(ceil_div(a.n, kPfQueries)) * a.n_q_heads * pieces;
+    a.counters = reinterpret_cast<uint32_t*>(w);
+    a.rec_ml = reinterpret_cast<float*>(w + kCounterBytes);
+    a.rec_o = reinterpret_cast<float*>(w + kCounterBytes +
+                                       align_up(recs * 2 * kPfQueries * sizeof(float), 256));
+    return AF_OK;
+}
+
 }  // namespace af
 
 using namespace af;
 
 // ---- b2 -----------------------------------------------------------------------
-extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_cache,
-                                    const void* v_cache, void* out, int out_stride, int p0, int n,
-                                    int kv_len, int max_seq, int n_q_heads, int n_kv_heads,
-                                    int head_dim, af_stream_t stream) {
+static int prefill_contig(const void* q, int q_stride, const void* k_cache, const void* v_cache,
+                          void* out, int out_stride, int p0, int n, int kv_len, int max_seq,
+                          int n_q_heads, int n_kv_heads, int head_dim, int key_pieces,
+                          void* workspace, size_t workspace_bytes, af_stream_t stream) {
     if (!q || !k_cache || !v_cache || !out || n < 0 || p0 < 0 || n_q_heads <= 0 ||
         n_kv_heads <= 0 || n_q_heads % n_kv_heads || max_seq <= 0)
         return AF_ERR_INVALID_ARG;
@@ -679,13 +904,43 @@ extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_c
     a.n_q_heads = n_q_heads;
     a.n_kv_heads = n_kv_heads;
     a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(head_dim)));
+    if (int st = set_pieces(a, key_pieces, workspace, workspace_bytes)) return st;
     return launch_prefill(a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* pool,
-                                          int layer, const int32_t* d_block_table,
-                                          int max_blocks, int p0, int n, int kv_len, void* out,
-                                          int out_stride, int n_q_heads, af_stream_t stream) {
+extern "C" int af_prefill_attention(const void* q, int q_stride, const void* k_cache,
+                                    const void* v_cache, void* out, int out_stride, int p0, int n,
+                                    int kv_len, int max_seq, int n_q_heads, int n_kv_heads,
+                                    int head_dim, af_stream_t stream) {
+    return prefill_contig(q, q_stride, k_cache, v_cache, out, out_stride, p0, n, kv_len, max_seq,
+                          n_q_heads, n_kv_heads, head_dim, 1, nullptr, 0, stream);
+}
+
+extern "C" int af_prefill_attention_ws(const void* q, int q_stride, const void* k_cache,
+                                       const void* v_cache, void* out, int out_stride, int p0,
+                                       int n, int kv_len, int max_seq, int n_q_heads,
+                                       int n_kv_heads, int head_dim, int key_pieces,
+                                       void* workspace, size_t workspace_bytes,
+                                       af_stream_t stream) {
+    return prefill_contig(q, q_stride, k_cache, v_cache, out, out_stride, p0, n, kv_len, max_seq,
+                          n_q_heads, n_kv_heads, head_dim, key_pieces, workspace, workspace_bytes,
+                          stream);
+}
+
+extern "C" size_t af_prefill_workspace_size(int p0, int n, int kv_len, int n_q_heads,
+                                            int key_pieces) {
+    if (p0 < 0 || n < 0 || n_q_heads <= 0 || key_pieces < 0 || key_pieces > kPfMaxPieces)
+        return 0;
+    int units = 0;
+    const int pieces = plan_pieces(p0, n, kv_len, n_q_heads,
+                                   key_pieces == 0 ? kPfMaxPieces : key_pieces, &units);
+    return piece_workspace_bytes(n, n_q_heads, pieces);
+}
+
+static int prefill_paged(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                         const int32_t* d_block_table, int max_blocks, int p0, int n, int kv_len,
+                         void* out, int out_stride, int n_q_heads, int key_pieces, void* workspace,
+                         size_t workspace_bytes, af_stream_t stream) {
     if (!q || !pool || !pool->base || !d_block_table || !out || n < 0 || p0 < 0 ||
         n_q_heads <= 0 || max_blocks <= 0)
         return AF_ERR_INVALID_ARG;
@@ -726,7 +981,26 @@ extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_
     a.table = d_block_table;
     a.bs_log2 = __builtin_ctz(unsigned(bs));
     a.max_block = int32_t(std::min<int64_t>(pool->total_blocks - 1, INT32_MAX));
+    if (int st = set_pieces(a, key_pieces, workspace, workspace_bytes)) return st;
     return launch_prefill(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* pool,
+                                          int layer, const int32_t* d_block_table,
+                                          int max_blocks, int p0, int n, int kv_len, void* out,
+                                          int out_stride, int n_q_heads, af_stream_t stream) {
+    return prefill_paged(q, q_stride, pool, layer, d_block_table, max_blocks, p0, n, kv_len, out,
+                         out_stride, n_q_heads, 1, nullptr, 0, stream);
+}
+
+extern "C" int af_paged_prefill_attention_ws(const void* q, int q_stride, const af_kv_pool* pool,
+                                             int layer, const int32_t* d_block_table,
+                                             int max_blocks, int p0, int n, int kv_len, void* out,
+                                             int out_stride, int n_q_heads, int key_pieces,
+                                             void* workspace, size_t workspace_bytes,
+                                             af_stream_t stream) {
+    return prefill_paged(q, q_stride, pool, layer, d_block_table, max_blocks, p0, n, kv_len, out,
+                         out_stride, n_q_heads, key_pieces, workspace, workspace_bytes, stream);
 }
 
 extern "C" int af_prefill_tile_map(const int32_t* h_chunks, int n_chunks, int32_t* h_tile_map,

@@ -123,6 +123,48 @@ def launch_paged_prefill_attention(q, q_stride, pool, layer, d_block_table, max_
           "launch_paged_prefill_attention")
 
 
+def _ws(workspace):
+    """(pointer, bytes) of a workspace object, or (None, 0)."""
+    return (None, 0) if workspace is None else (workspace.ptr, workspace.nbytes)
+
+
+class PrefillWorkspace:
+    """Key-piece workspace of one chunk shape (records + arrival counters),
+    zeroed once at creation; launches that share it must be ordered."""
+
+    def __init__(self, p0, n, kv_len, n_q_heads, key_pieces=0, stream=None):
+        self.nbytes = lib().af_prefill_workspace_size(p0, n, kv_len, n_q_heads, key_pieces)
+        if self.nbytes == 0:
+            raise AfError(-2, "af_prefill_workspace_size")
+        self.buf = DeviceBuffer(self.nbytes)
+        check(lib().af_attention_workspace_init(self.buf.ptr, self.nbytes, _s(stream)),
+              "af_attention_workspace_init")
+
+    @property
+    def ptr(self):
+        return self.buf.ptr
+
+
+def launch_prefill_attention_ws(q, q_stride, k_cache, v_cache, out, out_stride, p0, n, kv_len,
+                                max_seq, n_q_heads, n_kv_heads, head_dim, workspace, key_pieces=0,
+                                stream=None):
+    """launch_prefill_attention with heavy query tiles cut into key pieces."""
+    check(lib().af_prefill_attention_ws(_p(q), q_stride, _p(k_cache), _p(v_cache), _p(out),
+                                        out_stride, p0, n, kv_len, max_seq, n_q_heads, n_kv_heads,
+                                        head_dim, key_pieces, *_ws(workspace), _s(stream)),
+          "launch_prefill_attention_ws")
+
+
+def launch_paged_prefill_attention_ws(q, q_stride, pool, layer, d_block_table, max_blocks, p0, n,
+                                      kv_len, out, out_stride, n_q_heads, workspace, key_pieces=0,
+                                      stream=None):
+    """launch_paged_prefill_attention with heavy query tiles cut into key pieces."""
+    check(lib().af_paged_prefill_attention_ws(_p(q), q_stride, ctypes.byref(pool), layer,
+                                              _p(d_block_table), max_blocks, p0, n, kv_len, _p(out),
+                                              out_stride, n_q_heads, key_pieces, *_ws(workspace),
+                                              _s(stream)), "launch_paged_prefill_attention_ws")
+
+
 def prefill_tile_map(chunks):
     """(chunk, tile) pairs of the chunks [(p0, n, kv_len, row0), ...], heaviest first."""
     ch = np.ascontiguousarray(chunks, np.int32).reshape(-1, 4)

@@ -415,7 +415,10 @@ def prefill_flops(p0, n, kv_len):
 def bench_prefill(dev, kv, lib, stream, warmup, reps):
     """One layer of prefill: the ctx-8k prompt as one causal chunk, a 2048-token
     chunk at p0 = 6144 (contiguous cache and a bs-16 paged pool with a permuted
-    block table), and the 2048-row RoPE + append."""
+    block table), a 512-token chunk at p0 = 6144, and the 2048-row RoPE + append.
+    Attention runs through the key-piece entry points with the library's choice
+    of pieces (heavy query tiles of a chunk too small to fill the device are
+    cut into key ranges); the 512-token chunk is also timed uncut."""
     import atomflow_amd
     e0, e1 = dev.Event(), dev.Event()
 
@@ -441,13 +444,27 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     for i, b in enumerate((k, v, qkv)):
         randn(b, 0xA70F90 + i)
 
+    wss = {}
+
+    def ws(p0_, n_, kv_len_):  # key-piece workspace of one chunk shape
+        key = (p0_, n_, kv_len_)
+        if key not in wss:
+            wss[key] = kv.PrefillWorkspace(p0_, n_, kv_len_, NQ, 0, stream)
+        return wss[key]
+
+    def attn(p0_, n_, kv_len_):
+        w = ws(p0_, n_, kv_len_)
+        return lambda: kv.launch_prefill_attention_ws(qkv, QKV, k, v, out, Q_DIM, p0_, n_, kv_len_,
+                                                      LMAX, NQ, NKV, HD, w, stream=stream)
+
     def prompt(lp):  # an lp-token prompt as one causal chunk
-        return lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, 0, lp, lp, LMAX,
-                                                   NQ, NKV, HD, stream=stream)
+        return attn(0, lp, lp)
     full = prompt(L)
     p0, n = 6144, 2048
-    chunk = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, p0, n, p0 + n, LMAX,
-                                                NQ, NKV, HD, stream=stream)
+    chunk = attn(p0, n, p0 + n)
+    chunk512 = attn(p0, 512, p0 + 512)
+    chunk512_plain = lambda: kv.launch_prefill_attention(qkv, QKV, k, v, out, Q_DIM, p0, 512,
+                                                         p0 + 512, LMAX, NQ, NKV, HD, stream=stream)
     bs = 16
     nblocks = L // bs
     pool_buf = dev.DeviceBuffer(2 * nblocks * bs * KV_DIM * 2)
@@ -455,30 +472,35 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     pool = kv.make_pool(pool_buf, atomflow_amd.AF_KV_FP16, bs, 1, NKV, HD, nblocks)
     table = dev.DeviceBuffer.from_array(
         np.random.default_rng(0xA70F94).permutation(nblocks).astype(np.int32))
-    paged = lambda: kv.launch_paged_prefill_attention(qkv, QKV, pool, 0, table, nblocks, p0, n,
-                                                      p0 + n, out, Q_DIM, NQ, stream=stream)
+    paged = lambda: kv.launch_paged_prefill_attention_ws(qkv, QKV, pool, 0, table, nblocks, p0, n,
+                                                         p0 + n, out, Q_DIM, NQ, ws(p0, n, p0 + n),
+                                                         stream=stream)
     pool8_buf = dev.DeviceBuffer(2 * nblocks * bs * KV_DIM)
     atomflow_amd.check(lib.af_rt_fill_randn_fp8(pool8_buf.ptr, pool8_buf.nbytes, 0xA70F95, 20.0,
                                                 stream.handle))
     scales8 = dev.DeviceBuffer.from_array(np.full(2 * NKV, 0.05, np.float32))
     pool8 = kv.make_pool(pool8_buf, atomflow_amd.AF_KV_FP8_E4M3, bs, 1, NKV, HD, nblocks, scales8)
-    paged8 = lambda: kv.launch_paged_prefill_attention(qkv, QKV, pool8, 0, table, nblocks, p0, n,
-                                                       p0 + n, out, Q_DIM, NQ, stream=stream)
+    paged8 = lambda: kv.launch_paged_prefill_attention_ws(qkv, QKV, pool8, 0, table, nblocks, p0,
+                                                          n, p0 + n, out, Q_DIM, NQ,
+                                                          ws(p0, n, p0 + n), stream=stream)
     cos = dev.DeviceBuffer(L * (HD // 2) * 4)
     sin = dev.DeviceBuffer(L * (HD // 2) * 4)
     kv.build_rope_cache(cos, sin, L, HD, THETA)
     append = lambda: kv.launch_prefill_rope_append(qkv, n, k, v, cos, sin, p0, L, NQ, NKV, HD,
                                                    stream=stream)
-    us_full, us_chunk, us_paged, us_paged8, us_app, us_2k, us_16k = (
-        time_us(f) for f in (full, chunk, paged, paged8, append, prompt(2048), prompt(LMAX)))
+    us_full, us_chunk, us_paged, us_paged8, us_app, us_2k, us_16k, us_512, us_512p = (
+        time_us(f) for f in (full, chunk, paged, paged8, append, prompt(2048), prompt(LMAX),
+                             chunk512, chunk512_plain))
     tf = lambda fl, us: fl / (us * 1e-6) / 1e12
     f_full, f_chunk = prefill_flops(0, L, L), prefill_flops(p0, n, p0 + n)
     f_2k, f_16k = prefill_flops(0, 2048, 2048), prefill_flops(0, LMAX, LMAX)
+    f_512 = prefill_flops(p0, 512, p0 + 512)
     app_bytes = n * (QKV * 2 * 2 + 2 * KV_DIM * 2)  # qkv rows read + written, K/V rows written
     res = {
         "workload": "one layer, 24 Q / 8 KV heads x 128, fp16: 2048-, 8192- and 16384-token "
                     "prompts, each as one causal chunk; 2048-token chunk at p0 6144 (contiguous, paged bs 16 with a "
-                    "permuted block table, fp16 and FP8-E4M3 pools); 2048-row RoPE + append",
+                    "permuted block table, fp16 and FP8-E4M3 pools); 512-token chunk at p0 6144 "
+                    "with and without key pieces; 2048-row RoPE + append",
         "attn_8k_us": round(us_full, 1), "attn_8k_tflops": round(tf(f_full, us_full), 1),
         "attn_2k_us": round(us_2k, 1), "attn_2k_tflops": round(tf(f_2k, us_2k), 1),
         "attn_16k_us": round(us_16k, 1), "attn_16k_tflops": round(tf(f_16k, us_16k), 1),
@@ -488,6 +510,9 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
         "paged_chunk_2k_at_6k_tflops": round(tf(f_chunk, us_paged), 1),
         "paged_fp8_chunk_2k_at_6k_us": round(us_paged8, 1),
         "paged_fp8_chunk_2k_at_6k_tflops": round(tf(f_chunk, us_paged8), 1),
+        "chunk_512_at_6k_us": round(us_512, 1), "chunk_512_at_6k_tflops": round(tf(f_512, us_512), 1),
+        "chunk_512_at_6k_uncut_us": round(us_512p, 1),
+        "chunk_512_at_6k_uncut_tflops": round(tf(f_512, us_512p), 1),
         "rope_append_2k_us": round(us_app, 2),
         "rope_append_2k_gbs": round(app_bytes / (us_app * 1e-6) / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(tf(f_full, us_full), 1),
@@ -496,6 +521,8 @@ def bench_prefill(dev, kv, lib, stream, warmup, reps):
     }
     for b in (k, v, qkv, out, pool_buf, pool8_buf, scales8, table, cos, sin):
         b.free()
+    for w in wss.values():
+        w.buf.free()
     return res
 
 

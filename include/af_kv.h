@@ -381,6 +381,33 @@ int af_paged_prefill_attention(const void* q, int q_stride, const af_kv_pool* po
                                int kv_len, void* out, int out_stride, int n_q_heads,
                                af_stream_t stream);
 
+/* af_prefill_attention / af_paged_prefill_attention with key pieces (same
+ * arguments, results and rules; no counterpart in the reference). A chunk's
+ * query tiles (128 queries) attend unequal key ranges under the causal mask;
+ * a tile with more key tiles (64 keys) than one workgroup slot's share of the
+ * chunk's work is cut into up to four key ranges, each a workgroup, and the
+ * last of them to finish merges the pieces (online-softmax merge in piece
+ * order, so the output does not depend on which finishes last). key_pieces:
+ * 0 = the library's choice, 1 = no cut (bit-identical to the entry points
+ * above), 2..4 = at most that many pieces per tile. workspace: at least
+ * af_prefill_workspace_size(p0, n, kv_len, n_q_heads, key_pieces) bytes,
+ * 256-B aligned, zero-filled once by af_attention_workspace_init (each launch
+ * leaves its counters at zero); launches sharing a workspace must be ordered
+ * (one stream). AF_ERR_WORKSPACE if it is missing or too small when a cut is
+ * planned. */
+int af_prefill_attention_ws(const void* q, int q_stride, const void* k_cache, const void* v_cache,
+                            void* out, int out_stride, int p0, int n, int kv_len, int max_seq,
+                            int n_q_heads, int n_kv_heads, int head_dim, int key_pieces,
+                            void* workspace, size_t workspace_bytes, af_stream_t stream);
+int af_paged_prefill_attention_ws(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                                  const int32_t* d_block_table, int max_blocks, int p0, int n,
+                                  int kv_len, void* out, int out_stride, int n_q_heads,
+                                  int key_pieces, void* workspace, size_t workspace_bytes,
+                                  af_stream_t stream);
+/* Workspace bytes of the _ws prefill entry points for one chunk (0 on bad
+ * arguments). */
+size_t af_prefill_workspace_size(int p0, int n, int kv_len, int n_q_heads, int key_pieces);
+
 /* Several chunks (of different sequences) in one launch, the per-layer form of a
  * serving step's chunked prefill. d_chunks: device int32 [n_chunks][4] =
  * (p0, n, kv_len, row0): chunk c's queries are rows row0 .. row0+n-1 of q and out;

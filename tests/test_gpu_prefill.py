@@ -141,6 +141,73 @@ def test_prefill_attention_long_chunks(gpu, p0, n, kv_len):
         assert_attn_close(got[i], ref, what=f"row {i} (L={L})")
 
 
+# ---- key pieces: heavy query tiles cut into key ranges, merged by the last ------
+def run_prefill_ws(q, k, v, p0, n, kv_len, q_stride, key_pieces, ws=None, out_stride=Q_DIM):
+    d_q, d_k, d_v = up(q), up(k), up(v)
+    d_o = up(np.full((n, out_stride), np.float16(3.0)))
+    if ws is None:
+        ws = kv.PrefillWorkspace(p0, n, kv_len, NQ, key_pieces)
+    kv.launch_prefill_attention_ws(d_q, q_stride, d_k, d_v, d_o, out_stride, p0, n, kv_len,
+                                   k.shape[0], NQ, NKV, HD, ws, key_pieces=key_pieces)
+    return d_o.download(np.float16, (n, out_stride)), ws
+
+
+@pytest.mark.parametrize("p0,n,kv_len,key_pieces", [
+    (0, 2048, 2048, 0),      # a 2k prompt: tiles cut into up to 3 pieces
+    (3000, 300, 3300, 0),    # a chunk late in a prompt: 4 pieces per tile
+    (0, 700, 700, 2),        # 2 pieces, a partial last tile
+    (2000, 333, 2200, 3),    # queries past kv_len, a partial last wave
+    (0, 200, 200, 0)])       # too little work to cut: the plain launch
+def test_prefill_attention_key_pieces_vs_oracle(gpu, p0, n, kv_len, key_pieces):
+    """Every row against the float64 decode oracle over min(p0+i+1, kv_len) rows
+    (sampled for the 2k prompt); a second launch on the same workspace (its
+    counters re-zeroed by the first) gives the same bits."""
+    say(f"prefill key pieces p0={p0} n={n} kv_len={kv_len} key_pieces={key_pieces}")
+    max_seq = max(kv_len, p0 + n) + 3
+    q = randn_f16((n, QKV), 0xA70F90 + n + p0)
+    k, v = caches(max_seq, kv_len, 0xA70F91 + kv_len)
+    got, ws = run_prefill_ws(q, k, v, p0, n, kv_len, QKV, key_pieces, out_stride=Q_DIM + 64)
+    assert np.all(got[:, Q_DIM:] == np.float16(3.0))  # nothing past the row's heads
+    got = got[:, :Q_DIM]
+    edge = {0, 127, 128, 1000, n - 129, n - 1}
+    rows = range(n) if n <= 400 else sorted(
+        set(rng(n).choice(n, 40, replace=False).tolist()) | {i for i in edge if 0 <= i < n})
+    for i in rows:
+        L = min(p0 + i + 1, kv_len)
+        ref = oracle.cached_attention_f64(q[i, :Q_DIM], k, v, L, NQ, NKV, HD)
+        assert_attn_close(got[i], ref, what=f"row {i} (L={L})")
+    again, _ = run_prefill_ws(q, k, v, p0, n, kv_len, QKV, key_pieces, ws=ws,
+                              out_stride=Q_DIM + 64)
+    assert np.array_equal(bits(again[:, :Q_DIM]), bits(got))
+
+
+def test_prefill_attention_one_piece_equals_plain(gpu):
+    say("prefill key_pieces=1 == af_prefill_attention bit for bit; workspace checks")
+    p0, n, kv_len = 0, 1024, 1024
+    q = randn_f16((n, Q_DIM), 0xA70F95)
+    k, v = caches(kv_len, kv_len, 0xA70F96)
+    plain = run_prefill(q, k, v, p0, n, kv_len, Q_DIM)
+    one, _ = run_prefill_ws(q, k, v, p0, n, kv_len, Q_DIM, 1)
+    assert np.array_equal(bits(one), bits(plain))
+    lib = atomflow_amd.lib()
+    assert lib.af_prefill_workspace_size(p0, n, kv_len, NQ, 1) == 64 * 1024
+    big = lib.af_prefill_workspace_size(p0, n, kv_len, NQ, 0)
+    assert big > 64 * 1024
+    d_q, d_k, d_v = up(q), up(k), up(v)
+    d_o = up(np.zeros((n, Q_DIM), np.float16))
+    small = kv.PrefillWorkspace(p0, n, kv_len, NQ, 1)  # counters only
+    with pytest.raises(atomflow_amd.AfError) as e:
+        kv.launch_prefill_attention_ws(d_q, Q_DIM, d_k, d_v, d_o, Q_DIM, p0, n, kv_len, kv_len,
+                                       NQ, NKV, HD, small, key_pieces=0)
+    assert e.value.status == atomflow_amd.AF_ERR_WORKSPACE
+    with pytest.raises(atomflow_amd.AfError):
+        kv.launch_prefill_attention_ws(d_q, Q_DIM, d_k, d_v, d_o, Q_DIM, p0, n, kv_len, kv_len,
+                                       NQ, NKV, HD, None, key_pieces=0)
+    with pytest.raises(atomflow_amd.AfError):
+        kv.launch_prefill_attention_ws(d_q, Q_DIM, d_k, d_v, d_o, Q_DIM, p0, n, kv_len, kv_len,
+                                       NQ, NKV, HD, small, key_pieces=5)
+
+
 def test_prefill_attention_large_scores(gpu):
     say("prefill_attention: scaled inputs (scores up to ~100), lazy rescale path")
     p0, n, kv_len = 0, 160, 160
@@ -372,6 +439,46 @@ def test_paged_prefill_attention_fp8_pool(gpu, bs, p0, n, kv_len):
             p = np.exp(sc - sc.max())
             out[h] = p @ vf[:L, g] / p.sum()
         assert_attn_close(got[i], out.ravel(), ATOL_FP8, RTOL_FP8, what=f"row {i} vs float64")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_prefill_key_pieces_vs_oracle(gpu, fp8):
+    """Paged fp16 / FP8 pool, a chunk late in the prompt (4 pieces per tile):
+    every row against the paged decode oracle over min(p0+i+1, kv_len) rows."""
+    from inputs import ATOL_FP8, RTOL_FP8
+    bs, p0, n, kv_len = 16, 3000, 260, 3260
+    say(f"paged prefill key pieces fp8={fp8} bs={bs} p0={p0} n={n}")
+    layers, layer = 2, 1
+    max_blocks = (kv_len + bs - 1) // bs
+    nblocks = max_blocks + 5
+    r = rng(0xA70F98 + fp8)
+    table = r.permutation(nblocks)[:max_blocks].astype(np.int32)
+    q = randn_f16((n, QKV), 0xA70F99)
+    if fp8:
+        host = r.integers(0, 256, (layers, 2, nblocks * bs, KV_DIM), dtype=np.uint8)
+        host[(host & 0x7F) == 0x7F] = 0  # no NaN codes
+        scales = r.uniform(0.004, 0.02, (layers, 2, NKV)).astype(np.float32)
+        buf, d_scales = up(host), up(scales)
+        pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, d_scales)
+    else:
+        host, buf, pool = _paged_pool(bs, nblocks, layers, 0xA70F9A)
+    ws = kv.PrefillWorkspace(p0, n, kv_len, NQ, 0)
+    assert ws.nbytes > 64 * 1024  # the planner cuts this chunk
+    d_o = up(np.zeros((n, Q_DIM), np.float16))
+    kv.launch_paged_prefill_attention_ws(up(q), QKV, pool, layer, up(table), max_blocks, p0, n,
+                                         kv_len, d_o, Q_DIM, NQ, ws)
+    got = d_o.download(np.float16, (n, Q_DIM))
+    for i in range(n):
+        L = min(p0 + i + 1, kv_len)
+        if fp8:
+            ref = oracle.paged_attention_fp8(q[i, :Q_DIM], host[layer, 0], host[layer, 1],
+                                             scales[layer, 0], scales[layer, 1], table, L, bs, NQ,
+                                             NKV, HD)
+            assert_attn_close(got[i], ref, ATOL_FP8, RTOL_FP8, what=f"row {i}")
+        else:
+            ref = oracle.paged_attention_f16(q[i, :Q_DIM], host[layer, 0], host[layer, 1], table,
+                                             L, bs, NQ, NKV, HD)
+            assert_attn_close(got[i], ref, what=f"row {i}")
 
 
 @pytest.mark.parametrize("fp8", [False, True])
