@@ -74,6 +74,8 @@ PROTOTYPES = {
     "af_prefill_workspace_size": (SZ, [I, I, I, I, I]),
     "af_paged_prefill_attention_batched": (I, [P, I, P, I, P, I, P, P, I, P, I, I, P]),
     "af_prefill_tile_map": (I, [P, I, P, I]),
+    "af_prefill_piece_map": (I, [P, I, I, I, P, I, P, P, P]),
+    "af_paged_prefill_attention_batched_ws": (I, [P, I, P, I, P, I, P, P, I, I, I, P, I, I, P, SZ, P]),
     "af_weights_open": (I, [ctypes.c_char_p, P]),
     "af_weights_close": (I, [P]),
     "af_weights_layout_bytes": (SZ, [P]),

@@ -136,6 +136,10 @@ struct PrefillArgs {
     // pieces into the output and re-zeroes the counter.
     int32_t n_pieces;
     int32_t piece_units;
+    // Batched chunks with key pieces: tile_map entries are 4 ints, (chunk, tile,
+    // piece | pieces << 8, record group g); the pieces' records and counter
+    // are those of tile index g (as tile above), n_pieces the most pieces.
+    int32_t piece_map;
     float* rec_o;
     float* rec_ml;
     uint32_t* counters;
@@ -441,10 +445,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     const int rest = bid / a.n_kv_heads;
     const int head = kvh * group + rest % group;
     int tile;
+    int map_pieces = 0, rec_tile = 0;  // batched key pieces: from the map
     if (a.tile_map) {  // batched chunks: the host orders the tiles heaviest first
         const int tt = rest / group;
-        const int c = __builtin_amdgcn_readfirstlane(a.tile_map[2 * tt]);
-        tile = __builtin_amdgcn_readfirstlane(a.tile_map[2 * tt + 1]);
+        const int es = a.piece_map ? 4 : 2;
+        const int c = __builtin_amdgcn_readfirstlane(a.tile_map[es * tt]);
+        tile = __builtin_amdgcn_readfirstlane(a.tile_map[es * tt + 1]);
+        if (a.piece_map) {
+            const int pp = __builtin_amdgcn_readfirstlane(a.tile_map[4 * tt + 2]);
+            piece = pp & 0xff;
+            map_pieces = pp >> 8;
+            rec_tile = __builtin_amdgcn_readfirstlane(a.tile_map[4 * tt + 3]);
+        }
         const int32_t* ci = a.chunks + 4 * c;
         a.p0 = __builtin_amdgcn_readfirstlane(ci[0]);
         a.n = __builtin_amdgcn_readfirstlane(ci[1]);
@@ -475,7 +487,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     int pieces = 1;  // workgroup-uniform
     if (a.n_pieces > 1) {
         const int all = n_kt;
-        pieces = min(a.n_pieces, (all + a.piece_units - 1) / a.piece_units);
+        if (a.piece_map) {  // the host planned this tile's pieces (at most its key tiles)
+            pieces = min(map_pieces, all);
+        } else {
+            pieces = min(a.n_pieces, (all + a.piece_units - 1) / a.piece_units);
+            rec_tile = tile;
+        }
         if (piece >= pieces) return;  // a lighter tile needs fewer pieces
         kt_lo = piece * all / pieces;
         n_kt = (piece + 1) * all / pieces;
@@ -708,7 +725,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(const 
     if (kt < n_kt) step(kt, std::integral_constant<int, 0>{});
 
     if (pieces > 1) {
-        merge_pieces(a, o, m_run, l_run, tile, head, piece, pieces, t0, wq0, wave_live, v_scale);
+        merge_pieces(a, o, m_run, l_run, rec_tile, head, piece, pieces, t0, wq0, wave_live, v_scale);
         return;
     }
     if (!wave_live) return;
@@ -838,11 +855,24 @@ int plan_pieces(int p0, int n, int kv_len, int n_q_heads, int max_pieces, int* u
 
 // Workspace of a key-piece launch: the counter region of the attention
 // workspaces (zero between launches), then rec_ml, then rec_o.
-size_t piece_workspace_bytes(int n, int n_q_heads, int pieces) {
+size_t record_workspace_bytes(int groups, int n_q_heads, int pieces) {
     if (pieces <= 1) return kCounterBytes;
-    const size_t recs = size_t(ceil_div(n, kPfQueries)) * n_q_heads * pieces;
+    const size_t recs = size_t(groups) * n_q_heads * pieces;
     return kCounterBytes + align_up(recs * 2 * kPfQueries * sizeof(float), 256) +
            recs * kPfQueries * kPfHd * sizeof(float);
+}
+
+size_t piece_workspace_bytes(int n, int n_q_heads, int pieces) {
+    return record_workspace_bytes(ceil_div(n, kPfQueries), n_q_heads, pieces);
+}
+
+void carve_records(PrefillArgs& a, void* workspace, int groups, int pieces) {
+    char* w = static_cast<char*>(workspace);
+    const size_t recs = size_t(groups) * a.n_q_heads * pieces;
+    a.counters = reinterpret_cast<uint32_t*>(w);
+    a.rec_ml = reinterpret_cast<float*>(w + kCounterBytes);
+    a.rec_o = reinterpret_cast<float*>(w + kCounterBytes +
+                                       align_up(recs * 2 * kPfQueries * sizeof(float), 256));
 }
 
 // Sets a's key pieces (key_pieces: 0 = plan_pieces' choice, 1 = none, else at
@@ -858,12 +888,7 @@ int set_pieces(PrefillArgs& a, int key_pieces, void* workspace, size_t workspace
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) ||
         workspace_bytes < piece_workspace_bytes(a.n, a.n_q_heads, pieces))
         return AF_ERR_WORKSPACE;
-    char* w = static_cast<char*>(workspace);
-    const size_t recs = size_t(ceil_div(a.n, kPfQueries)) * a.n_q_heads * pieces;
-    a.counters = reinterpret_cast<uint32_t*>(w);
-    a.rec_ml = reinterpret_cast<float*>(w + kCounterBytes);
-    a.rec_o = reinterpret_cast<float*>(w + kCounterBytes +
-                                       align_up(recs * 2 * kPfQueries * sizeof(float), 256));
+    carve_records(a, workspace, ceil_div(a.n, kPfQueries), pieces);
     return AF_OK;
 }
 
@@ -1030,12 +1055,74 @@ extern "C" int af_prefill_tile_map(const int32_t* h_chunks, int n_chunks, int32_
     return int(tiles.size());
 }
 
-extern "C" int af_paged_prefill_attention_batched(
-    const void* q, int q_stride, const af_kv_pool* pool, int layer, const int32_t* d_tables,
-    int max_blocks, const int32_t* d_chunks, const int32_t* d_tile_map, int n_tiles, void* out,
-    int out_stride, int n_q_heads, af_stream_t stream) {
+extern "C" int af_prefill_piece_map(const int32_t* h_chunks, int n_chunks, int n_q_heads,
+                                    int key_pieces, int32_t* h_map, int max_entries, int* n_groups,
+                                    int* max_pieces, size_t* workspace_bytes) {
+    if (!h_chunks || !h_map || !n_groups || !max_pieces || !workspace_bytes || n_chunks < 0 ||
+        max_entries < 0 || n_q_heads <= 0 || key_pieces < 0 || key_pieces > kPfMaxPieces)
+        return AF_ERR_INVALID_ARG;
+    struct T {
+        int units, c, t, g, pieces;
+    };
+    std::vector<T> tiles;
+    int64_t work = 0;
+    for (int c = 0; c < n_chunks; ++c) {
+        const int p0 = h_chunks[4 * c], n = h_chunks[4 * c + 1], kv_len = h_chunks[4 * c + 2];
+        if (p0 < 0 || n < 0 || h_chunks[4 * c + 3] < 0) return AF_ERR_INVALID_ARG;
+        if (n > 0 && kv_len <= 0) return AF_ERR_OUT_OF_RANGE;
+        for (int t = 0; t * kPfQueries < n; ++t) {
+            const int keys = std::min(p0 + std::min((t + 1) * kPfQueries, n), kv_len);
+            const int u = ceil_div(std::max(keys, 1), kPfKeys);
+            tiles.push_back({u, c, t, int(tiles.size()), 1});
+            work += u;
+        }
+    }
+    // The rule of plan_pieces over the launch's tiles: cut only a grid that has
+    // fewer workgroups than the device has slots.
+    const int64_t slots = 2 * int64_t(device_compute_units());
+    const int cap = key_pieces == 0 ? kPfMaxPieces : key_pieces;
+    int most = 1;
+    if (cap > 1 && int64_t(tiles.size()) * n_q_heads < slots &&
+        int64_t(tiles.size()) * n_q_heads <= kMaxCounters) {
+        const int per = int(std::max<int64_t>(kPfMinPieceTiles,
+                                              (work * n_q_heads + slots - 1) / slots));
+        for (T& x : tiles) {
+            x.pieces = std::min(cap, ceil_div(x.units, per));
+            most = std::max(most, x.pieces);
+        }
+    }
+    // entries: every piece, heaviest piece first (a tile's pieces stay together)
+    std::stable_sort(tiles.begin(), tiles.end(), [](const T& x, const T& y) {
+        return int64_t(x.units) * y.pieces > int64_t(y.units) * x.pieces;
+    });
+    int n_entries = 0;
+    for (const T& x : tiles) n_entries += x.pieces;
+    if (n_entries > max_entries) return AF_ERR_WORKSPACE;
+    int e = 0;
+    for (const T& x : tiles)
+        for (int p = 0; p < x.pieces; ++p, ++e) {
+            h_map[4 * e] = x.c;
+            h_map[4 * e + 1] = x.t;
+            h_map[4 * e + 2] = p | (x.pieces << 8);
+            h_map[4 * e + 3] = x.g;
+        }
+    *n_groups = int(tiles.size());
+    *max_pieces = most;
+    *workspace_bytes = record_workspace_bytes(int(tiles.size()), n_q_heads, most);
+    return n_entries;
+}
+
+static int prefill_batched(const void* q, int q_stride, const af_kv_pool* pool, int layer,
+                           const int32_t* d_tables, int max_blocks, const int32_t* d_chunks,
+                           const int32_t* d_tile_map, int n_tiles, int n_groups, int max_pieces,
+                           void* out, int out_stride, int n_q_heads, void* workspace,
+                           size_t workspace_bytes, af_stream_t stream) {
+    const bool pieced = max_pieces > 0;  // a 4-int piece map
     if (!q || !pool || !pool->base || !d_tables || !d_chunks || !d_tile_map || !out ||
         n_tiles < 0 || n_q_heads <= 0 || max_blocks <= 0)
+        return AF_ERR_INVALID_ARG;
+    if (pieced && (max_pieces > kPfMaxPieces || n_groups < 0 ||
+                   int64_t(n_groups) * n_q_heads > kMaxCounters))
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
         n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0)
@@ -1073,6 +1160,16 @@ extern "C" int af_paged_prefill_attention_batched(
     a.tile_map = d_tile_map;
     a.chunks = d_chunks;
     a.max_blocks = max_blocks;
+    if (pieced) {
+        a.piece_map = 1;
+        a.n_pieces = max_pieces;
+        if (max_pieces > 1) {
+            if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) ||
+                workspace_bytes < record_workspace_bytes(n_groups, n_q_heads, max_pieces))
+                return AF_ERR_WORKSPACE;
+            carve_records(a, workspace, n_groups, max_pieces);
+        }
+    }
     const dim3 grid(n_tiles * n_q_heads), block(kPfThreads);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fp8)
@@ -1081,6 +1178,25 @@ extern "C" int af_paged_prefill_attention_batched(
         hipLaunchKernelGGL((prefill_attention_kernel<true, false>), grid, block, 0, s, a);
     AF_TRY_LAUNCH();
     return AF_OK;
+}
+
+extern "C" int af_paged_prefill_attention_batched(
+    const void* q, int q_stride, const af_kv_pool* pool, int layer, const int32_t* d_tables,
+    int max_blocks, const int32_t* d_chunks, const int32_t* d_tile_map, int n_tiles, void* out,
+    int out_stride, int n_q_heads, af_stream_t stream) {
+    return prefill_batched(q, q_stride, pool, layer, d_tables, max_blocks, d_chunks, d_tile_map,
+                           n_tiles, 0, 0, out, out_stride, n_q_heads, nullptr, 0, stream);
+}
+
+extern "C" int af_paged_prefill_attention_batched_ws(
+    const void* q, int q_stride, const af_kv_pool* pool, int layer, const int32_t* d_tables,
+    int max_blocks, const int32_t* d_chunks, const int32_t* d_piece_map, int n_entries,
+    int n_groups, int max_pieces, void* out, int out_stride, int n_q_heads, void* workspace,
+    size_t workspace_bytes, af_stream_t stream) {
+    if (max_pieces < 1) return AF_ERR_INVALID_ARG;
+    return prefill_batched(q, q_stride, pool, layer, d_tables, max_blocks, d_chunks, d_piece_map,
+                           n_entries, n_groups, max_pieces, out, out_stride, n_q_heads, workspace,
+                           workspace_bytes, stream);
 }
 
 extern "C" int af_tiled_attention(const void* q, const void* k, const void* v, void* out,

@@ -186,6 +186,46 @@ def launch_paged_prefill_attention_batched(q, q_stride, pool, layer, d_tables, m
         "launch_paged_prefill_attention_batched")
 
 
+def prefill_piece_map(chunks, n_q_heads, key_pieces=0):
+    """Key-piece map of the chunks [(p0, n, kv_len, row0), ...]: (entries [n][4],
+    n_groups, max_pieces, workspace bytes), heaviest piece first."""
+    ch = np.ascontiguousarray(chunks, np.int32).reshape(-1, 4)
+    max_entries = 4 * int(sum((int(n) + 127) // 128 for n in ch[:, 1])) + 1
+    out = np.zeros((max_entries, 4), np.int32)
+    groups, most, nbytes = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+    n = lib().af_prefill_piece_map(ch.ctypes.data, len(ch), n_q_heads, key_pieces,
+                                   out.ctypes.data, max_entries, ctypes.byref(groups),
+                                   ctypes.byref(most), ctypes.byref(nbytes))
+    if n < 0:
+        raise AfError(n, "af_prefill_piece_map")
+    return out[:n].copy(), groups.value, most.value, nbytes.value
+
+
+class RecordWorkspace:
+    """A key-piece workspace of a given size, zeroed once at creation."""
+
+    def __init__(self, nbytes, stream=None):
+        self.nbytes = max(int(nbytes), 64 * 1024)
+        self.buf = DeviceBuffer(self.nbytes)
+        check(lib().af_attention_workspace_init(self.buf.ptr, self.nbytes, _s(stream)),
+              "af_attention_workspace_init")
+
+    @property
+    def ptr(self):
+        return self.buf.ptr
+
+
+def launch_paged_prefill_attention_batched_ws(q, q_stride, pool, layer, d_tables, max_blocks,
+                                              d_chunks, d_piece_map, n_entries, n_groups,
+                                              max_pieces, out, out_stride, n_q_heads, workspace,
+                                              stream=None):
+    """launch_paged_prefill_attention_batched over a key-piece map."""
+    check(lib().af_paged_prefill_attention_batched_ws(
+        _p(q), q_stride, ctypes.byref(pool), layer, _p(d_tables), max_blocks, _p(d_chunks),
+        _p(d_piece_map), n_entries, n_groups, max_pieces, _p(out), out_stride, n_q_heads,
+        *_ws(workspace), _s(stream)), "launch_paged_prefill_attention_batched_ws")
+
+
 def launch_tiled_attention_kernel(q, k, v, out, seq_q, seq_kv, head_dim, n_q_heads, n_kv_heads,
                                   stream=None):
     """tiled_attention.cu launch_tiled_attention_kernel<half>: query i attends keys s <= i."""

@@ -579,6 +579,7 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
     e0, e1 = dev.Event(), dev.Event()
     rec = []
     arrived, ttft = {}, []  # steps from arrival to the first output token
+    pf_ws = None  # key-piece workspace of the batched prefill, grown to the largest step
     for k in range(warmup + steps):
         t0 = time.perf_counter()
         if shared_prefix:
@@ -611,9 +612,14 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
             ctab, _ = bm.export_tables([c[1] for c in p["prefill"]], max_blocks)
             desc = np.array([(p0, n, p0 + n, nd + int(a["chunks"][i, 3]))
                              for i, (_, _, p0, n, _, _) in enumerate(p["prefill"])], np.int32)
-            tmap = kv.prefill_tile_map(desc)
+            pmap, groups, most, pf_bytes = kv.prefill_piece_map(desc, NQ)
+            if pf_ws is None or pf_ws.nbytes < pf_bytes:
+                if pf_ws is not None:
+                    pf_ws.buf.free()
+                pf_ws = kv.RecordWorkspace(pf_bytes, stream)
+                stream.sync()
             cb = [dev.DeviceBuffer.from_array(ctab), dev.DeviceBuffer.from_array(desc),
-                  dev.DeviceBuffer.from_array(tmap)]
+                  dev.DeviceBuffer.from_array(pmap)]
             bufs += cb
         ncp = len(p["copies"])
         if ncp:
@@ -639,9 +645,9 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
                     kv.launch_paged_attention(q + s0 * QKV * 2, QKV, pool, l, *args,
                                               stream=stream)
             if nch:
-                kv.launch_paged_prefill_attention_batched(q, QKV, pool, l, cb[0], max_blocks,
-                                                          cb[1], cb[2], len(tmap), out, Q_DIM,
-                                                          NQ, stream=stream)
+                kv.launch_paged_prefill_attention_batched_ws(q, QKV, pool, l, cb[0], max_blocks,
+                                                             cb[1], cb[2], len(pmap), groups, most,
+                                                             out, Q_DIM, NQ, pf_ws, stream=stream)
         e1.record(stream)
         e1.sync()
         t2 = time.perf_counter()
@@ -658,7 +664,7 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
                     "[128, 8192] decoding + one 2048-token prompt arriving per step, prefill chunk "
                     "512, step budget 2048 tokens, 28 layers x (one paged append for all new rows, "
                     "decode attention for the batch, one batched prefill attention for the "
-                    "chunks)" + (f"; every prompt shares its first {shared_prefix} tokens, prefix "
+                    "chunks, heavy query tiles cut into key pieces)" + (f"; every prompt shares its first {shared_prefix} tokens, prefix "
                                  "cache of 4 entries" if shared_prefix else "")
                     + ("; decode batch grouped by share group, each group's prefix attended "
                        "once (shared-prefix entry)" if group_decode else ""),
@@ -677,6 +683,8 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
         res["grouped_decode_seqs_per_step"] = round(float(grouped), 2)
     for b in (pool_buf, d_cos, d_sin, qkv, out):
         b.free()
+    if pf_ws is not None:
+        pf_ws.buf.free()
     sched.close()
     bm.close()
     return res

@@ -425,6 +425,27 @@ int af_paged_prefill_attention_batched(const void* q, int q_stride, const af_kv_
  * tile). Returns the tile count, or AF_ERR_WORKSPACE when it exceeds max_tiles. */
 int af_prefill_tile_map(const int32_t* h_chunks, int n_chunks, int32_t* h_tile_map,
                         int max_tiles);
+/* Key pieces for the batched launch (no counterpart in the reference): as
+ * af_prefill_tile_map, but when the launch's tiles x n_q_heads are fewer than
+ * the device's workgroup slots (two per CU), heavy tiles are cut into up to
+ * key_pieces (0 = 4) key ranges, with the rule of af_prefill_attention_ws.
+ * h_map [max_entries][4] = (chunk, tile, piece | pieces << 8, tile index),
+ * heaviest piece first. Returns the entry count (AF_ERR_WORKSPACE when it
+ * exceeds max_entries) and sets *n_groups (tiles), *max_pieces and the
+ * workspace bytes af_paged_prefill_attention_batched_ws needs. */
+int af_prefill_piece_map(const int32_t* h_chunks, int n_chunks, int n_q_heads, int key_pieces,
+                         int32_t* h_map, int max_entries, int* n_groups, int* max_pieces,
+                         size_t* workspace_bytes);
+/* af_paged_prefill_attention_batched over a piece map (d_piece_map: the
+ * uploaded h_map, n_entries, n_groups and max_pieces as af_prefill_piece_map
+ * returned them). Cut tiles merge their pieces as af_prefill_attention_ws does;
+ * the workspace rules are the same (zeroed once, ordered launches). */
+int af_paged_prefill_attention_batched_ws(const void* q, int q_stride, const af_kv_pool* pool,
+                                          int layer, const int32_t* d_tables, int max_blocks,
+                                          const int32_t* d_chunks, const int32_t* d_piece_map,
+                                          int n_entries, int n_groups, int max_pieces, void* out,
+                                          int out_stride, int n_q_heads, void* workspace,
+                                          size_t workspace_bytes, af_stream_t stream);
 
 /* launch_tiled_attention_kernel<half> (include/ops/kernel.h:73-85,
  * src/kernel/tiled_attention.cu:136-161): q [seq_q, n_q_heads*head_dim],

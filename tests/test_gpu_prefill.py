@@ -531,3 +531,80 @@ def test_batched_paged_prefill_equals_per_chunk_launches(gpu, fp8):
             assert_attn_close(got[r0:r0 + n],
                               oracle.prefill_attention_f64(q[r0:r0 + n], kc, vc, p0, n, kvl, NQ,
                                                            NKV, HD), what=f"chunk {c}")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_batched_paged_prefill_key_pieces(gpu, fp8):
+    """The batched launch over a key-piece map: with key_pieces=1 it equals the
+    plain batched launch bit for bit; cut (heavy tiles in up to 4 pieces) it
+    matches the oracle per chunk, and a second launch on the same workspace gives
+    the same bits."""
+    from inputs import ATOL_FP8, RTOL_FP8
+    say(f"batched paged prefill key pieces fp8={fp8}")
+    bs, layers, layer = 16, 1, 0
+    chunks = [(3000, 300, 3300), (0, 300, 300), (1000, 100, 1100), (0, 1, 1), (2000, 200, 2150)]
+    max_blocks = max((kvl + bs - 1) // bs for _, _, kvl in chunks)
+    nblocks = sum((kvl + bs - 1) // bs for _, _, kvl in chunks) + 4
+    r = rng(0xA70F9C + fp8)
+    if fp8:
+        host = r.integers(0, 256, (layers, 2, nblocks * bs, KV_DIM), dtype=np.uint8)
+        host[(host & 0x7F) == 0x7F] = 0
+        scales = r.uniform(0.004, 0.02, (layers, 2, NKV)).astype(np.float32)
+        d_scales, buf = up(scales), up(host)
+        pool = kv.make_pool(buf, atomflow_amd.AF_KV_FP8_E4M3, bs, layers, NKV, HD, nblocks, d_scales)
+    else:
+        host, buf, pool = _paged_pool(bs, nblocks, layers, 0xA70F9D)
+    perm = r.permutation(nblocks).astype(np.int32)
+    tables = np.zeros((len(chunks), max_blocks), np.int32)
+    at = 0
+    for c, (_, _, kvl) in enumerate(chunks):
+        nb = (kvl + bs - 1) // bs
+        tables[c, :nb] = perm[at:at + nb]
+        at += nb
+    rows = sum(n for _, n, _ in chunks)
+    q = randn_f16((rows, QKV), 0xA70F9E)
+    desc, row0 = [], 0
+    for p0, n, kvl in chunks:
+        desc.append((p0, n, kvl, row0))
+        row0 += n
+    d_q, d_t, d_c = up(q), up(tables), up(np.array(desc, np.int32))
+
+    def run(key_pieces, ws=None):
+        pmap, groups, most, nbytes = kv.prefill_piece_map(desc, NQ, key_pieces)
+        ws = ws or kv.RecordWorkspace(nbytes)
+        d_o = up(np.zeros((rows, Q_DIM), np.float16))
+        kv.launch_paged_prefill_attention_batched_ws(d_q, QKV, pool, layer, d_t, max_blocks, d_c,
+                                                     up(pmap), len(pmap), groups, most, d_o, Q_DIM,
+                                                     NQ, ws)
+        return d_o.download(np.float16, (rows, Q_DIM)), pmap, most, ws
+
+    tmap = kv.prefill_tile_map(desc)
+    d_o = up(np.zeros((rows, Q_DIM), np.float16))
+    kv.launch_paged_prefill_attention_batched(d_q, QKV, pool, layer, d_t, max_blocks, d_c, up(tmap),
+                                              len(tmap), d_o, Q_DIM, NQ)
+    plain = d_o.download(np.float16, (rows, Q_DIM))
+    one, pmap1, most1, _ = run(1)
+    assert most1 == 1 and len(pmap1) == len(tmap)
+    assert np.array_equal(bits(one), bits(plain))
+    got, pmap, most, ws = run(0)
+    assert most > 1  # 10 tiles x 24 heads: the planner cuts the heavy tiles
+    seen = {(int(c), int(t), int(pp) & 0xff) for c, t, pp, _ in pmap}
+    assert len(seen) == len(pmap)  # every (chunk, tile, piece) once
+    for c, t, pp, g in pmap:
+        assert (int(pp) & 0xff) < (int(pp) >> 8) <= 4
+    again, _, _, _ = run(0, ws)
+    assert np.array_equal(bits(again), bits(got))
+    for c, (p0, n, kvl, r0) in enumerate(desc):
+        sample = range(n) if n <= 100 else sorted(set(rng(c).choice(n, 40, replace=False).tolist())
+                                                   | {0, 127, 128, n - 1})
+        for i in sample:
+            L = min(p0 + i + 1, kvl)
+            if fp8:
+                ref = oracle.paged_attention_fp8(q[r0 + i, :Q_DIM], host[layer, 0], host[layer, 1],
+                                                 scales[layer, 0], scales[layer, 1], tables[c], L,
+                                                 bs, NQ, NKV, HD)
+                assert_attn_close(got[r0 + i], ref, ATOL_FP8, RTOL_FP8, what=f"chunk {c} row {i}")
+            else:
+                ref = oracle.paged_attention_f16(q[r0 + i, :Q_DIM], host[layer, 0], host[layer, 1],
+                                                 tables[c], L, bs, NQ, NKV, HD)
+                assert_attn_close(got[r0 + i], ref, what=f"chunk {c} row {i}")
