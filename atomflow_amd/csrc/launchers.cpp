@@ -123,6 +123,29 @@ void launch_paged_prefill_attention(const __half* q, int q_stride, const af_kv_p
           "launch_paged_prefill_attention");
 }
 
+void launch_prefill_attention_ws(const __half* q, int q_stride, const View& k_cache,
+                                 const View& v_cache, __half* out, int out_stride, int p0, int n,
+                                 int kv_len, int n_q_heads, int n_kv_heads, int head_dim,
+                                 int key_pieces, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+    const int max_seq = int(k_cache.dims[0] < v_cache.dims[0] ? k_cache.dims[0] : v_cache.dims[0]);
+    check(af_prefill_attention_ws(q, q_stride, k_cache.data_ptr, v_cache.data_ptr, out, out_stride,
+                                  p0, n, kv_len, max_seq, n_q_heads, n_kv_heads, head_dim,
+                                  key_pieces, workspace, workspace_bytes, stream),
+          "launch_prefill_attention_ws");
+}
+
+void launch_paged_prefill_attention_ws(const __half* q, int q_stride, const af_kv_pool& pool,
+                                       int layer, const int32_t* d_block_table, int max_blocks,
+                                       int p0, int n, int kv_len, __half* out, int out_stride,
+                                       int n_q_heads, int key_pieces, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+    check(af_paged_prefill_attention_ws(q, q_stride, &pool, layer, d_block_table, max_blocks, p0,
+                                        n, kv_len, out, out_stride, n_q_heads, key_pieces,
+                                        workspace, workspace_bytes, stream),
+          "launch_paged_prefill_attention_ws");
+}
+
 void launch_cached_attention_ws(const __half* q, const __half* k_cache, const __half* v_cache,
                                 __half* out, int seq_len, const int32_t* d_seq_len,
                                 int max_seq_len, int head_dim, int n_q_heads, int n_kv_heads,

@@ -69,6 +69,22 @@ void launch_prefill_attention(const __half* q, int q_stride, const View& k_cache
                               int kv_len, int n_q_heads, int n_kv_heads, int head_dim,
                               hipStream_t stream);
 
+// The two prefill attention launchers with key pieces (af_prefill_attention_ws,
+// af_paged_prefill_attention_ws): a chunk too small to fill the device has its
+// heavy query tiles cut into key ranges merged in the kernel. key_pieces 0 =
+// the library's choice; workspace of af_prefill_workspace_size bytes, zeroed
+// once with af_attention_workspace_init.
+void launch_prefill_attention_ws(const __half* q, int q_stride, const View& k_cache,
+                                 const View& v_cache, __half* out, int out_stride, int p0, int n,
+                                 int kv_len, int n_q_heads, int n_kv_heads, int head_dim,
+                                 int key_pieces, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+void launch_paged_prefill_attention_ws(const __half* q, int q_stride, const af_kv_pool& pool,
+                                       int layer, const int32_t* d_block_table, int max_blocks,
+                                       int p0, int n, int kv_len, __half* out, int out_stride,
+                                       int n_q_heads, int key_pieces, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream);
+
 // Decode QKV projection + RoPE + KV append (launch_w8a16_gemv, launch_rope and
 // launch_write_kv_cache at position pos in one kernel; d_pos overrides pos).
 void launch_qkv_rope_append(const View& act_x, const View& w_qkv, const View& scales,
