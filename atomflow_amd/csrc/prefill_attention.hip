@@ -822,32 +822,58 @@ int launch_prefix_partials(const PrefixPartialArgs& p, hipStream_t stream) {
     return AF_OK;
 }
 
-// Key pieces of one chunk. Only a chunk whose plain grid (query tiles x Q heads)
-// has fewer workgroups than the device has slots (two per CU) is cut: a grid
-// that fills the device is already balanced by its heaviest-first order, and
-// cutting it only adds record traffic (MI355X: a 4096-token prompt 129 -> 143
-// us). Its work (64-key tiles x Q heads) is spread over the slots: a query tile
-// with more key tiles than one slot's share is cut into pieces of about that
-// share (at least kPfMinPieceTiles tiles each: shorter pieces cost more in
-// set-up and merge than they gain; at most max_pieces per tile). Returns the
-// most pieces of any tile (1: no cut) and the tiles per piece in *units.
-int plan_pieces(int p0, int n, int kv_len, int n_q_heads, int max_pieces, int* units) {
-    *units = 0;
-    const int nt = ceil_div(n, kPfQueries);
-    if (n <= 0 || max_pieces <= 1 || int64_t(nt) * n_q_heads > kMaxCounters) return 1;
+// Key-tiles per piece for a launch whose query tiles need units[i] 64-key
+// tiles each (times n_q_heads workgroups), or 0 for no cut. Only a grid with
+// fewer workgroups than the device has slots (two per CU) is cut: a grid that
+// fills the device is already balanced by its heaviest-first order, and cutting
+// it only adds record traffic (MI355X: a 4096-token prompt 129 -> 143 us). A
+// piece is about 1.6 slot shares of the launch's work (1.0 / 1.3 / 1.6 measured:
+// a serving step's chunks 67 / 61 / 59 us, a 2048-token prompt 52 / 48 / 48 us),
+// and at least kPfMinPieceTiles tiles (shorter pieces cost more in set-up and
+// merge than they gain). Tile i then has min(cap, ceil(units[i] / per)) pieces.
+// With `concurrent`, per also grows until every piece has a slot at once: the
+// single-chunk grid orders pieces by tile, not by size, so a piece that waited
+// for a slot could be a whole uncut tile queued behind smaller pieces.
+int piece_tiles(const std::vector<int>& units, int n_q_heads, int cap, bool concurrent) {
+    const int64_t slots = 2 * int64_t(device_compute_units());
+    const int64_t tiles = int64_t(units.size());
+    if (cap <= 1 || tiles == 0 || tiles * n_q_heads >= slots || tiles * n_q_heads > kMaxCounters)
+        return 0;
     int64_t work = 0;
     int most = 0;
-    for (int t = 0; t < nt; ++t) {
-        const int keys = std::min(p0 + std::min((t + 1) * kPfQueries, n), kv_len);
-        const int u = ceil_div(std::max(keys, 1), kPfKeys);
+    for (int u : units) {
         work += u;
         most = std::max(most, u);
     }
-    work *= n_q_heads;
-    const int64_t slots = 2 * int64_t(device_compute_units());
-    if (int64_t(nt) * n_q_heads >= slots) return 1;
-    const int per = int(std::max<int64_t>(kPfMinPieceTiles, (work + slots - 1) / slots));
-    const int pieces = std::min(std::min(max_pieces, kPfMaxPieces), ceil_div(most, per));
+    int per = int(std::max<int64_t>(kPfMinPieceTiles, (work * n_q_heads * 8 + 5 * slots - 1) /
+                                                          (5 * slots)));
+    auto wgs = [&](int pt) {
+        int64_t w = 0;
+        for (int u : units) w += std::min(cap, ceil_div(u, pt));
+        return w * n_q_heads;
+    };
+    if (concurrent)
+        while (per < most && wgs(per) > slots) ++per;
+    return per < most ? per : 0;
+}
+
+// Key pieces of one chunk (piece_tiles over its query tiles). Returns the most
+// pieces of any tile (1: no cut) and the tiles per piece in *units.
+int plan_pieces(int p0, int n, int kv_len, int n_q_heads, int max_pieces, int* units) {
+    *units = 0;
+    const int nt = ceil_div(n, kPfQueries);
+    if (n <= 0) return 1;
+    std::vector<int> u(nt);
+    int most = 0;
+    for (int t = 0; t < nt; ++t) {
+        const int keys = std::min(p0 + std::min((t + 1) * kPfQueries, n), kv_len);
+        u[t] = ceil_div(std::max(keys, 1), kPfKeys);
+        most = std::max(most, u[t]);
+    }
+    const int cap = std::min(max_pieces, kPfMaxPieces);
+    const int per = piece_tiles(u, n_q_heads, cap, true);
+    if (per == 0) return 1;
+    const int pieces = std::min(cap, ceil_div(most, per));
     if (pieces <= 1) return 1;
     *units = per;
     return pieces;
@@ -1065,7 +1091,6 @@ extern "C" int af_prefill_piece_map(const int32_t* h_chunks, int n_chunks, int n
         int units, c, t, g, pieces;
     };
     std::vector<T> tiles;
-    int64_t work = 0;
     for (int c = 0; c < n_chunks; ++c) {
         const int p0 = h_chunks[4 * c], n = h_chunks[4 * c + 1], kv_len = h_chunks[4 * c + 2];
         if (p0 < 0 || n < 0 || h_chunks[4 * c + 3] < 0) return AF_ERR_INVALID_ARG;
@@ -1074,23 +1099,20 @@ extern "C" int af_prefill_piece_map(const int32_t* h_chunks, int n_chunks, int n
             const int keys = std::min(p0 + std::min((t + 1) * kPfQueries, n), kv_len);
             const int u = ceil_div(std::max(keys, 1), kPfKeys);
             tiles.push_back({u, c, t, int(tiles.size()), 1});
-            work += u;
         }
     }
-    // The rule of plan_pieces over the launch's tiles: cut only a grid that has
-    // fewer workgroups than the device has slots.
-    const int64_t slots = 2 * int64_t(device_compute_units());
+    // piece_tiles over the launch's tiles; the map orders pieces by size, so
+    // pieces may queue for slots.
     const int cap = key_pieces == 0 ? kPfMaxPieces : key_pieces;
+    std::vector<int> units;
+    for (const T& x : tiles) units.push_back(x.units);
+    const int per = piece_tiles(units, n_q_heads, cap, false);
     int most = 1;
-    if (cap > 1 && int64_t(tiles.size()) * n_q_heads < slots &&
-        int64_t(tiles.size()) * n_q_heads <= kMaxCounters) {
-        const int per = int(std::max<int64_t>(kPfMinPieceTiles,
-                                              (work * n_q_heads + slots - 1) / slots));
+    if (per > 0)
         for (T& x : tiles) {
             x.pieces = std::min(cap, ceil_div(x.units, per));
             most = std::max(most, x.pieces);
         }
-    }
     // entries: every piece, heaviest piece first (a tile's pieces stay together)
     std::stable_sort(tiles.begin(), tiles.end(), [](const T& x, const T& y) {
         return int64_t(x.units) * y.pieces > int64_t(y.units) * x.pieces;
