@@ -6,7 +6,8 @@
 // sandbox (BlockManager fork + copy-on-write, paged append, paged attention,
 // and the shared-prefix form over the forked pair), and a decode step of
 // several layers over the engine's one-arena KV pool [L0_K | L0_V | L1_K | ...]
-// (engine.cu:187-215, model_state.h:56-64).
+// (engine.cu:187-215, model_state.h:56-64), and a prompt chunk's causal
+// attention through the key-piece launcher (launch_prefill_attention_ws).
 // Inputs come from a fixed xorshift stream; inputs and outputs are written to
 // <out_dir>/*.bin so tests/test_gpu_cpp_host.py can check them against the
 // oracle. Exit status 0 only if every call succeeded and the in-program checks
@@ -370,6 +371,46 @@ int pooled_step(const std::string& dir, hipStream_t s) {
 
 }  // namespace
 
+// A 300-token prompt chunk at p0 700 (kv_len 1000) through
+// launch_prefill_attention_ws with the library's choice of key pieces (its three
+// query tiles are cut), and the same chunk through launch_prefill_attention.
+int prefill_step(const std::string& dir, hipStream_t s) {
+    const int p0 = 700, n = 300, kv_len = 1000;
+    auto q = randn_like(size_t(n) * Q_DIM, 31);
+    auto kc = randn_like(size_t(MAX_SEQ) * KV_DIM, 32);
+    auto vc = randn_like(size_t(MAX_SEQ) * KV_DIM, 33);
+    save(dir, "f_q", q.data(), q.size() * 2);
+    save(dir, "f_k", kc.data(), kc.size() * 2);
+    save(dir, "f_v", vc.data(), vc.size() * 2);
+    uint16_t* d_q = dev_upload(q);
+    uint16_t* d_k = dev_upload(kc);
+    uint16_t* d_v = dev_upload(vc);
+    uint16_t *d_out = nullptr, *d_plain = nullptr;
+    HIP_OK(hipMalloc(&d_out, size_t(n) * Q_DIM * 2));
+    HIP_OK(hipMalloc(&d_plain, size_t(n) * Q_DIM * 2));
+    const size_t ws_bytes = af_prefill_workspace_size(p0, n, kv_len, NH, 0);
+    void* ws = nullptr;
+    HIP_OK(hipMalloc(&ws, ws_bytes));
+    if (af_attention_workspace_init(ws, ws_bytes, s) != AF_OK) throw std::runtime_error("ws init");
+    View k_cache = create_contiguous_view(d_k, DataType::FP16, {MAX_SEQ, KV_DIM});
+    View v_cache = create_contiguous_view(d_v, DataType::FP16, {MAX_SEQ, KV_DIM});
+    const __half* hq = reinterpret_cast<const __half*>(d_q);
+    launch_prefill_attention_ws(hq, Q_DIM, k_cache, v_cache, reinterpret_cast<__half*>(d_out),
+                                Q_DIM, p0, n, kv_len, NH, NKV, HD, 0, ws, ws_bytes, s);
+    launch_prefill_attention(hq, Q_DIM, k_cache, v_cache, reinterpret_cast<__half*>(d_plain),
+                             Q_DIM, p0, n, kv_len, NH, NKV, HD, s);
+    HIP_OK(hipStreamSynchronize(s));
+    auto out = dev_download(d_out, size_t(n) * Q_DIM);
+    auto plain = dev_download(d_plain, size_t(n) * Q_DIM);
+    save(dir, "f_attn", out.data(), out.size() * 2);
+    save(dir, "f_attn_plain", plain.data(), plain.size() * 2);
+    const uint64_t ws_size = ws_bytes;
+    save(dir, "f_ws_bytes", &ws_size, sizeof(ws_size));
+    for (void* p : {(void*)d_q, (void*)d_k, (void*)d_v, (void*)d_out, (void*)d_plain, ws})
+        HIP_OK(hipFree(p));
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc != 2) {
         std::fprintf(stderr, "usage: %s OUT_DIR\n", argv[0]);
@@ -383,6 +424,7 @@ int main(int argc, char** argv) {
         int rc = contiguous_step(dir, s);
         if (rc == 0) rc = paged_step(dir, s);
         if (rc == 0) rc = pooled_step(dir, s);
+        if (rc == 0) rc = prefill_step(dir, s);
         HIP_OK(hipStreamDestroy(s));
         if (rc == 0) std::puts("ok");
         return rc;

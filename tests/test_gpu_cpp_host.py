@@ -111,3 +111,26 @@ def test_cpp_host_pooled_layers(gpu, tmp_path):
         assert_attn_close(got_attn[layer], ref, what=f"pooled layer {layer}")
     got_pool = load(d, "pl_pool_out", np.uint16, (NL, 2, MAX_SEQ, KV_DIM))
     assert np.array_equal(got_pool, pool.view(np.uint16))
+
+
+def test_cpp_host_prefill_key_pieces(gpu, tmp_path):
+    """launch_prefill_attention_ws from the C++ host: a 300-token chunk at p0 700
+    (kv_len 1000) with its query tiles cut into key pieces (the workspace the
+    library sized is larger than the counter region) against the float64
+    oracle on every row, beside launch_prefill_attention on the same inputs."""
+    print("[case] C++ host: prefill chunk with key pieces", flush=True)
+    r = subprocess.run([EXE, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
+    d = str(tmp_path)
+    p0, n, kv_len = 700, 300, 1000
+    assert load(d, "f_ws_bytes", np.uint64)[0] > 64 * 1024  # the chunk was cut
+    q = load(d, "f_q", np.float16, (n, Q_DIM))
+    k = load(d, "f_k", np.float16, (MAX_SEQ, KV_DIM))
+    v = load(d, "f_v", np.float16, (MAX_SEQ, KV_DIM))
+    got = load(d, "f_attn", np.float16, (n, Q_DIM))
+    plain = load(d, "f_attn_plain", np.float16, (n, Q_DIM))
+    for i in range(n):
+        L = min(p0 + i + 1, kv_len)
+        ref = oracle.cached_attention_f64(q[i], k, v, L, NQ, NKV, HD)
+        assert_attn_close(got[i], ref, what=f"pieces row {i}")
+        assert_attn_close(plain[i], ref, what=f"plain row {i}")
