@@ -244,10 +244,19 @@ __device__ __forceinline__ void fp8_store(char* ks, char* vs, int tid, const Fp8
     *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 1)) = e4m3x8_to_f16(t.k0.z, t.k0.w);
     *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 2)) = e4m3x8_to_f16(t.k1.x, t.k1.y);
     *reinterpret_cast<uint4*>(ks + k_off(row, 4 * q + 3)) = e4m3x8_to_f16(t.k1.z, t.k1.w);
-    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 0)) = e4m3x8_to_f16(t.v0.x, t.v0.y);
-    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 1)) = e4m3x8_to_f16(t.v0.z, t.v0.w);
-    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 2)) = e4m3x8_to_f16(t.v1.x, t.v1.y);
-    *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + 3)) = e4m3x8_to_f16(t.v1.z, t.v1.w);
+    // V's swizzle permutes whole 64-B chunk groups by row % 4, so the same store
+    // of rows r and r + 1 would meet in the same banks (counters: 0.67 conflicts
+    // per LDS access). Each lane stores its four chunks rotated by row % 4, so
+    // one instruction's rows land in different 16-B bank groups.
+    const uint4 c0 = e4m3x8_to_f16(t.v0.x, t.v0.y), c1 = e4m3x8_to_f16(t.v0.z, t.v0.w);
+    const uint4 c2 = e4m3x8_to_f16(t.v1.x, t.v1.y), c3 = e4m3x8_to_f16(t.v1.z, t.v1.w);
+    const int rot = row & 3;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int cc = (c + rot) & 3;
+        const uint4 val = cc == 0 ? c0 : cc == 1 ? c1 : cc == 2 ? c2 : c3;
+        *reinterpret_cast<uint4*>(vs + v_off(row, 4 * q + cc)) = val;
+    }
 }
 
 __device__ __forceinline__ half8 lds_half8(const char* p) {
