@@ -1620,8 +1620,12 @@ int default_splits(int max_seq_len, int batch, int n_kv_heads) {
     // Long sequences: spans of about 1024 rows, but never more workgroups than
     // CUs. A grid just past the CU count doubles up a few CUs, and the launch
     // then waits on them (ctx 32k on MI355X: 33 splits x 8 heads = 264
-    // workgroups ran 40.5 us, 32 splits 29.6 us, 64 splits 31.3 us).
-    splits = std::max(splits, std::min(ceil_div(max_seq_len, 1024), std::max(1, cus / pairs)));
+    // workgroups ran 40.5 us, 32 splits 29.6 us, 64 splits 31.3 us). With the
+    // dedicated combiner (at most kCombMaxGroups pairs) every pair also takes
+    // a combiner workgroup, and one more CU per pair left free measured best
+    // (ctx 32k, 8 heads: 30 / 31 / 32 splits 28.5 / 28.9 / 29.3 us).
+    const int room = pairs <= kCombMaxGroups ? (cus - 2 * pairs) / pairs : cus / pairs;
+    splits = std::max(splits, std::min(ceil_div(max_seq_len, 1024), std::max(1, room)));
     splits = std::min(splits, std::max(1, ceil_div(max_seq_len, kMinSpan)));
     return std::min(std::max(splits, 1), kMaxSplits);
 }

@@ -78,8 +78,9 @@ def test_default_split_counts():
     from atomflow_amd import kv
     assert kv.default_splits(8193, 1, 8) == 24
     assert kv.default_splits(24577, 1, 8) == 25  # ceil(24577 / 1024)
-    assert kv.default_splits(32769, 1, 8) == 32
-    assert kv.default_splits(131072, 1, 8) == 32
+    # one workgroup per CU at most, counting each pair's combiner and one spare CU per pair
+    assert kv.default_splits(32769, 1, 8) == 30
+    assert kv.default_splits(131072, 1, 8) == 30
     assert kv.default_splits(1025, 1, 8) == 17   # one 64-row step per split
     assert kv.default_splits(8193, 32, 8) == 17  # batched: ceil(8193 / 512)
     assert kv.default_splits(0, 1, 8) == 1
