@@ -593,7 +593,7 @@ class Scheduler:
 # Rows a share group must save per launch, (members - 1) x shared rows, before
 # its own launch pair pays: the prefix launch and the second decode cost about
 # as much as reading 10-12k KV rows of 8 heads x 128 on MI355X.
-SHARE_MIN_SAVED_ROWS = 10240
+SHARE_MIN_SAVED_ROWS = 24576
 
 
 def decode_share_segments(groups, rows, min_members=2, min_saved_rows=SHARE_MIN_SAVED_ROWS):

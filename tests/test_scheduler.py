@@ -254,7 +254,7 @@ def test_decode_share_segments():
     assert list(order) == [0, 1] and segs == [(0, 2, 0)]
     order, segs = kv.decode_share_segments([4] * 64, [4096] * 64)
     assert segs == [(0, 64, 4096)]
-    assert kv.SHARE_MIN_SAVED_ROWS == 10240
+    assert kv.SHARE_MIN_SAVED_ROWS == 24576
     assert kv.decode_share_segments([], [])[1] == []
     # only groups that save enough row reads: group 3 saves 2 x 40, group 5 1 x 100
     order, segs = kv.decode_share_segments(groups, rows, min_saved_rows=81)
