@@ -39,6 +39,28 @@
 namespace af {
 namespace {
 
+#ifdef AF_PHASE_STAMPS
+// Measurement build only (`make stamps`, libatomflow_kv_stamps.so): thread 0
+// of every workgroup records s_memrealtime (100 MHz) at each phase of the
+// decode kernel; af_dbg_phase_stamps copies the table out. Split phases: 0
+// start, 1 ring prologue issued, 2 main loop entered, 3 rows streamed, 4
+// partials in LDS, 5 partial stores issued, 6 stores acknowledged (flag set).
+// Dedicated-combiner phases: 0 start, 6 last flag seen, 7 output written.
+constexpr int kStampWgs = 2048, kStampPhases = 8;
+__device__ uint64_t g_phase_stamps[kStampWgs][kStampPhases];
+#define AF_STAMP(ph)                                                                       \
+    do {                                                                                   \
+        __builtin_amdgcn_sched_barrier(0);                                                 \
+        if (threadIdx.x == 0 && blockIdx.x < kStampWgs)                                    \
+            g_phase_stamps[blockIdx.x][ph] = __builtin_amdgcn_s_memrealtime();             \
+        __builtin_amdgcn_sched_barrier(0);                                                 \
+    } while (0)
+#else
+#define AF_STAMP(ph) \
+    do {             \
+    } while (0)
+#endif
+
 typedef _Float16 f16;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
@@ -234,6 +256,7 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
         }
     }
 
+    AF_STAMP(0);
     const uint32_t all = n_active >= 32 ? ~0u : ((1u << n_active) - 1u);
     uint32_t have = 0;
     float mv = -INFINITY, lv = 0.f;  // lane s: split s
@@ -259,6 +282,7 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
         }
     }
     const bool timed_out = act && have != all;
+    AF_STAMP(6);
 
     const float w = merge_weight(mv, lv);  // lane s: split s's weight
     float r0 = 0.f, r1 = 0.f;
@@ -288,6 +312,7 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
             }
         }
     }
+    AF_STAMP(7);
     if (timed_out && lane == 0 && a.d_status) *a.d_status = AF_ERR_TIMEOUT;
     // Every wave has read Q and finished polling past this barrier: the flags
     // return to zero for the next launch and the rotated Q is stored.
@@ -415,6 +440,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
+    AF_STAMP(0);
 
     // ---- stage this split's block-table entries (paged) --------------------
     int tab_base = 0;
@@ -524,6 +550,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     Row ring[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) load_row(ring[i], min(i, n_steps - 1));
+    AF_STAMP(1);
 
     // ---- query fragment -----------------------------------------------------
     half2_t qv[GROUP][EPL / 2];
@@ -768,6 +795,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     // keep the loop single-exit with the same load sequence on every path, so
     // the compiler waits only for the slot being consumed; the last partial
     // round is drained without refills.
+    AF_STAMP(2);
     const int n_full = n_steps / NB;
     if constexpr (FP8) {  // slots consumed and refilled two at a time
         static_assert(NB % 2 == 0, "FP8 ring pairs slots");
@@ -799,6 +827,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
             if (i < rem) process_row(ring[i], n_full * NB + i);
     }
 
+    AF_STAMP(3);
     if constexpr (PERSIST)  // the claim issued at the item's start has long returned
         if (tid == 0) s_next = next_item;
 
@@ -873,6 +902,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
         }
     }
     __syncthreads();
+    AF_STAMP(4);
     if constexpr (PERSIST) {
         // The next item's block-table window (thread t: entry t, up to kThreads
         // entries): loaded here, it arrives while this item merges and
@@ -920,6 +950,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
             }
         }
     }
+    AF_STAMP(5);
     if (direct) {
         if constexpr (FUSED) {  // the only reader of these Q heads: rotate in place now
             uint16_t* qd = a.q + size_t(b) * a.q_stride + size_t(hw) * GHD;
@@ -953,6 +984,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     // order of these instructions; af_common.h rejects any other target.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    AF_STAMP(6);
     if constexpr (COMB) {  // the dedicated combiner reads the partial once the flag is set
         if (tid == 0)
             __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, 1u,
@@ -1639,6 +1671,19 @@ static int min_splits_for_table(int max_seq_len, int block_size) {
 }  // namespace af
 
 using namespace af;
+
+#ifdef AF_PHASE_STAMPS
+// Measurement build only: the phase table of the last launch per workgroup
+// (uint64 [2048][8], s_memrealtime ticks of 10 ns; 0 = phase not reached).
+extern "C" int af_dbg_phase_stamps(void* host, size_t bytes) {
+    if (bytes > sizeof(g_phase_stamps)) bytes = sizeof(g_phase_stamps);
+    return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase_stamps), bytes));
+}
+extern "C" int af_dbg_phase_stamps_clear(void) {
+    static uint64_t zeros[kStampWgs][kStampPhases];
+    return int(hipMemcpyToSymbol(HIP_SYMBOL(g_phase_stamps), zeros, sizeof(zeros)));
+}
+#endif
 
 extern "C" size_t af_attention_workspace_size(int batch, int n_q_heads, int n_kv_heads,
                                               int head_dim, int num_splits) {

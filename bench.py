@@ -76,6 +76,10 @@ def parse():
                     help="run only the fan-out decode measurement and print its JSON object")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
+    ap.add_argument("--stamps", action="store_true",
+                    help="run only the per-phase timeline of the configs[1] attention launch "
+                         "(needs libatomflow_kv_stamps.so: make -C atomflow_amd/csrc stamps) and "
+                         "print its JSON object")
     ap.add_argument("--read-probe", action="store_true",
                     help="run only the streaming-read probes (per-launch read ceilings of each "
                          "workload's bytes) and print their JSON object")
@@ -1293,6 +1297,107 @@ def bench_read_probe(args, dev):
     return out
 
 
+STAMP_PHASES = ["split start", "ring prologue issued", "main loop entered", "rows streamed",
+                "partials in LDS", "partial stores issued", "stores acknowledged, flag set"]
+COMBINER_PHASES = {0: "combiner start", 6: "combiner: last flag seen", 7: "combiner: output written"}
+
+
+def bench_stamps(args, dev, kv, lib):
+    """Where one attention launch's time goes (configs[1], batch 1): the stamps
+    build records s_memrealtime (10 ns ticks) per workgroup at each phase of the
+    decode kernel (split workgroups, then the dedicated combiners). For the last
+    launch of a 28-layer graph (fused step, then attention only), after each of
+    `steps` replays: every phase's median and slowest workgroup, in us from the
+    first workgroup's start; the medians over replays are reported."""
+    import ctypes
+    import atomflow_amd
+
+    ctx = args.ctx
+    L = ctx + 1
+    max_seq = (L + 127) // 128 * 128
+    slab = max_seq * KV_DIM * 2
+    stream = dev.Stream()
+    pool = dev.DeviceBuffer(LAYERS * 2 * slab)
+    qkv = dev.DeviceBuffer(LAYERS * QKV * 2)
+    out = dev.DeviceBuffer(LAYERS * Q_DIM * 2)
+    d_cos = dev.DeviceBuffer(max_seq * HD // 2 * 4)
+    d_sin = dev.DeviceBuffer(max_seq * HD // 2 * 4)
+    kv.build_rope_cache(d_cos, d_sin, max_seq, HD, THETA, stream)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(pool.ptr, LAYERS * 2 * slab // 2, 7, 1.0, stream.handle))
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, LAYERS * QKV, 11, 1.0, stream.handle))
+    splits = args.splits or kv.default_splits(L, 1, NKV)
+    ws = kv.AttentionWorkspace(1, NQ, NKV, HD, splits, stream)
+    stream.sync()
+    raw = ctypes.CDLL(atomflow_amd.LIB_PATH)
+    raw.af_dbg_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    n_wg, n_ph = 2048, 8
+    table = np.zeros((n_wg, n_ph), np.uint64)
+
+    def ptrs(l):
+        return (qkv.ptr + l * QKV * 2, pool.ptr + 2 * l * slab, pool.ptr + (2 * l + 1) * slab,
+                out.ptr + l * Q_DIM * 2)
+
+    def fused():
+        for l in range(LAYERS):
+            q, k, v, o = ptrs(l)
+            kv.launch_decode_attention_fused(q, k, v, d_cos, d_sin, ctx, max_seq, o, NQ, NKV, HD,
+                                             ws, num_splits=splits, stream=stream)
+
+    def attention():
+        for l in range(LAYERS):
+            q, k, v, o = ptrs(l)
+            kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws,
+                                          num_splits=splits, stream=stream)
+
+    result = {"workload": f"configs[1] ctx {ctx}, batch 1, {splits} splits x {NKV} KV heads",
+              "splits": splits, "phases": STAMP_PHASES + list(COMBINER_PHASES.values()),
+              "unit": "us from the first workgroup's start", "replays": args.steps}
+    for name, fn in (("fused", fused), ("attention", attention)):
+        graph = dev.Graph.capture(stream, fn)
+        for _ in range(args.warmup):
+            graph.launch(stream)
+        stream.sync()
+        per = []
+        for _ in range(args.steps):
+            atomflow_amd.check(raw.af_dbg_phase_stamps_clear())
+            graph.launch(stream)
+            stream.sync()
+            atomflow_amd.check(raw.af_dbg_phase_stamps(table.ctypes.data, table.nbytes))
+            t = table[: splits * NKV].astype(np.float64)
+            c = table[splits * NKV: splits * NKV + NKV].astype(np.float64)
+            t0 = min(t[:, 0][t[:, 0] > 0].min(), c[:, 0][c[:, 0] > 0].min() if (c[:, 0] > 0).any() else np.inf)
+            row = {}
+            for rows, phases in ((t, dict(enumerate(STAMP_PHASES))), (c, COMBINER_PHASES)):
+                for ph, pname in phases.items():
+                    v = rows[:, ph]
+                    v = (v[v > 0] - t0) * 0.01
+                    if len(v):
+                        row[pname] = (float(np.median(v)), float(v.max()), int(len(v)))
+            # per KV head (workgroup id = split * heads + head: every split of
+            # head h runs on XCD h when heads = 8)
+            heads = np.arange(splits * NKV) % NKV
+            for ph in (1, 3):
+                row[f"by_kv_head {STAMP_PHASES[ph]}"] = [
+                    float(np.median((t[heads == h, ph] - t0) * 0.01)) for h in range(NKV)]
+            per.append(row)
+        graph.destroy()
+        summary = {}
+        for pname in STAMP_PHASES + list(COMBINER_PHASES.values()):
+            vals = [r[pname] for r in per if pname in r]
+            if vals:
+                summary[pname] = {"median_us": round(float(np.median([v[0] for v in vals])), 3),
+                                  "slowest_us": round(float(np.median([v[1] for v in vals])), 3),
+                                  "workgroups": vals[0][2]}
+        for ph in (1, 3):
+            key = f"by_kv_head {STAMP_PHASES[ph]}"
+            summary[key] = [round(float(np.median([r[key][h] for r in per])), 3) for h in range(NKV)]
+        result[name] = summary
+    for b in (pool, qkv, out, d_cos, d_sin):
+        b.free()
+    stream.destroy()
+    return result
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1303,6 +1408,9 @@ def main():
     from atomflow_amd import device as dev
     from atomflow_amd import kv
 
+    if args.stamps:  # the measurement build of the same library
+        atomflow_amd.LIB_PATH = os.environ.get(
+            "AF_STAMPS_LIB", os.path.join(ROOT, "atomflow_amd", "libatomflow_kv_stamps.so"))
     lib = atomflow_amd.lib()
     dev.set_device(0)
     info = dev.device_info()
@@ -1312,6 +1420,9 @@ def main():
         return
     if args.read_probe:
         print(json.dumps({"read_probe": bench_read_probe(args, dev)}), flush=True)
+        return
+    if args.stamps:
+        print(json.dumps({"stamps": bench_stamps(args, dev, kv, lib)}), flush=True)
         return
     if args.config == 2:
         result = bench_contiguous(args, dev, kv, lib, info)
