@@ -50,10 +50,12 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 //                                per (sequence, KV head); words [kFlagBase,
 //                                kFlagBase + kCombMaxGroups * kCombSplits):
 //                                ready flags of the dedicated-combiner form, one
-//                                per (sequence, KV head, split); the last two
-//                                words: the persistent form's item counters. All
-//                                zero between launches (each launch re-zeroes
-//                                what it used)
+//                                per (sequence, KV head, split), then one
+//                                generation word per (sequence, KV head) (a flag
+//                                holds its launch's generation + 1); the last two
+//                                words: the persistent form's item counters.
+//                                Counters are zero between launches (each launch
+//                                re-zeroes what it used)
 //   [kCounterBytes, ...)         part_ml [batch][n_kv_heads][splits][2 * group]
 //                                (group = n_q_heads / n_kv_heads: max..., sum...)
 //   then                         part_o  [batch][n_kv_heads][splits][group * head_dim]
@@ -75,11 +77,13 @@ static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= int(kCounterBytes / si
 // two words of the counter region).
 constexpr int kItemCounter = int(kCounterBytes / sizeof(uint32_t)) - 2;
 constexpr int kDoneCounter = kItemCounter + 1;
-static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= kItemCounter, "counter words overlap");
+constexpr int kGenBase = kFlagBase + kCombMaxGroups * kCombSplits;
+static_assert(kGenBase + kCombMaxGroups <= kItemCounter, "counter words overlap");
 
 struct AttnWorkspace {
     uint32_t* counters;
     uint32_t* flags;
+    uint32_t* gens;
     float* part_ml;
     float* part_o;
 };
@@ -95,6 +99,7 @@ inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, 
     AttnWorkspace w;
     w.counters = reinterpret_cast<uint32_t*>(p);
     w.flags = w.counters + kFlagBase;
+    w.gens = w.counters + kGenBase;
     p += kCounterBytes;
     w.part_ml = reinterpret_cast<float*>(p);
     p += align_up(size_t(batch) * n_q_heads * num_splits * 2 * sizeof(float), 256);
@@ -107,7 +112,11 @@ int device_compute_units();
 
 // Default split count: batched launches cover about kBatchSpan tokens per
 // split; small ones about 3/4 of a workgroup per CU, each split at least
-// kMinSpan tokens; at most kMaxSplits.
+// kMinSpan tokens; at most kMaxSplits. `combiner`: the launch's shape can take
+// the dedicated combiner (contiguous, head_dim 128, up to 4 query heads per KV
+// head), which then leaves room for its combiner workgroups; default_splits
+// assumes such a shape.
+int default_splits_for(int max_seq_len, int batch, int n_kv_heads, bool combiner);
 int default_splits(int max_seq_len, int batch, int n_kv_heads);
 // Target tokens per split that goes with default_splits.
 int default_span(int batch, int n_kv_heads);

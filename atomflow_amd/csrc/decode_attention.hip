@@ -145,6 +145,7 @@ struct AttnArgs {
     // batch * n_kv_heads are one combiner per (sequence, KV head) that waits on
     // its splits' ready flags ([batch * n_kv_heads][kCombSplits]).
     uint32_t* flags;
+    uint32_t* gens;      // generation word of each (sequence, KV head): flags carry gen + 1
     int32_t split_wgs;
     int32_t batch;       // sequences (the persistent form claims items over their rows)
     int32_t item_big;    // persistent form: row-steps of a big / small item
@@ -238,6 +239,10 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
     const float* ml = a.part_ml + grp * a.rec_stride * 2 * GQ;
     const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + grp * a.rec_stride * GHD);
     uint32_t* flags = a.flags + grp * kCombSplits;
+    // A ready flag holds the launch's generation + 1 (the generation word is
+    // read first, before anything else is loaded); flags of an earlier launch
+    // never match, so the flags are not re-zeroed.
+    const uint32_t ready = __hip_atomic_load(a.gens + grp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
     // The query heads are stored back rotated, as the last-arrival combine does
     // (every split has read them once the records are complete). Their inputs
@@ -268,7 +273,7 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
             const uint32_t f = lane < n_active ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED,
                                                                    __HIP_MEMORY_SCOPE_AGENT)
                                                : 0u;
-            const uint32_t fresh = uint32_t(__builtin_amdgcn_ballot_w64(f != 0u)) & all & ~have;
+            const uint32_t fresh = uint32_t(__builtin_amdgcn_ballot_w64(f == ready)) & all & ~have;
             if (lane < kCombSplits && ((fresh >> lane) & 1u)) {
                 mv = load_agent(ml + lane * 2 * GQ + gh);
                 lv = load_agent(ml + lane * 2 * GQ + GQ + gh);
@@ -314,11 +319,13 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
     }
     AF_STAMP(7);
     if (timed_out && lane == 0 && a.d_status) *a.d_status = AF_ERR_TIMEOUT;
-    // Every wave has read Q and finished polling past this barrier: the flags
-    // return to zero for the next launch and the rotated Q is stored.
+    // Every wave has read Q and finished polling past this barrier: the next
+    // launch's flags carry the next generation, and the rotated Q is stored.
+    // Every split read the generation in its first instructions, and all of
+    // them were dispatched before this combiner (workgroups start in id order),
+    // so even after a timeout no split of this launch reads the new generation.
     __syncthreads();
-    if (tid < n_active)
-        __hip_atomic_store(flags + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(a.gens + grp, ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (FUSED)
         if (act) *reinterpret_cast<uint32_t*>(qh + d) = qrot;
 }
@@ -440,6 +447,13 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
+    // Dedicated-combiner form: the generation of (b, hw), loaded before
+    // anything else; the ready flag is set to it + 1.
+    uint32_t gen = 0;
+    if constexpr (COMB)
+        if (!direct)
+            gen = __hip_atomic_load(a.gens + size_t(b) * nhw + hw, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
     AF_STAMP(0);
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -987,7 +1001,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     AF_STAMP(6);
     if constexpr (COMB) {  // the dedicated combiner reads the partial once the flag is set
         if (tid == 0)
-            __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, 1u,
+            __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, gen + 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -1556,8 +1570,10 @@ int persistent_dispatch(const AttnArgs& a, int group, bool fp8, bool fused, int 
 // last-arriving split: few (sequence, KV head) pairs (combiners are one
 // workgroup each, dispatched after every split), at most kCombSplits splits,
 // and one output pair per combiner thread.
+bool combiner_shape(int group, int head_dim) { return head_dim == 128 && group <= kWaves; }
+
 bool use_combiner(int batch, int n_kv_heads, int num_splits, int group, int head_dim) {
-    return num_splits >= 2 && num_splits <= kCombSplits && head_dim == 128 && group <= kWaves &&
+    return num_splits >= 2 && num_splits <= kCombSplits && combiner_shape(group, head_dim) &&
            int64_t(batch) * n_kv_heads <= kCombMaxGroups;
 }
 
@@ -1639,7 +1655,7 @@ int default_span(int batch, int n_kv_heads) {
     return int64_t(batch) * n_kv_heads * 2 >= device_compute_units() ? kBatchSpan : kMinSpan;
 }
 
-int default_splits(int max_seq_len, int batch, int n_kv_heads) {
+int default_splits_for(int max_seq_len, int batch, int n_kv_heads, bool combiner) {
     if (max_seq_len <= 0) return 1;
     if (default_span(batch, n_kv_heads) == kBatchSpan)
         return std::min(std::max(ceil_div(max_seq_len, kBatchSpan), 1), kMaxSplits);
@@ -1648,18 +1664,29 @@ int default_splits(int max_seq_len, int batch, int n_kv_heads) {
     // (the split-K combine grows with the split count faster than more
     // workgroups add bandwidth).
     const int cus = device_compute_units();
-    int splits = std::max(1, (3 * cus) / (4 * pairs));
+    const int base = std::max(1, (3 * cus) / (4 * pairs));
     // Long sequences: spans of about 1024 rows, but never more workgroups than
     // CUs. A grid just past the CU count doubles up a few CUs, and the launch
     // then waits on them (ctx 32k on MI355X: 33 splits x 8 heads = 264
-    // workgroups ran 40.5 us, 32 splits 29.6 us, 64 splits 31.3 us). With the
-    // dedicated combiner (at most kCombMaxGroups pairs) every pair also takes
-    // a combiner workgroup, and one more CU per pair left free measured best
-    // (ctx 32k, 8 heads: 30 / 31 / 32 splits 28.5 / 28.9 / 29.3 us).
-    const int room = pairs <= kCombMaxGroups ? (cus - 2 * pairs) / pairs : cus / pairs;
-    splits = std::max(splits, std::min(ceil_div(max_seq_len, 1024), std::max(1, room)));
-    splits = std::min(splits, std::max(1, ceil_div(max_seq_len, kMinSpan)));
-    return std::min(std::max(splits, 1), kMaxSplits);
+    // workgroups ran 40.5 us, 32 splits 29.6 us, 64 splits 31.3 us). A launch
+    // that takes the dedicated combiner gives each pair a combiner workgroup,
+    // and one more CU per pair left free measured best (ctx 32k, 8 heads: 30 /
+    // 31 / 32 splits 28.5 / 28.9 / 29.3 us); the room for splits is then
+    // (CUs - 2 pairs) / pairs.
+    auto pick = [&](int room) {
+        int sp = std::max(base, std::min(ceil_div(max_seq_len, 1024), std::max(1, room)));
+        sp = std::min(sp, std::max(1, ceil_div(max_seq_len, kMinSpan)));
+        return std::min(std::max(sp, 1), kMaxSplits);
+    };
+    if (combiner && pairs <= kCombMaxGroups) {
+        const int sp = pick((cus - 2 * pairs) / pairs);
+        if (sp <= kCombSplits) return sp;  // the launch does take the combiner
+    }
+    return pick(cus / pairs);
+}
+
+int default_splits(int max_seq_len, int batch, int n_kv_heads) {
+    return default_splits_for(max_seq_len, batch, n_kv_heads, true);
 }
 
 // Smallest split count whose span fits the LDS-staged block table.
@@ -1717,7 +1744,9 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     if (!q || !k_cache || !v_cache || !out || max_seq_len <= 0) return AF_ERR_INVALID_ARG;
     if (int st = check_heads(head_dim, n_q_heads, n_kv_heads)) return st;
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return AF_ERR_INVALID_ARG;
-    if (num_splits <= 0) num_splits = default_splits(max_seq_len, 1, n_kv_heads);
+    if (num_splits <= 0)
+        num_splits = default_splits_for(max_seq_len, 1, n_kv_heads,
+                                        combiner_shape(n_q_heads / n_kv_heads, head_dim));
     if (num_splits > kMaxSplits) return AF_ERR_INVALID_ARG;
     if (n_kv_heads > kMaxCounters) return AF_ERR_UNSUPPORTED;
     if (!workspace || workspace_bytes < attn_workspace_bytes(1, n_q_heads, head_dim, num_splits))
@@ -1754,6 +1783,7 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     int grid = num_splits * n_kv_heads;
     if (use_combiner(1, n_kv_heads, num_splits, n_q_heads / n_kv_heads, head_dim)) {
         a.flags = w.flags;
+        a.gens = w.gens;
         a.split_wgs = grid;
         grid += n_kv_heads;  // one combiner per KV head, dispatched after every split
     }
@@ -1808,7 +1838,10 @@ extern "C" int af_cached_attention(const void* q, const void* k_cache, const voi
     int st = owned_workspace(1, n_q_heads, head_dim, static_cast<hipStream_t>(stream), &ws, &bytes);
     if (st) return st;
     return af_cached_attention_ex(q, k_cache, v_cache, out, seq_len, nullptr, seq_len, head_dim,
-                                  n_q_heads, n_kv_heads, default_splits(seq_len, 1, n_kv_heads), ws,
+                                  n_q_heads, n_kv_heads,
+                                  default_splits_for(seq_len, 1, n_kv_heads,
+                                                     combiner_shape(n_q_heads / n_kv_heads, head_dim)),
+                                  ws,
                                   bytes, stream);
 }
 
@@ -1851,7 +1884,8 @@ extern "C" int af_cached_attention_noalloc(const void* q, const void* k_cache,
                                            af_stream_t stream) {
     if (seq_len <= 0) return AF_ERR_INVALID_ARG;
     if (int st = check_heads(head_dim, n_q_heads, n_kv_heads)) return st;
-    const int splits = default_splits(seq_len, 1, n_kv_heads);
+    const int splits = default_splits_for(seq_len, 1, n_kv_heads,
+                                          combiner_shape(n_q_heads / n_kv_heads, head_dim));
     const size_t need = attn_workspace_bytes(1, n_q_heads, head_dim, splits);
     if (need > kScratchBytes) return AF_ERR_WORKSPACE;  // shape beyond the static scratch
     void* ws = nullptr;
@@ -1918,7 +1952,7 @@ static int paged_attention(void* q, int q_stride, const af_kv_pool* pool, int la
     int span = kMinSpan;
     bool persistent_ok = false;  // the default partition of a batch may run persistent
     if (num_splits <= 0) {
-        num_splits = std::max(default_splits(suffix_max, batch, nkv), min_sp);
+        num_splits = std::max(default_splits_for(suffix_max, batch, nkv, false), min_sp);
         span = default_span(batch, nkv);
         // (FP8 pools; the fp16 kernel streams faster than its per-item
         // set-up and merge let a persistent workgroup overlap, so fp16 batches

@@ -106,7 +106,17 @@ int af_rope_append(void* qkv_out, void* k_cache, void* v_cache, const float* cos
 /* Replaces launch_cached_attention (include/ops/kernel.h:93-103,
  * src/kernel/tiled_attention.cu:275-296), same arguments. Split-K over the
  * sequence with a library-owned workspace (allocated on the first call per
- * device; call af_attention_reserve() first when the call will be captured). */
+ * device; call af_attention_reserve() first when the call will be captured).
+ * Combiner timeout: with the default split count (2..32 splits for up to 16 KV
+ * heads, head_dim 128, up to 4 query heads per KV head) one combiner workgroup
+ * per KV head merges the splits' partials, waiting on each split's ready flag
+ * with a bounded poll (about a second). Forward progress rests on in-order
+ * workgroup dispatch: the combiners have the highest workgroup ids, so every
+ * split is resident before a combiner waits. If a split never publishes, the
+ * affected outputs are NaN; this entry point has no status argument, so NaN
+ * is the only signal (af_decode_attention_fused also stores AF_ERR_TIMEOUT).
+ * Flags carry a per-launch generation, so a late flag never matches a later
+ * launch. */
 int af_cached_attention(const void* q, const void* k_cache, const void* v_cache, void* out,
                         int seq_len, int head_dim, int n_q_heads, int n_kv_heads,
                         af_stream_t stream);
@@ -146,7 +156,8 @@ int af_attention_default_splits(int max_seq_len, int batch, int n_kv_heads);
  * splits, n_kv_heads <= 16, head_dim 128 and up to 4 query heads per KV head,
  * one combiner workgroup per KV head merges the splits' partials as they are
  * published (a combiner that waits about a second for a split that never
- * publishes writes NaN; the fused form then stores AF_ERR_TIMEOUT). */
+ * publishes writes NaN; the fused form then stores AF_ERR_TIMEOUT; see
+ * af_cached_attention for the dispatch-order rule it rests on). */
 int af_cached_attention_ex(const void* q, const void* k_cache, const void* v_cache, void* out,
                            int seq_len, const int32_t* d_seq_len, int max_seq_len, int head_dim,
                            int n_q_heads, int n_kv_heads, int num_splits, void* workspace,

@@ -84,6 +84,9 @@ def test_default_split_counts():
     assert kv.default_splits(1025, 1, 8) == 17   # one 64-row step per split
     assert kv.default_splits(8193, 32, 8) == 17  # batched: ceil(8193 / 512)
     assert kv.default_splits(0, 1, 8) == 1
+    # more splits than the combiner form takes (32): no CUs held back for combiners
+    assert kv.default_splits(200000, 1, 2) == 128  # kMaxSplits; 126 with the combiner's room
+    assert kv.default_splits(32769, 1, 4) == 48    # 3/4 of a workgroup per CU
 
 
 def test_shared_prefix_argument_checks_without_gpu():

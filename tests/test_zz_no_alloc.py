@@ -50,12 +50,12 @@ def test_noalloc_attention_matches_allocating_entry_point(gpu):
 
 def test_noalloc_rejects_shapes_beyond_the_scratch(gpu):
     lib = atomflow_amd.lib()
-    # 128 Q heads x head_dim 128 over 2 KV heads at 200k tokens: 126 splits (one
-    # CU per pair left for its combiner and one spare), an 8.1 MiB workspace,
-    # more than the array holds. Rejected before any launch, so the (small)
-    # buffers are never read.
-    assert lib.af_attention_default_splits(200000, 1, 2) == 126
-    assert (lib.af_attention_workspace_size(1, 128, 2, 128, 126)
+    # 128 Q heads x head_dim 128 over 2 KV heads at 200k tokens: 128 splits (more
+    # than the combiner form takes, so no CUs are held back for combiners), an
+    # 8.2 MiB workspace, more than the array holds. Rejected before any launch,
+    # so the (small) buffers are never read.
+    assert lib.af_attention_default_splits(200000, 1, 2) == 128
+    assert (lib.af_attention_workspace_size(1, 128, 2, 128, 128)
             > lib.af_cached_attention_noalloc_max_bytes())
     d = dev.DeviceBuffer(4096)
     p = ctypes.c_void_p(d.ptr)
