@@ -2,11 +2,14 @@
 release/acquire fence. It relies on gfx950 instruction semantics instead:
 agent-scope stores (`sc1`) retired by `s_waitcnt vmcnt(0)`, an `s_barrier`,
 then one returning `global_atomic_add`; the last arrival reads with
-agent-scope loads (`sc1`) issued after that atomic. This test compiles
-decode_attention.hip for gfx950 (device code only, assembly out) and checks
-that order in every instantiation that has a combine, so a compiler change
-that reorders or drops any of it fails here, on the CPU. The key pieces of
-prefill_attention_kernel publish and merge the same way and are checked too."""
+agent-scope loads (`sc1`) issued after that atomic. The dedicated-combiner
+form publishes with an agent-scope ready-flag store behind the same wait and
+barrier, and the persistent form's arrival follows the same rule. This test
+compiles decode_attention.hip for gfx950 (device code only, assembly out) and
+checks that order in every instantiation, read to the end of each function,
+so a compiler change that reorders or drops any of it fails here, on the CPU.
+The key pieces of prefill_attention_kernel publish and merge the same way and
+are checked too."""
 import os
 import re
 import shutil
@@ -29,11 +32,44 @@ def _compile(tmp_path, arch="gfx950", src="decode_attention"):
     return r, out
 
 
-def _functions(asm, kernel="decode_attn_kernel", end="s_endpgm"):
+def _functions(asm, kernel="decode_attn_kernel", end=r"\.Lfunc_end"):
+    """(name, instructions) of every function whose name contains `kernel`, read
+    to its end (early exits end in s_endpgm blocks of their own)."""
     pat = re.compile(r"^(_Z\S*" + kernel + r"\S*):[^\n]*\n(.*?)" + end, re.S | re.M)
     for name, body in pat.findall(asm):
         lines = [l.strip() for l in body.splitlines()]
         yield name, [l for l in lines if l and not l.startswith(";") and not l.startswith(".")]
+
+
+def _is_mem(l):
+    return l.startswith(("global_", "buffer_", "flat_"))
+
+
+def _full_wait(l):
+    return l.startswith("s_waitcnt") and ("vmcnt(0)" in l or l == "s_waitcnt 0")
+
+
+def _sc1_stores(ins):
+    return [i for i, l in enumerate(ins) if l.startswith("global_store") and " sc1" in l]
+
+
+def _publication(name, ins, signal):
+    """The partial records' agent-scope stores, a full vector-memory wait, an
+    s_barrier and then the instruction at index `signal` (the arrival atomic or
+    the ready-flag store), with no memory instruction between the wait and it.
+    Returns the wait's index."""
+    bar = max(i for i in range(signal) if ins[i].startswith("s_barrier"))
+    wait = max(i for i in range(bar) if ins[i].startswith("s_waitcnt"))
+    assert _full_wait(ins[wait]), (name, ins[wait])
+    assert not any(_is_mem(l) for l in ins[wait + 1:signal]), (name, ins[wait + 1:signal])
+    # partial records (o pair, m, l) go out with agent-scope stores before the wait
+    records = [i for i in _sc1_stores(ins) if i < wait]
+    assert len(records) >= 3, (name, [ins[i] for i in records])
+    return wait
+
+
+def _arrival_atomics(ins):
+    return [i for i, l in enumerate(ins) if l.startswith("global_atomic")]
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None,
@@ -42,34 +78,62 @@ def test_combine_publication_order(tmp_path):
     r, out = _compile(tmp_path)
     assert r.returncode == 0, r.stderr[-2000:]
     asm = open(out).read()
-    checked = 0
-    for name, ins in _functions(asm):
-        atomics = [i for i, l in enumerate(ins) if l.startswith("global_atomic")]
-        if not atomics:
-            continue  # an instantiation whose grid never splits has no combine
+    grid = comb = persistent = 0
+    for name, ins in _functions(asm, "decode_attn_kernel"):
+        atomics = _arrival_atomics(ins)
+        if name.endswith("Lb1EEEvNS0_8AttnArgsE") and "decode_attn_kernelI" in name:
+            # dedicated-combiner form: no arrival counter; each split publishes
+            # with its ready flag, an agent-scope store behind the same wait and
+            # barrier, and the combiner polls the flags and loads the records
+            # with agent-scope loads
+            assert not atomics, (name, [ins[i] for i in atomics])
+            flags = [i for i in _sc1_stores(ins) if ins[i].startswith("global_store_dword ")]
+            published = []
+            for f in flags:
+                try:
+                    published.append(_publication(name, ins, f))
+                except (AssertionError, ValueError):
+                    continue
+            assert len(published) == 1, (name, [ins[i] for i in flags])
+            loads = [i for i, l in enumerate(ins) if l.startswith("global_load") and " sc1" in l]
+            assert len(loads) >= 3, (name, len(loads))  # generation, flags, records
+            comb += 1
+            continue
+        # every other instantiation: one returning, agent-scope arrival atomic
         assert len(atomics) == 1, (name, [ins[i] for i in atomics])
         a = atomics[0]
         assert re.match(r"global_atomic_add\s+v\d+, v\d+, v\d+, s\[\d+:\d+\]\s+sc0$", ins[a]), \
             (name, ins[a])  # returning (sc0), agent scope: no sc1 / nt bits
-        # the barrier the atomic waits behind, and the full vmcnt wait before it
-        bar = max(i for i in range(a) if ins[i].startswith("s_barrier"))
-        wait = max(i for i in range(bar) if ins[i].startswith("s_waitcnt"))
-        assert "vmcnt(0)" in ins[wait] or ins[wait] == "s_waitcnt 0", (name, ins[wait])
-        between = ins[wait + 1:a]
-        assert not any(l.startswith(("global_", "buffer_", "flat_")) for l in between), \
-            (name, between)
-        # partial records: agent-scope stores, all before that wait
-        stores = [i for i, l in enumerate(ins) if l.startswith("global_store") and " sc1" in l]
-        before = [i for i in stores if i < wait]
-        after = [i for i in stores if i > a]
-        assert len(before) >= 3, (name, [ins[i] for i in stores])  # o pair + m + l
+        wait = _publication(name, ins, a)
+        after = [i for i in _sc1_stores(ins) if i > a]
         assert len(after) <= 1, (name, [ins[i] for i in after])  # the counter re-arm only
-        assert not any(wait < i < a for i in stores)
         # the combine's reads: agent-scope loads, none before the atomic
         loads = [i for i, l in enumerate(ins) if l.startswith("global_load") and " sc1" in l]
         assert loads and min(loads) > a, (name, min(loads) if loads else None, a)
-        checked += 1
-    assert checked >= 30, checked
+        assert not any(wait < i < a for i in _sc1_stores(ins))
+        grid += 1
+    for name, ins in _functions(asm, "decode_attn_persistent"):
+        # item claim, arrival, finished-workgroup count: the arrival is the one
+        # behind the records' publication
+        atomics = _arrival_atomics(ins)
+        assert len(atomics) == 3, (name, [ins[i] for i in atomics])
+        arrivals = []
+        for a in atomics:
+            try:
+                _publication(name, ins, a)
+                arrivals.append(a)
+            except (AssertionError, ValueError):
+                continue
+        assert len(arrivals) == 1, (name, [ins[i] for i in atomics])
+        a = arrivals[0]
+        assert re.match(r"global_atomic_add\s+v\d+, v\d+, v\d+, s\[\d+:\d+\]\s+sc0$", ins[a]), \
+            (name, ins[a])
+        loads = [i for i, l in enumerate(ins) if l.startswith("global_load") and " sc1" in l and i > a]
+        assert len(loads) >= 3, (name, len(loads))  # (m, l) and the first batch of records
+        persistent += 1
+    # 62 grid-form kernels (contiguous / paged, fp16 / FP8, fused, pairs, 3wg),
+    # 8 dedicated-combiner kernels, 30 persistent kernels
+    assert grid >= 60 and comb == 8 and persistent == 30, (grid, comb, persistent)
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None,
@@ -89,7 +153,7 @@ def test_prefill_key_piece_publication_order(tmp_path):
     checked = 0
     # the whole function: early exits (a piece a lighter tile does not need) end
     # in s_endpgm blocks of their own
-    for name, ins in _functions(asm, "prefill_attention_kernel", end=r"\.Lfunc_end"):
+    for name, ins in _functions(asm, "prefill_attention_kernel"):
         atomics = [i for i, l in enumerate(ins) if l.startswith("global_atomic")]
         assert len(atomics) == 1, (name, [ins[i] for i in atomics])
         a = atomics[0]
