@@ -15,6 +15,14 @@
   oracle: the rotated query and the appended K/V codes bit for bit, attention
   within the FP8 bar and the fp16 bar. The unfused paged attention over the
   updated pool must equal the fused output bit for bit.
+* configs[2] at its stated scale: an fp16 paged pool of 28 layers and
+  16-token blocks (about 16 GiB, sized like bench.py's: the blocks the batch
+  needs plus 10 %), 32 sequences with contexts uniform in [128, 8192],
+  permuted block tables. The fused paged decode step (the compact batched
+  grid) runs at layer 0 and at layer 27, whose slabs start past 2^32 bytes.
+  Sampled sequences are checked against the oracle (the rotated query and the
+  appended K/V rows bit for bit, attention at the fp16 bar), and the unfused
+  kernel over the updated pool must equal the fused output bit for bit.
 * configs[1] as bench.py times it: the 28-layer contiguous stack at ctx 8192,
   every layer's fused step in one captured hipGraph, each layer against the
   oracle.
@@ -23,7 +31,7 @@ import numpy as np
 import pytest
 
 import oracle
-from atomflow_amd import AF_KV_FP8_E4M3
+from atomflow_amd import AF_KV_FP16, AF_KV_FP8_E4M3
 from atomflow_amd import check as af_check
 from atomflow_amd import device as dev
 from atomflow_amd import kv
@@ -239,6 +247,92 @@ def test_config5_fp8_paged_at_scale(gpu):
             what = f"configs[4] layer {layer} seq {b} L={int(lens[b])}"
             assert_attn_close(got[b], ref, ATOL_FP8, RTOL_FP8, what=what + " (fp8 bar)")
             assert_attn_close(got[b], ref, what=what + " (fp16 bar)")
+        del d_qkv, d_out, d_out2
+    pool.free()
+    bm.close()
+
+
+def test_config3_fp16_paged_at_scale(gpu):
+    """fp16 paged pool of ~16 GiB, B = 32, L in [128, 8192]."""
+    bs, layers, B = 16, 28, 32
+    r = np.random.Generator(np.random.PCG64(SEED_BASE + 3))
+    ctx = r.integers(128, 8193, B)
+    lens_after = ctx + 1
+    need = int(sum((int(n) + bs - 1) // bs for n in lens_after))
+    total = int(need * 1.1) + 8  # bench.py's sizing: 10 % free-list headroom
+    bm = kv.BlockManager(total, bs, layers, NKV, HD, AF_KV_FP16)
+    ids = [bm.allocate_block() for _ in range(total)]
+    for b in r.permutation(ids):
+        bm.free_block(int(b))
+    seqs = []
+    for n in ctx:
+        sq = bm.seq_create()
+        assert not isinstance(bm.seq_extend(sq, int(n)), int)
+        seqs.append(sq)
+    slots, positions, copies = bm.plan_decode(seqs)
+    assert len(copies) == 0 and np.array_equal(positions, ctx)
+    max_len = int(lens_after.max())
+    max_blocks = (max_len + bs - 1) // bs
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    desc = bm.pool()
+    nbytes = kv.pool_bytes(desc)
+    slab_bytes = total * bs * KV_DIM * 2
+    say(f"configs[2] at scale: {total} blocks, pool {nbytes / 2**30:.1f} GiB, layer 27 K slab at "
+        f"byte {54 * slab_bytes}, max block id in use {int(tables.max())}")
+    assert nbytes > 2**33 and 54 * slab_bytes > 2**32
+    assert B * NKV * 2 >= dev.device_info()["compute_units"]  # the batched (compact grid) form
+    lib = af_lib()
+    pool = dev.DeviceBuffer(nbytes)
+    af_check(lib.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, None), "fill pool")
+    bm.attach_pool(pool.ptr, None)
+    desc = bm.pool()
+    max_pos = max_len + 1
+    c, s = oracle.rope_table(max_pos, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    d_tables, d_lens = up(tables), up(lens)
+    d_slots, d_pos = up(slots), up(positions)
+    ws = kv.AttentionWorkspace(B, NQ, NKV, HD, 0)
+    sample = _sample(r, tables, lens, 6)
+    for layer in (0, layers - 1):
+        qkv = (r.standard_normal((B, QKV))).astype(np.float16)
+        d_qkv = up(qkv)
+        d_out = dev.DeviceBuffer(B * Q_DIM * 2)
+        d_out2 = dev.DeviceBuffer(B * Q_DIM * 2)
+        say(f"layer {layer}: fused paged decode over {B} sequences, {int(lens.sum())} rows")
+        kv.launch_paged_decode_fused(d_qkv, B, desc, layer, d_slots, d_pos, d_c, d_s, max_pos,
+                                     d_tables, max_blocks, max_len, d_out, Q_DIM, NQ, ws)
+        kv.launch_paged_attention(d_qkv, QKV, desc, layer, d_tables, max_blocks, d_lens, B,
+                                  max_len, d_out2, Q_DIM, NQ, ws)
+        dev.synchronize()
+        got = d_out.download(np.float16, (B, Q_DIM))
+        assert np.array_equal(bits(got), bits(d_out2.download(np.float16, (B, Q_DIM))))
+        got_qkv = d_qkv.download(np.float16, (B, QKV))
+        base_k = (2 * layer) * slab_bytes
+        base_v = (2 * layer + 1) * slab_bytes
+        row_bytes = KV_DIM * 2
+        for b in sample:
+            n_blk = (int(lens[b]) + bs - 1) // bs
+            blk = tables[b, :n_blk]
+            kslab = np.empty((n_blk * bs, KV_DIM), np.float16)
+            vslab = np.empty((n_blk * bs, KV_DIM), np.float16)
+            for i, bid in enumerate(blk):
+                off = int(bid) * bs * row_bytes
+                kslab[i * bs:(i + 1) * bs] = pool.download(np.float16, (bs, KV_DIM),
+                                                           offset=base_k + off)
+                vslab[i * bs:(i + 1) * bs] = pool.download(np.float16, (bs, KV_DIM),
+                                                           offset=base_v + off)
+            pos = int(positions[b])
+            got_k, got_v = kslab[pos].copy(), vslab[pos].copy()
+            rq = oracle.rope_append(qkv[b], np.zeros((1, KV_DIM), np.float16),
+                                    np.zeros((1, KV_DIM), np.float16), c[pos:], s[pos:], 0, NQ,
+                                    NKV, HD)
+            assert np.array_equal(bits(got_qkv[b]), bits(rq)), f"rotated qkv, sequence {b}"
+            assert np.array_equal(bits(got_k), bits(rq[Q_DIM:Q_DIM + KV_DIM])), f"K row, seq {b}"
+            assert np.array_equal(bits(got_v), bits(rq[Q_DIM + KV_DIM:])), f"V row, seq {b}"
+            ref = oracle.paged_attention_f16(rq[:Q_DIM], kslab, vslab,
+                                             np.arange(n_blk, dtype=np.int32), int(lens[b]), bs,
+                                             NQ, NKV, HD)
+            assert_attn_close(got[b], ref, what=f"configs[2] layer {layer} seq {b} L={int(lens[b])}")
         del d_qkv, d_out, d_out2
     pool.free()
     bm.close()
