@@ -13,7 +13,9 @@ import subprocess
 from . import _abi
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libatomflow_kv.so")
+# ATOMFLOW_KV_LIB selects another build of the same library (the host sanitizer
+# build of tests/test_host_sanitizers.py); the default is the in-tree build.
+LIB_PATH = os.environ.get("ATOMFLOW_KV_LIB") or os.path.join(_HERE, "libatomflow_kv.so")
 _lib = None
 
 # af_kv.h status codes
