@@ -50,9 +50,9 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 //                                per (sequence, KV head); words [kFlagBase,
 //                                kFlagBase + kCombMaxGroups * kCombSplits):
 //                                ready flags of the dedicated-combiner form, one
-//                                per (sequence, KV head, split), then one
-//                                generation word per (sequence, KV head) (a flag
-//                                holds its launch's generation + 1); the last two
+//                                per (sequence, KV head, split), then the poison
+//                                word (set by a combiner that timed out); the
+//                                last two
 //                                words: the persistent form's item counters.
 //                                Counters are zero between launches (each launch
 //                                re-zeroes what it used)
@@ -77,13 +77,12 @@ static_assert(kFlagBase + kCombMaxGroups * kCombSplits <= int(kCounterBytes / si
 // two words of the counter region).
 constexpr int kItemCounter = int(kCounterBytes / sizeof(uint32_t)) - 2;
 constexpr int kDoneCounter = kItemCounter + 1;
-constexpr int kGenBase = kFlagBase + kCombMaxGroups * kCombSplits;
-static_assert(kGenBase + kCombMaxGroups <= kItemCounter, "counter words overlap");
+constexpr int kPoisonWord = kFlagBase + kCombMaxGroups * kCombSplits;
+static_assert(kPoisonWord < kItemCounter, "counter words overlap");
 
 struct AttnWorkspace {
     uint32_t* counters;
     uint32_t* flags;
-    uint32_t* gens;
     float* part_ml;
     float* part_o;
 };
@@ -99,7 +98,6 @@ inline AttnWorkspace attn_workspace_carve(void* base, int batch, int n_q_heads, 
     AttnWorkspace w;
     w.counters = reinterpret_cast<uint32_t*>(p);
     w.flags = w.counters + kFlagBase;
-    w.gens = w.counters + kGenBase;
     p += kCounterBytes;
     w.part_ml = reinterpret_cast<float*>(p);
     p += align_up(size_t(batch) * n_q_heads * num_splits * 2 * sizeof(float), 256);

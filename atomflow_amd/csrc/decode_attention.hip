@@ -145,7 +145,6 @@ struct AttnArgs {
     // batch * n_kv_heads are one combiner per (sequence, KV head) that waits on
     // its splits' ready flags ([batch * n_kv_heads][kCombSplits]).
     uint32_t* flags;
-    uint32_t* gens;      // generation word of each (sequence, KV head): flags carry gen + 1
     int32_t split_wgs;
     int32_t batch;       // sequences (the persistent form claims items over their rows)
     int32_t item_big;    // persistent form: row-steps of a big / small item
@@ -239,10 +238,13 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
     const float* ml = a.part_ml + grp * a.rec_stride * 2 * GQ;
     const uint64_t* po = reinterpret_cast<const uint64_t*>(a.part_o + grp * a.rec_stride * GHD);
     uint32_t* flags = a.flags + grp * kCombSplits;
-    // A ready flag holds the launch's generation + 1 (the generation word is
-    // read first, before anything else is loaded); flags of an earlier launch
-    // never match, so the flags are not re-zeroed.
-    const uint32_t ready = __hip_atomic_load(a.gens + grp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    // A combiner that gave up poisons the workspace (a split that publishes
+    // after that sets a flag nothing clears); every later combiner on it then
+    // trusts no flag and writes NaN with AF_ERR_TIMEOUT, until the workspace
+    // is re-initialised.
+    uint32_t* poison = a.counters + kPoisonWord;
+    const bool poisoned =
+        __hip_atomic_load(poison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
 
     // The query heads are stored back rotated, as the last-arrival combine does
     // (every split has read them once the records are complete). Their inputs
@@ -268,12 +270,12 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
     uint64_t ov[kCombSplits];
 #pragma unroll
     for (int sp = 0; sp < kCombSplits; ++sp) ov[sp] = 0;
-    if (act) {
+    if (act && !poisoned) {
         for (int polls = 0; have != all && polls < kCombMaxPolls; ++polls) {
             const uint32_t f = lane < n_active ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED,
                                                                    __HIP_MEMORY_SCOPE_AGENT)
                                                : 0u;
-            const uint32_t fresh = uint32_t(__builtin_amdgcn_ballot_w64(f == ready)) & all & ~have;
+            const uint32_t fresh = uint32_t(__builtin_amdgcn_ballot_w64(f != 0u)) & all & ~have;
             if (lane < kCombSplits && ((fresh >> lane) & 1u)) {
                 mv = load_agent(ml + lane * 2 * GQ + gh);
                 lv = load_agent(ml + lane * 2 * GQ + GQ + gh);
@@ -318,14 +320,15 @@ __device__ __forceinline__ void combine_dedicated(const AttnArgs& a, int b, int 
         }
     }
     AF_STAMP(7);
-    if (timed_out && lane == 0 && a.d_status) *a.d_status = AF_ERR_TIMEOUT;
-    // Every wave has read Q and finished polling past this barrier: the next
-    // launch's flags carry the next generation, and the rotated Q is stored.
-    // Every split read the generation in its first instructions, and all of
-    // them were dispatched before this combiner (workgroups start in id order),
-    // so even after a timeout no split of this launch reads the new generation.
+    if (timed_out && lane == 0) {
+        __hip_atomic_store(poison, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.d_status) *a.d_status = AF_ERR_TIMEOUT;
+    }
+    // Every wave has read Q and finished polling past this barrier: the flags
+    // return to zero for the next launch and the rotated Q is stored.
     __syncthreads();
-    if (tid == 0) __hip_atomic_store(a.gens + grp, ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < n_active)
+        __hip_atomic_store(flags + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (FUSED)
         if (act) *reinterpret_cast<uint32_t*>(qh + d) = qrot;
 }
@@ -447,13 +450,6 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     uint16_t* out_b = a.out + size_t(b) * a.out_stride + size_t(hw) * GHD;
     const bool direct = n_active == 1 && pre_used == 0;  // no combine: write the output
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
-    // Dedicated-combiner form: the generation of (b, hw), loaded before
-    // anything else; the ready flag is set to it + 1.
-    uint32_t gen = 0;
-    if constexpr (COMB)
-        if (!direct)
-            gen = __hip_atomic_load(a.gens + size_t(b) * nhw + hw, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
     AF_STAMP(0);
 
     // ---- stage this split's block-table entries (paged) --------------------
@@ -1001,7 +997,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     AF_STAMP(6);
     if constexpr (COMB) {  // the dedicated combiner reads the partial once the flag is set
         if (tid == 0)
-            __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, gen + 1u,
+            __hip_atomic_store(a.flags + (size_t(b) * nhw + hw) * kCombSplits + split, 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -1783,7 +1779,6 @@ static int contiguous_attention(void* q, int q_stride, void* k_cache, void* v_ca
     int grid = num_splits * n_kv_heads;
     if (use_combiner(1, n_kv_heads, num_splits, n_q_heads / n_kv_heads, head_dim)) {
         a.flags = w.flags;
-        a.gens = w.gens;
         a.split_wgs = grid;
         grid += n_kv_heads;  // one combiner per KV head, dispatched after every split
     }

@@ -115,8 +115,13 @@ int af_rope_append(void* qkv_out, void* k_cache, void* v_cache, const float* cos
  * split is resident before a combiner waits. If a split never publishes, the
  * affected outputs are NaN; this entry point has no status argument, so NaN
  * is the only signal (af_decode_attention_fused also stores AF_ERR_TIMEOUT).
- * Flags carry a per-launch generation, so a late flag never matches a later
- * launch. */
+ * A combiner that gives up poisons the workspace: every later launch on it
+ * returns NaN for the pairs the combiner merges (and AF_ERR_TIMEOUT where there
+ * is a status) until af_attention_workspace_init clears it, because a split of
+ * the failed launch may still set a flag that a later launch would trust. The
+ * library-owned workspace of this entry point (and the static array of the
+ * _noalloc form) then stays poisoned until the process ends: a timeout means
+ * the device left a resident workgroup unrun for about a second. */
 int af_cached_attention(const void* q, const void* k_cache, const void* v_cache, void* out,
                         int seq_len, int head_dim, int n_q_heads, int n_kv_heads,
                         af_stream_t stream);
@@ -145,7 +150,9 @@ int af_attention_reserve(int batch, int n_q_heads, int n_kv_heads, int head_dim)
 size_t af_attention_workspace_size(int batch, int n_q_heads, int n_kv_heads, int head_dim,
                                    int num_splits);
 /* Zero-fills a workspace (a fill kernel, not a memset node). Needed once after
- * allocation; every attention launch leaves its counters at zero again. */
+ * allocation; every attention launch leaves its counters at zero again, except
+ * after a combiner timeout, which leaves the workspace poisoned (see
+ * af_cached_attention) until this is called again. */
 int af_attention_workspace_init(void* workspace, size_t workspace_bytes, af_stream_t stream);
 /* Split count the library picks for a given longest sequence and batch. */
 int af_attention_default_splits(int max_seq_len, int batch, int n_kv_heads);

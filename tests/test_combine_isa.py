@@ -96,7 +96,7 @@ def test_combine_publication_order(tmp_path):
                     continue
             assert len(published) == 1, (name, [ins[i] for i in flags])
             loads = [i for i, l in enumerate(ins) if l.startswith("global_load") and " sc1" in l]
-            assert len(loads) >= 3, (name, len(loads))  # generation, flags, records
+            assert len(loads) >= 3, (name, len(loads))  # poison word, flags, records
             comb += 1
             continue
         # every other instantiation: one returning, agent-scope arrival atomic
