@@ -254,6 +254,10 @@ class AttentionWorkspace:
         if self.nbytes == 0:
             raise AfError(-2, "af_attention_workspace_size")
         self.buf = DeviceBuffer(self.nbytes)
+        self.reset(stream)
+
+    def reset(self, stream=None):
+        """Zero the counters again (clears the poison a timed-out combiner leaves)."""
         check(lib().af_attention_workspace_init(self.buf.ptr, self.nbytes, _s(stream)),
               "af_attention_workspace_init")
 

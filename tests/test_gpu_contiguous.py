@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
+from atomflow_amd import AF_ERR_TIMEOUT
 from atomflow_amd import device as dev
 from atomflow_amd import kv
 from inputs import (HD, KV_DIM, NKV, NQ, Q_DIM, SEED_BASE, THETA, assert_attn_close,
@@ -338,3 +339,52 @@ def test_fused_graph_replay_advances_position(gpu):
     assert d_pos.download(np.int32)[0] == pos0 + steps and d_st.download(np.int32)[0] == 0
     graph.destroy()
     stream.destroy()
+
+
+# Counter word a combiner that timed out sets (kFlagBase + kCombMaxGroups * kCombSplits).
+POISON_BYTE = (8192 + 16 * 32) * 4
+
+
+def test_poisoned_workspace_writes_nan_and_status(gpu):
+    """A combiner that gives up poisons its workspace. The host sets that word here (no kernel
+    is made to wait): every later dedicated-combiner launch on the workspace writes NaN and
+    AF_ERR_TIMEOUT while the splits' append still lands, and af_attention_workspace_init
+    brings back the same bits as before."""
+    pos, max_seq = 4000, 4096
+    splits = kv.default_splits(pos + 1, 1, NKV)
+    assert 2 <= splits <= 32  # the dedicated-combiner form
+    say(f"poisoned workspace pos={pos} splits={splits}")
+    c, s = oracle.rope_table(max_seq, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    qkv, k, v = contiguous_case(max_seq, pos, 901)
+    ws = kv.AttentionWorkspace(1, NQ, NKV, HD, 0)
+
+    def fused():
+        d_qkv, d_k, d_v, d_o = up(qkv), up(k), up(v), dev.DeviceBuffer(Q_DIM * 2)
+        d_st = up(np.array([0], np.int32))
+        kv.launch_decode_attention_fused(d_qkv, d_k, d_v, d_c, d_s, pos, max_seq, d_o, NQ, NKV,
+                                         HD, ws, d_status=d_st)
+        dev.synchronize()
+        return d_o.download(np.uint16), d_k.download(np.uint16), int(d_st.download(np.int32)[0])
+
+    def attention():
+        d_o = dev.DeviceBuffer(Q_DIM * 2)
+        kv.launch_cached_attention_ex(up(qkv), up(k), up(v), d_o, pos, max_seq, HD, NQ, NKV, ws)
+        dev.synchronize()
+        return d_o.download(np.uint16)
+
+    o0, k0, st0 = fused()
+    a0 = attention()
+    assert st0 == 0 and np.all(np.isfinite(o0.view(np.float16)))
+    assert np.all(np.isfinite(a0.view(np.float16)))
+    ws.buf.upload(np.array([1], np.uint32), offset=POISON_BYTE)
+    for _ in range(2):  # it stays poisoned
+        o1, k1, st1 = fused()
+        assert st1 == AF_ERR_TIMEOUT
+        assert np.all(np.isnan(o1.view(np.float16)))
+        assert np.array_equal(k1, k0)  # the append is the splits' work
+        assert np.all(np.isnan(attention().view(np.float16)))
+    ws.reset()
+    o2, k2, st2 = fused()
+    assert st2 == 0 and np.array_equal(o2, o0) and np.array_equal(k2, k0)
+    assert np.array_equal(attention(), a0)
