@@ -848,16 +848,24 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
         // larger reference. Lanes 0..7 of each row then hold one partial
         // (m, l, o[]) and the kParts = 4 * kWaves partials per head are summed
         // through LDS.
+        // One v_mul and one v_add_f32 with the DPP operand per value: no
+        // contraction (the DPP operand cannot be an FMA's accumulator), and
+        // the adds stay here, with every lane active (sunk into the
+        // lanes-0..7 branch below they could not read a disabled lane
+        // through DPP and would need a v_mov_dpp each).
 #pragma unroll
         for (int gh = 0; gh < GROUP; ++gh) {
+#pragma clang fp contract(off)
             const float mp = fmaxf(m_run[gh], dpp<0x128>(m_run[gh]));
             const float f = fast_exp2(m_run[gh] - mp);  // groups that saw no row hold l = acc = 0
             const float l = l_run[gh] * f;
             l_run[gh] = l + dpp<0x128>(l);
+            asm volatile("" ::"v"(l_run[gh]));
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
                 const float x = acc[gh][e] * f;
                 acc[gh][e] = x + dpp<0x128>(x);
+                asm volatile("" ::"v"(acc[gh][e]));
             }
             m_run[gh] = mp;
         }
