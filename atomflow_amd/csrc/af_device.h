@@ -59,7 +59,8 @@ __device__ __forceinline__ void rope_rotate(uint16_t x, uint16_t y, float c, flo
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---- cross-lane reductions (wave64) -----------------------------------------
-// DPP move of v (row_mask, bank_mask all lanes; no bound_ctrl).
+// DPP move of v (row_mask, bank_mask all lanes; bound_ctrl: a source lane
+// outside the row would read 0, which none of the controls used here has).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(

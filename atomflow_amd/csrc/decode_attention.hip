@@ -46,8 +46,13 @@ namespace {
 // start, 1 ring prologue issued, 2 main loop entered, 3 rows streamed, 4
 // partials in LDS, 5 partial stores issued, 6 stores acknowledged (flag set).
 // Dedicated-combiner phases: 0 start, 6 last flag seen, 7 output written.
-constexpr int kStampWgs = 2048, kStampPhases = 8;
-__device__ uint64_t g_phase_stamps[kStampWgs][kStampPhases];
+// Grid and dedicated-combiner forms also record 8 kernel entry (before the
+// split mapping) with, in slot 9, the hardware ids XCC_ID | HW_ID << 32 (CU,
+// shader array and engine; one 16-byte store), 10 last-arrival combine done,
+// 11 block-table window staged (paged). Slots are not cleared: a reader keeps
+// a slot only if it is later than the same workgroup's entry.
+constexpr int kStampWgs = 4096, kStampPhases = 12;
+__device__ __align__(16) uint64_t g_phase_stamps[kStampWgs][kStampPhases];
 #define AF_STAMP(ph)                                                                       \
     do {                                                                                   \
         __builtin_amdgcn_sched_barrier(0);                                                 \
@@ -55,9 +60,25 @@ __device__ uint64_t g_phase_stamps[kStampWgs][kStampPhases];
             g_phase_stamps[blockIdx.x][ph] = __builtin_amdgcn_s_memrealtime();             \
         __builtin_amdgcn_sched_barrier(0);                                                 \
     } while (0)
+#define AF_STAMP_ENTRY()                                                                   \
+    do {                                                                                   \
+        __builtin_amdgcn_sched_barrier(0);                                                 \
+        if (threadIdx.x == 0 && blockIdx.x < kStampWgs) {                                  \
+            uint32_t xcc, hwid;                                                            \
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));      \
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));             \
+            const uint64_t t = __builtin_amdgcn_s_memrealtime();                           \
+            *reinterpret_cast<ulonglong2*>(&g_phase_stamps[blockIdx.x][8]) =               \
+                make_ulonglong2(t, uint64_t(xcc) | (uint64_t(hwid) << 32));                \
+        }                                                                                  \
+        __builtin_amdgcn_sched_barrier(0);                                                 \
+    } while (0)
 #else
 #define AF_STAMP(ph) \
     do {             \
+    } while (0)
+#define AF_STAMP_ENTRY() \
+    do {                 \
     } while (0)
 #endif
 
@@ -380,6 +401,18 @@ __device__ __forceinline__ int grid_splits(const AttnArgs& a, int L, int step_ro
     return max(1, min(a.num_splits, (total_steps + span_steps - 1) / span_steps));
 }
 
+// Inclusive prefix sum over the wave's 64 lanes on DPP: row_shr 1, 2, 4, 8
+// within each 16-lane row, then row_bcast 15 and 31 carry the row totals up.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false); // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false); // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
 // One decode-attention work item: rows [t_begin, t_end) of (sequence b, KV
 // head group hw), split `split` of n_active (record slot pre_used + split).
 struct Seg {
@@ -471,6 +504,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
             }
         }
         __syncthreads();
+        AF_STAMP(11);
     }
 
     const uint8_t* kbase = a.k + size_t(h) * LY::kRowBytes + j * 16;
@@ -1101,6 +1135,7 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
             *reinterpret_cast<uint32_t*>(a.q + size_t(b) * a.q_stride + size_t(hw) * GHD + 2 * q2) =
                 *reinterpret_cast<const uint32_t*>(&s_q[2 * q2]);
     }
+    AF_STAMP(10);
 }
 
 // One workgroup = (sequence b, KV head h, split), or with PAIR (sequence b,
@@ -1116,6 +1151,7 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
     const int nkv = a.n_kv_heads;
     const int nhw = nkv / KVH;  // workgroups per (sequence, split)
     int id = blockIdx.x;
+    AF_STAMP_ENTRY();
     // A dedicated combiner decodes as split 0 of its (sequence, KV head).
     const bool comb = COMB && id >= a.split_wgs;
     if (comb) {
@@ -1123,34 +1159,57 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
         id = (c / nhw) * a.num_splits * nhw + c % nhw;
     }
     int hw, split, b;
-    if (a.compact) {
-        __shared__ int32_t s_splits[kThreads];      // splits of each sequence
-        __shared__ int64_t s_first[kThreads + 1];   // exclusive prefix: its first split
-        if (tid < a.batch) {
-            int Lb;
+    int Lc = 0;  // compact grid: the length sequence b attends, from the mapping
+    if (PAGED && a.compact) {
+        // Sequence bb owns nhw * splits(L_bb) consecutive workgroup ids.
+        auto length = [&](int bb) {
             if constexpr (FUSED) {  // the length the fused step attends (0: out of range)
-                const int pb = a.positions ? a.positions[tid] : a.pos_host;
-                const int64_t rb = a.slots ? a.slots[tid] : int64_t(pb);
+                const int pb = a.positions ? a.positions[bb] : a.pos_host;
+                const int64_t rb = a.slots ? a.slots[bb] : int64_t(pb);
                 const bool ok = pb >= 0 && pb < a.max_pos && pb < a.max_seq_len && rb >= 0 &&
                                 rb < a.max_rows;
-                Lb = ok ? pb + 1 : 0;
+                return ok ? pb + 1 : 0;
             } else {
-                Lb = min(a.seq_lens ? a.seq_lens[tid] : a.seq_len_host, a.max_seq_len);
+                return min(a.seq_lens ? a.seq_lens[bb] : a.seq_len_host, a.max_seq_len);
             }
-            // an out-of-range fused append keeps one workgroup (per head) that
-            // reports it, as an empty sequence keeps one for its zero output
-            s_splits[tid] = grid_splits(a, Lb, STEP);
+        };
+        // an out-of-range fused append keeps one workgroup (per head) that
+        // reports it, as an empty sequence keeps one for its zero output
+        int64_t first_b;
+        if (a.batch <= 64) {
+            // The batch fits one wave's lanes: every wave maps on its own (a
+            // wave-wide scan and a ballot; no LDS round trip, no barrier).
+            const int lane = tid & 63;
+            const int Lb = lane < a.batch ? length(lane) : 0;
+            const int n = lane < a.batch ? grid_splits(a, Lb, STEP) : 0;
+            const int incl = wave_inclusive_sum(n);
+            if (id >= int64_t(__builtin_amdgcn_readlane(incl, 63)) * nhw) return;
+            // the first sequence whose splits end past id
+            b = __builtin_ctzll(__builtin_amdgcn_ballot_w64(int64_t(incl) * nhw > id));
+            first_b = __builtin_amdgcn_readlane(incl - n, b);
+            Lc = __builtin_amdgcn_readlane(Lb, b);
+        } else {
+            __shared__ int32_t s_splits[kThreads];     // splits of each sequence
+            __shared__ int32_t s_len[kThreads];        // its length
+            __shared__ int64_t s_first[kThreads + 1];  // exclusive prefix: its first split
+            if (tid < a.batch) {
+                const int Lb = length(tid);
+                s_len[tid] = Lb;
+                s_splits[tid] = grid_splits(a, Lb, STEP);
+            }
+            __syncthreads();
+            block_exclusive_scan(s_splits, s_first, a.batch);
+            if (id >= s_first[a.batch] * nhw) return;
+            int lo = 0, hi = a.batch - 1;  // the last sequence whose first split is <= id
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) / 2;
+                if (s_first[mid] * nhw <= id) lo = mid; else hi = mid - 1;
+            }
+            b = lo;
+            first_b = s_first[b];
+            Lc = s_len[b];
         }
-        __syncthreads();
-        block_exclusive_scan(s_splits, s_first, a.batch);
-        if (id >= s_first[a.batch] * nhw) return;
-        int lo = 0, hi = a.batch - 1;  // the last sequence whose first split is <= id
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) / 2;
-            if (s_first[mid] * nhw <= id) lo = mid; else hi = mid - 1;
-        }
-        b = lo;
-        const int r = id - int(s_first[b] * nhw);
+        const int r = id - int(first_b * nhw);
         hw = r % nhw;
         split = r / nhw;
     } else {
@@ -1162,14 +1221,24 @@ __device__ __forceinline__ void decode_attn_body(const AttnArgs& a) {
 
     int L, pos = 0;
     if constexpr (FUSED) {
-        pos = a.positions ? a.positions[b] : a.pos_host;
-        const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
-        if (pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 || row >= a.max_rows) {
+        bool in_range;
+        if (PAGED && a.compact) {  // the mapping checked the position and the slot
+            in_range = Lc > 0;
+            pos = Lc - 1;
+        } else {
+            pos = a.positions ? a.positions[b] : a.pos_host;
+            const int64_t row = a.slots ? a.slots[b] : int64_t(pos);
+            in_range = !(pos < 0 || pos >= a.max_pos || pos >= a.max_seq_len || row < 0 ||
+                         row >= a.max_rows);
+        }
+        if (!in_range) {
             if (tid == 0 && split == 0 && hw == 0 && !comb && a.d_status)
                 *a.d_status = AF_ERR_OUT_OF_RANGE;
             return;  // out-of-range append: nothing is written
         }
         L = pos + 1;
+    } else if (PAGED && a.compact) {
+        L = Lc;
     } else {
         L = a.seq_lens ? a.seq_lens[b] : a.seq_len_host;
         L = min(L, a.max_seq_len);

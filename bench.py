@@ -81,7 +81,8 @@ def parse():
                     help="also run a plain copy kernel of known size (scales PMC byte counters)")
     ap.add_argument("--stamps", action="store_true",
                     help="run only the per-phase timeline of the configs[1] attention launch "
-                         "(needs libatomflow_kv_stamps.so: make -C atomflow_amd/csrc stamps) and "
+                         "(with --config 3: of the configs[2] paged launch; needs "
+                         "libatomflow_kv_stamps.so: make -C atomflow_amd/csrc stamps) and "
                          "print its JSON object")
     ap.add_argument("--read-probe", action="store_true",
                     help="run only the streaming-read probes (per-launch read ceilings of each "
@@ -1308,6 +1309,140 @@ STAMP_PHASES = ["split start", "ring prologue issued", "main loop entered", "row
 COMBINER_PHASES = {0: "combiner start", 6: "combiner: last flag seen", 7: "combiner: output written"}
 
 
+STAMP_WGS, STAMP_SLOTS = 4096, 12  # the stamps build's table: [workgroup][slot]
+# slots of the grid form beyond STAMP_PHASES: 8 kernel entry, 9 hardware ids
+# (XCC_ID | HW_ID << 32), 10 last-arrival combine done, 11 block table staged;
+# a slot counts only if it is later than the same workgroup's entry (no clearing)
+GRID_PHASES = [(8, "entry"), (0, "mapped (split start)"), (11, "block table staged"),
+               (1, "ring prologue issued"), (2, "main loop entered"), (3, "rows streamed"),
+               (4, "partials in LDS"), (5, "partial stores issued"), (6, "stores acknowledged")]
+
+
+def bench_stamps_paged(args, dev, kv, lib):
+    """Timeline of one configs[2] attention launch (paged fp16, B = 32, the compact
+    grid) from the stamps build: each workgroup's phases, how many workgroups are in
+    each state over time, and per CU the share of the launch during which none of
+    its workgroups is streaming rows. 4 layers (549 MB of KV each, past the MALL)
+    in a graph; the last launch of each of `steps` replays; medians over replays."""
+    import ctypes
+    import atomflow_amd
+    from atomflow_amd import AF_KV_FP16
+
+    layers = 4
+    r = np.random.Generator(np.random.PCG64(0xA70F10 + 3))  # bench_paged's configs[2] draw
+    bs, ctx_lens = 16, r.integers(128, 8193, 32)
+    B = len(ctx_lens)
+    lens_after = ctx_lens + 1
+    need = sum((int(n) + bs - 1) // bs for n in lens_after)
+    total_blocks = int(need * 1.1) + 8
+    bm = kv.BlockManager(total_blocks, bs, layers, NKV, HD, AF_KV_FP16)
+    ids = [bm.allocate_block() for _ in range(total_blocks)]
+    for b in r.permutation(ids):
+        bm.free_block(int(b))
+    seqs = []
+    for n in lens_after:
+        sq = bm.seq_create()
+        assert not isinstance(bm.seq_extend(sq, int(n)), int)
+        seqs.append(sq)
+    max_len = int(lens_after.max())
+    max_blocks = (max_len + bs - 1) // bs
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    stream = dev.Stream()
+    nbytes = kv.pool_bytes(bm.pool())
+    pool = dev.DeviceBuffer(nbytes)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, stream.handle))
+    bm.attach_pool(pool.ptr, None)
+    desc = bm.pool()
+    qkv = dev.DeviceBuffer(layers * B * QKV * 2)
+    atomflow_amd.check(lib.af_rt_fill_randn_f16(qkv.ptr, layers * B * QKV, 11, 1.0, stream.handle))
+    out = dev.DeviceBuffer(layers * B * Q_DIM * 2)
+    d_tables, d_lens = dev.DeviceBuffer.from_array(tables), dev.DeviceBuffer.from_array(lens)
+    ws = kv.AttentionWorkspace(B, NQ, NKV, HD, 0, stream)
+    stream.sync()
+    raw = ctypes.CDLL(atomflow_amd.LIB_PATH)
+    raw.af_dbg_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    table = np.zeros((STAMP_WGS, STAMP_SLOTS), np.uint64)
+
+    def attention():
+        for l in range(layers):
+            kv.launch_paged_attention(qkv.ptr + l * B * QKV * 2, QKV, desc, l, d_tables, max_blocks,
+                                      d_lens, B, max_len, out.ptr + l * B * Q_DIM * 2, Q_DIM, NQ,
+                                      ws, stream=stream)
+
+    graph = dev.Graph.capture(stream, attention)
+    for _ in range(args.warmup):
+        graph.launch(stream)
+    stream.sync()
+    per = []
+    for _ in range(args.steps):
+        graph.launch(stream)
+        stream.sync()
+        atomflow_amd.check(raw.af_dbg_phase_stamps(table.ctypes.data, table.nbytes))
+        st = table.astype(np.int64)
+        hwids = st[:, 9].copy()
+        # this launch's entries (within 1 ms of the latest), and slots after them
+        fresh = st[:, 8] > st[:, 8].max() - 100000
+        st[:, 9] = 0
+        valid = (st > st[:, 8:9]) | (np.arange(STAMP_SLOTS) == 8)
+        st = np.where(valid & fresh[:, None], st, 0)
+        real = (st[:, 0] > 0) & (st[:, 8] > 0)  # workgroups with a split (not past the batch)
+        t0 = st[st[:, 8] > 0, 8].min()
+        us = np.where(st > 0, (st - t0) * 0.01, np.nan)[real]
+        end = np.where(np.isnan(us[:, 10]), us[:, 6], us[:, 10])
+        row = {"workgroups": int(real.sum()), "launched": int(fresh.sum()),
+               "span_us": float(np.nanmax(end))}
+        for (pa, na), (pb, nb) in zip(GRID_PHASES[:-1], GRID_PHASES[1:]):
+            d = us[:, pb] - us[:, pa]
+            row[f"{na} -> {nb}"] = (float(np.nanmedian(d)), float(np.nanpercentile(d, 90)))
+        d = us[:, 10] - us[:, 6]
+        row["stores acknowledged -> combine done (last arrivals)"] = (
+            float(np.nanmedian(d)), float(np.nanpercentile(d, 90)), int(np.sum(~np.isnan(d))))
+        life = end - us[:, 8]
+        row["streaming share of a workgroup's life"] = float(np.nanmedian((us[:, 3] - us[:, 2]) / life))
+        # per CU: the share of the launch with no workgroup streaming rows
+        hw = hwids[real]
+        cu = (hw & 0xF) * 1024 + ((hw >> 32) >> 8 & 0xFF)  # XCC, then CU / SH / SE bits of HW_ID
+        span = row["span_us"]
+        grid_t = np.arange(0.0, span, 0.1)
+        idle = []
+        for c in np.unique(cu):
+            m = cu == c
+            on = np.zeros(len(grid_t), bool)
+            for a0, a1 in zip(us[m, 2], us[m, 3]):
+                on |= (grid_t >= a0) & (grid_t < a1)
+            idle.append(1.0 - on.mean())
+        row["CUs"] = int(len(idle))
+        row["CU share with no workgroup streaming"] = float(np.mean(idle))
+        states = []
+        for t in np.arange(0.0, span, 4.0):
+            pre = int(np.sum((us[:, 8] <= t) & (us[:, 2] > t)))
+            strm = int(np.sum((us[:, 2] <= t) & (us[:, 3] > t)))
+            epi = int(np.sum((us[:, 3] <= t) & (end > t)))
+            states.append((round(float(t)), pre, strm, epi))
+        row["states"] = states
+        per.append(row)
+    graph.destroy()
+    result = {"workload": f"configs[2] paged fp16, B={B}, 16-token blocks, {layers} layers rotated; "
+                          "attention only (af_paged_attention, compact grid)",
+              "replays": args.steps, "unit": "us from the launch's first workgroup entry"}
+    for k, v in per[0].items():
+        if k == "states":
+            continue
+        vals = [r[k] for r in per]
+        if isinstance(v, tuple):
+            result[k] = [round(float(np.median([x[i] for x in vals])), 3) for i in range(len(v))]
+        else:
+            result[k] = round(float(np.median(vals)), 4)
+    mid = sorted(per, key=lambda r: r["span_us"])[len(per) // 2]
+    result["states (t us: prologue / streaming / epilogue workgroups), median-span replay"] = \
+        mid["states"]
+    bm.close()
+    for b in (pool, qkv, out, d_tables, d_lens):
+        b.free()
+    stream.destroy()
+    return result
+
+
 def bench_stamps(args, dev, kv, lib):
     """Where one attention launch's time goes (configs[1], batch 1): the stamps
     build records s_memrealtime (10 ns ticks) per workgroup at each phase of the
@@ -1336,8 +1471,7 @@ def bench_stamps(args, dev, kv, lib):
     stream.sync()
     raw = ctypes.CDLL(atomflow_amd.LIB_PATH)
     raw.af_dbg_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
-    n_wg, n_ph = 2048, 8
-    table = np.zeros((n_wg, n_ph), np.uint64)
+    table = np.zeros((STAMP_WGS, STAMP_SLOTS), np.uint64)
 
     def ptrs(l):
         return (qkv.ptr + l * QKV * 2, pool.ptr + 2 * l * slab, pool.ptr + (2 * l + 1) * slab,
@@ -1428,7 +1562,8 @@ def main():
         print(json.dumps({"read_probe": bench_read_probe(args, dev)}), flush=True)
         return
     if args.stamps:
-        print(json.dumps({"stamps": bench_stamps(args, dev, kv, lib)}), flush=True)
+        fn = bench_stamps_paged if args.config == 3 else bench_stamps
+        print(json.dumps({"stamps": fn(args, dev, kv, lib)}), flush=True)
         return
     if args.config == 2:
         result = bench_contiguous(args, dev, kv, lib, info)
