@@ -485,7 +485,28 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     const bool owner = FUSED && split == n_active - 1;  // holds the new token (t = L - 1)
     AF_STAMP(0);
 
-    int tab_base = 0;  // the split's first block-table entry (paged), staged below
+    // ---- stage this split's block-table entries (paged) --------------------
+    int tab_base = 0;
+    if constexpr (PAGED) {
+        const int first = t_begin >> a.block_shift;
+        const int last = (t_end - 1) >> a.block_shift;
+        tab_base = first;
+        if (PERSIST && sg.staged) {
+            // the previous item loaded this window's entries (thread t holds
+            // entry t) while it merged
+            if (tid <= last - first) s_tab[tid] = min(max(nx_entry, 0), int(a.total_blocks - 1));
+        } else {
+            const int32_t* trow = a.tables + size_t(b) * a.max_blocks;
+            for (int e = tid; e <= last - first; e += kThreads) {
+                int blk = trow[first + e];
+                blk = min(max(blk, 0), int(a.total_blocks - 1));  // never address outside the pool
+                s_tab[e] = blk;
+            }
+        }
+        __syncthreads();
+        AF_STAMP(11);
+    }
+
     const uint8_t* kbase = a.k + size_t(h) * LY::kRowBytes + j * 16;
     const uint8_t* vbase = a.v + size_t(h) * LY::kRowBytes + j * 16;
     // Rows that may be read from memory: [t_begin, L) unfused; [t_begin, L-1)
@@ -565,28 +586,6 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
                 for (int w = 0; w < LY::kElemsPerLoad / 8; ++w)
                     qraw[gh][i * (LY::kElemsPerLoad / 8) + w] =
                         *reinterpret_cast<const uint4*>(qb + gh * HD + LY::dim(i, j, 0) + w * 8);
-    }
-
-    // ---- stage this split's block-table entries (paged) --------------------
-    // (after the query loads, so the table's round trip and theirs overlap)
-    if constexpr (PAGED) {
-        const int first = t_begin >> a.block_shift;
-        const int last = (t_end - 1) >> a.block_shift;
-        tab_base = first;
-        if (PERSIST && sg.staged) {
-            // the previous item loaded this window's entries (thread t holds
-            // entry t) while it merged
-            if (tid <= last - first) s_tab[tid] = min(max(nx_entry, 0), int(a.total_blocks - 1));
-        } else {
-            const int32_t* trow = a.tables + size_t(b) * a.max_blocks;
-            for (int e = tid; e <= last - first; e += kThreads) {
-                int blk = trow[first + e];
-                blk = min(max(blk, 0), int(a.total_blocks - 1));  // never address outside the pool
-                s_tab[e] = blk;
-            }
-        }
-        __syncthreads();
-        AF_STAMP(11);
     }
 
     // ---- ring prologue: the first NB row-steps go in flight ----------------
