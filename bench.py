@@ -75,6 +75,14 @@ def parse():
     ap.add_argument("--no-weights", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-matrix", action="store_true",
                     help="skip the per-config matrix (configs[1] ctx 1k/32k, configs[2..4])")
+    ap.add_argument("--compare-lib", default=None,
+                    help="in-process A/B: time the in-tree library (A) against this build (B) on the "
+                         "same buffers and workspaces, graphs replayed alternately; prints one line "
+                         "per workload and launch kind")
+    ap.add_argument("--compare-work", default="ctx8k,ctx32k,cfg3,cfg4,cfg5",
+                    help="workloads of --compare-lib: ctx8k, ctx32k (configs[1]), cfg3 (configs[2]), "
+                         "cfg4 (configs[3], plain and shared-prefix), cfg5 (configs[4])")
+    ap.add_argument("--compare-rounds", type=int, default=8)
     ap.add_argument("--fanout-only", action="store_true",
                     help="run only the fan-out decode measurement and print its JSON object")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -1538,6 +1546,190 @@ def bench_stamps(args, dev, kv, lib):
     return result
 
 
+def bench_compare(args):
+    """In-process A/B of two builds of the library. Both are loaded with RTLD_LOCAL (each
+    resolves its own symbols), the buffers are allocated once, and every workload's graph
+    is captured once per build on one shared workspace (the builds must share the workspace
+    layout); the graphs are then replayed alternately, `compare_rounds` rounds of `steps`
+    replays, and the median per-launch microseconds of each build are printed with B/A. The
+    spread between processes (a fresh pool lands on different memory) does not enter."""
+    import ctypes
+    import atomflow_amd
+    from atomflow_amd import AF_KV_FP16, AF_KV_FP8_E4M3, _abi
+
+    paths = [atomflow_amd.LIB_PATH, os.path.abspath(args.compare_lib)]
+    libs = [_abi.bind(ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)) for p in paths]
+    atomflow_amd._lib = libs[0]
+    from atomflow_amd import device as dev
+    from atomflow_amd import kv
+    dev.set_device(0)
+    stream = dev.Stream()
+    lib0 = libs[0]
+    print(f"A = {paths[0]}\nB = {paths[1]}", flush=True)
+
+    def timed(graph):
+        e0, e1 = dev.Event(), dev.Event()
+        ts = []
+        for _ in range(args.steps):
+            e0.record(stream)
+            graph.launch(stream)
+            e1.record(stream)
+            stream.sync()
+            ts.append(e0.elapsed_ms(e1) * 1e3 / LAYERS)
+        e0.destroy()
+        e1.destroy()
+        return float(np.median(ts))
+
+    def ab(name, mkws, kinds):
+        ws = mkws()
+        graphs = {}
+        for li, L in enumerate(libs):
+            atomflow_amd._lib = L
+            for kind, fn in kinds.items():
+                g = dev.Graph.capture(stream, lambda: fn(ws))
+                for _ in range(max(args.warmup, 1)):
+                    g.launch(stream)
+                stream.sync()
+                graphs[(li, kind)] = g
+        atomflow_amd._lib = libs[0]
+        res = {k: [] for k in graphs}
+        for r in range(args.compare_rounds):
+            order = list(graphs)
+            for k in (order if r % 2 == 0 else order[::-1]):
+                res[k].append(timed(graphs[k]))
+        for kind in kinds:
+            va, vb = np.array(res[(0, kind)]), np.array(res[(1, kind)])
+            print(f"{name:7s} {kind:10s} A {np.median(va):9.2f} us  B {np.median(vb):9.2f} us  "
+                  f"B/A {np.median(vb) / np.median(va):.4f}   (A {va.min():.2f}-{va.max():.2f}, "
+                  f"B {vb.min():.2f}-{vb.max():.2f})", flush=True)
+        for g in graphs.values():
+            g.destroy()
+        ws.buf.free()
+
+    def contiguous(ctx):
+        L = ctx + 1
+        max_seq = (L + 127) // 128 * 128
+        slab = max_seq * KV_DIM * 2
+        pool = dev.DeviceBuffer(LAYERS * 2 * slab)
+        qkv = dev.DeviceBuffer(LAYERS * QKV * 2)
+        out = dev.DeviceBuffer(LAYERS * Q_DIM * 2)
+        d_cos = dev.DeviceBuffer(max_seq * HD // 2 * 4)
+        d_sin = dev.DeviceBuffer(max_seq * HD // 2 * 4)
+        kv.build_rope_cache(d_cos, d_sin, max_seq, HD, THETA, stream)
+        atomflow_amd.check(lib0.af_rt_fill_randn_f16(pool.ptr, LAYERS * 2 * slab // 2, 7, 1.0,
+                                                     stream.handle))
+        atomflow_amd.check(lib0.af_rt_fill_randn_f16(qkv.ptr, LAYERS * QKV, 11, 1.0, stream.handle))
+        stream.sync()
+
+        def ptrs(l):
+            return (qkv.ptr + l * QKV * 2, pool.ptr + 2 * l * slab, pool.ptr + (2 * l + 1) * slab,
+                    out.ptr + l * Q_DIM * 2)
+
+        def fused(ws):
+            for l in range(LAYERS):
+                q, k, v, o = ptrs(l)
+                kv.launch_decode_attention_fused(q, k, v, d_cos, d_sin, ctx, max_seq, o, NQ, NKV, HD,
+                                                 ws, stream=stream)
+
+        def attention(ws):
+            for l in range(LAYERS):
+                q, k, v, o = ptrs(l)
+                kv.launch_cached_attention_ex(q, k, v, o, L, max_seq, HD, NQ, NKV, ws, stream=stream)
+        ab(f"ctx{ctx // 1024}k", lambda: kv.AttentionWorkspace(1, NQ, NKV, HD, 0, stream),
+           {"fused": fused, "attention": attention})
+        for b in (pool, qkv, out, d_cos, d_sin):
+            b.free()
+
+    def paged(cfg):
+        r = np.random.Generator(np.random.PCG64(0xA70F10 + cfg))  # bench_paged's draws
+        fp8 = cfg == 5
+        bs = 32 if fp8 else 16
+        if cfg == 3:
+            lens_new = r.integers(128, 8193, 32)
+        elif cfg == 5:
+            lens_new = r.integers(8192, 16385, 128)
+        else:
+            prefix, suffix = 2048, r.integers(1, 1025, 64)
+        B = 64 if cfg == 4 else len(lens_new)
+        if cfg == 4:
+            need = prefix // bs + sum((int(x) + 1 + bs - 1) // bs for x in suffix)
+        else:
+            need = sum((int(n) + 1 + bs - 1) // bs for n in lens_new)
+        total_blocks = int(need * 1.1) + 8
+        bm = kv.BlockManager(total_blocks, bs, LAYERS, NKV, HD, AF_KV_FP8_E4M3 if fp8 else AF_KV_FP16)
+        ids = [bm.allocate_block() for _ in range(total_blocks)]
+        for b in r.permutation(ids):
+            bm.free_block(int(b))
+        if cfg == 4:
+            root = bm.seq_create()
+            bm.seq_extend(root, prefix)
+            seqs = [root] + [bm.seq_fork(root) for _ in range(B - 1)]
+            for sq, n in zip(seqs, suffix):
+                assert not isinstance(bm.seq_extend(sq, int(n)), int)
+        else:
+            seqs = []
+            for n in lens_new:
+                sq = bm.seq_create()
+                assert not isinstance(bm.seq_extend(sq, int(n)), int)
+                seqs.append(sq)
+        plan = bm.plan_decode(seqs)
+        assert not isinstance(plan, int), plan
+        slots, positions, _ = plan
+        max_len = int(positions.max()) + 1
+        max_blocks = (max_len + bs - 1) // bs
+        tables, lens = bm.export_tables(seqs, max_blocks)
+        nbytes = kv.pool_bytes(bm.pool())
+        pool = dev.DeviceBuffer(nbytes)
+        scales = None
+        if fp8:
+            sc = 5.0 / 448.0
+            scales = dev.DeviceBuffer.from_array(np.full((LAYERS, 2, NKV), sc, np.float32))
+            atomflow_amd.check(lib0.af_rt_fill_randn_fp8(pool.ptr, nbytes, 7, 1.0 / sc, stream.handle))
+        else:
+            atomflow_amd.check(lib0.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, stream.handle))
+        bm.attach_pool(pool.ptr, scales.ptr if scales else None)
+        desc = bm.pool()
+        max_pos = max_len + 1
+        d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+        d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)
+        kv.build_rope_cache(d_cos, d_sin, max_pos, HD, THETA, stream)
+        qkv = dev.DeviceBuffer(LAYERS * B * QKV * 2)
+        atomflow_amd.check(lib0.af_rt_fill_randn_f16(qkv.ptr, LAYERS * B * QKV, 11, 1.0,
+                                                     stream.handle))
+        out = dev.DeviceBuffer(LAYERS * B * Q_DIM * 2)
+        d_t, d_l = dev.DeviceBuffer.from_array(tables), dev.DeviceBuffer.from_array(lens)
+        d_sl, d_p = dev.DeviceBuffer.from_array(slots), dev.DeviceBuffer.from_array(positions)
+        bufs = [pool, d_cos, d_sin, qkv, out, d_t, d_l, d_sl, d_p] + ([scales] if scales else [])
+        stream.sync()
+        qp = lambda l: qkv.ptr + l * B * QKV * 2
+        op = lambda l: out.ptr + l * B * Q_DIM * 2
+        kinds = {}
+        if cfg == 4:
+            d_root = dev.DeviceBuffer.from_array(np.ascontiguousarray(tables[0]))
+            bufs.append(d_root)
+            kinds["shared"] = lambda ws: [kv.launch_paged_attention_shared_prefix(
+                qp(l), QKV, desc, l, d_root, prefix, d_t, max_blocks, d_l, B, max_len, op(l), Q_DIM,
+                NQ, ws, stream=stream) for l in range(LAYERS)]
+        else:
+            kinds["fused"] = lambda ws: [kv.launch_paged_decode_fused(
+                qp(l), B, desc, l, d_sl, d_p, d_cos, d_sin, max_pos, d_t, max_blocks, max_len, op(l),
+                Q_DIM, NQ, ws, stream=stream) for l in range(LAYERS)]
+        kinds["attention" if cfg != 4 else "plain"] = lambda ws: [kv.launch_paged_attention(
+            qp(l), QKV, desc, l, d_t, max_blocks, d_l, B, max_len, op(l), Q_DIM, NQ, ws,
+            stream=stream) for l in range(LAYERS)]
+        ab(f"cfg{cfg}", lambda: kv.AttentionWorkspace(B, NQ, NKV, HD, 0, stream), kinds)
+        bm.close()
+        for b in bufs:
+            b.free()
+
+    for w in args.compare_work.split(","):
+        if w.startswith("ctx"):
+            contiguous(int(w[3:-1]) * 1024)
+        else:
+            paged(int(w[3:]))
+    stream.destroy()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1551,6 +1743,9 @@ def main():
     if args.stamps:  # the measurement build of the same library
         atomflow_amd.LIB_PATH = os.environ.get(
             "AF_STAMPS_LIB", os.path.join(ROOT, "atomflow_amd", "libatomflow_kv_stamps.so"))
+    if args.compare_lib:
+        bench_compare(args)
+        return
     lib = atomflow_amd.lib()
     dev.set_device(0)
     info = dev.device_info()
