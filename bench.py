@@ -1549,8 +1549,9 @@ def bench_stamps(args, dev, kv, lib):
 def bench_compare(args):
     """In-process A/B of two builds of the library. Both are loaded with RTLD_LOCAL (each
     resolves its own symbols), the buffers are allocated once, and every workload's graph
-    is captured once per build on one shared workspace (the builds must share the workspace
-    layout); the graphs are then replayed alternately, `compare_rounds` rounds of `steps`
+    is captured once per build, on a workspace of that build's own (sized and initialised by
+    it, so the builds may lay their workspaces out differently); the graphs are then replayed
+    alternately, `compare_rounds` rounds of `steps`
     replays, and the median per-launch microseconds of each build are printed with B/A. The
     spread between processes (a fresh pool lands on different memory) does not enter."""
     import ctypes
@@ -1581,10 +1582,11 @@ def bench_compare(args):
         return float(np.median(ts))
 
     def ab(name, mkws, kinds):
-        ws = mkws()
-        graphs = {}
+        graphs, wss = {}, []
         for li, L in enumerate(libs):
             atomflow_amd._lib = L
+            ws = mkws()
+            wss.append(ws)
             for kind, fn in kinds.items():
                 g = dev.Graph.capture(stream, lambda: fn(ws))
                 for _ in range(max(args.warmup, 1)):
@@ -1604,7 +1606,8 @@ def bench_compare(args):
                   f"B {vb.min():.2f}-{vb.max():.2f})", flush=True)
         for g in graphs.values():
             g.destroy()
-        ws.buf.free()
+        for ws in wss:
+            ws.buf.free()
 
     def contiguous(ctx):
         L = ctx + 1
