@@ -31,6 +31,7 @@ AF_ERR_BAD_FILE = -9
 AF_ERR_TIMEOUT = -10
 AF_KV_FP16 = 1
 AF_KV_FP8_E4M3 = 3
+AF_KV_POOL_SHARED_BLOCKS = 1
 
 
 class AfError(RuntimeError):

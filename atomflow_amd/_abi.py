@@ -24,7 +24,7 @@ class KvPool(ctypes.Structure):
         ("n_layers", I32),
         ("n_kv_heads", I32),
         ("head_dim", I32),
-        ("reserved", I32),
+        ("flags", I32),
         ("total_blocks", I64),
     ]
 

@@ -389,6 +389,7 @@ extern "C" int af_paged_qkv_rope_append(const void* x, int64_t x_stride, int m,
         !sin_table || max_pos <= 0 || n_q_heads <= 0)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers) return AF_ERR_INVALID_ARG;
+    if (pool->flags & ~AF_KV_POOL_SHARED_BLOCKS) return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if (!fp8 && pool->dtype != AF_KV_FP16) return AF_ERR_UNSUPPORTED;
     if (fp8 && !pool->scales) return AF_ERR_INVALID_ARG;

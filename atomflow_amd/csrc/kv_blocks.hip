@@ -127,6 +127,7 @@ static int pool_check(const af_kv_pool* p) {
         return AF_ERR_INVALID_ARG;
     if (p->block_size & (p->block_size - 1)) return AF_ERR_UNSUPPORTED;
     if (p->dtype != AF_KV_FP16 && p->dtype != AF_KV_FP8_E4M3) return AF_ERR_UNSUPPORTED;
+    if (p->flags & ~AF_KV_POOL_SHARED_BLOCKS) return AF_ERR_INVALID_ARG;
     const size_t esz = p->dtype == AF_KV_FP8_E4M3 ? 1 : 2;
     if ((size_t(p->n_kv_heads) * p->head_dim * esz) % 16) return AF_ERR_UNSUPPORTED;
     if (!aligned16(p->base)) return AF_ERR_INVALID_ARG;

@@ -1005,7 +1005,8 @@ static int prefill_paged(const void* q, int q_stride, const af_kv_pool* pool, in
         n_q_heads <= 0 || max_blocks <= 0)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
-        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0)
+        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0 ||
+        (pool->flags & ~AF_KV_POOL_SHARED_BLOCKS))
         return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;
@@ -1156,7 +1157,8 @@ static int prefill_batched(const void* q, int q_stride, const af_kv_pool* pool, 
                    int64_t(n_groups) * n_q_heads > kMaxCounters))
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers || pool->n_kv_heads <= 0 ||
-        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0)
+        n_q_heads % pool->n_kv_heads || pool->total_blocks <= 0 ||
+        (pool->flags & ~AF_KV_POOL_SHARED_BLOCKS))
         return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if ((!fp8 && pool->dtype != AF_KV_FP16) || pool->head_dim != kPfHd) return AF_ERR_UNSUPPORTED;

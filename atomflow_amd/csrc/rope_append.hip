@@ -352,6 +352,7 @@ extern "C" int af_paged_rope_append(void* qkv_out, int batch, const af_kv_pool* 
         !sin_table || batch < 0 || max_pos <= 0 || n_q_heads <= 0)
         return AF_ERR_INVALID_ARG;
     if (layer < 0 || layer >= pool->n_layers) return AF_ERR_INVALID_ARG;
+    if (pool->flags & ~AF_KV_POOL_SHARED_BLOCKS) return AF_ERR_INVALID_ARG;
     const bool fp8 = pool->dtype == AF_KV_FP8_E4M3;
     if (!fp8 && pool->dtype != AF_KV_FP16) return AF_ERR_UNSUPPORTED;
     if (fp8 && !pool->scales) return AF_ERR_INVALID_ARG;

@@ -287,7 +287,10 @@ def launch_decode_attention_fused(qkv_out, k_cache, v_cache, cos_table, sin_tabl
 
 
 # ---- a6-a8: paged pool -----------------------------------------------------
-def make_pool(base, dtype, block_size, n_layers, n_kv_heads, head_dim, total_blocks, scales=None):
+def make_pool(base, dtype, block_size, n_layers, n_kv_heads, head_dim, total_blocks, scales=None,
+              flags=0):
+    """af_kv_pool over `base`. flags: AF_KV_POOL_SHARED_BLOCKS when the block tables of one
+    launch may map a block for several sequences (forks, prefix caching)."""
     p = _abi.KvPool()
     p.base = _p(base)
     p.scales = _p(scales)
@@ -296,7 +299,7 @@ def make_pool(base, dtype, block_size, n_layers, n_kv_heads, head_dim, total_blo
     p.n_layers = n_layers
     p.n_kv_heads = n_kv_heads
     p.head_dim = head_dim
-    p.reserved = 0
+    p.flags = flags
     p.total_blocks = total_blocks
     return p
 

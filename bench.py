@@ -577,6 +577,8 @@ def bench_serving(dev, kv, lib, steps=12, warmup=3, shared_prefix=0, group_decod
     atomflow_amd.check(lib.af_rt_fill_randn_f16(pool_buf.ptr, nbytes // 2, 7, 1.0, stream.handle))
     bm.attach_pool(pool_buf.ptr)
     pool = bm.pool()
+    if shared_prefix:  # requests fork cached prompt prefixes: keep KV rows cached
+        pool.flags = atomflow_amd.AF_KV_POOL_SHARED_BLOCKS
     sched = kv.Scheduler(bm, max_running, budget, chunk, 16, 4 if shared_prefix else 0)
     for i, c in enumerate(ctx):
         assert sched.add_request(i, int(c), old_gen)
@@ -728,6 +730,7 @@ def bench_fanout(dev, kv, lib, steps=8, n_req=64, prefix=4096, suffix=16, prefix
     atomflow_amd.check(lib.af_rt_fill_randn_f16(pool_buf.ptr, nbytes // 2, 9, 1.0, stream.handle))
     bm.attach_pool(pool_buf.ptr)
     pool = bm.pool()
+    pool.flags = atomflow_amd.AF_KV_POOL_SHARED_BLOCKS  # every request forks the cached prefix
     sched = kv.Scheduler(bm, n_req, 8192, 4096, 0, 1)
     assert sched.add_request(0, prompt, 64, 3, prefix)
     while sched.step()["cache_entries"] == 0:
@@ -1037,6 +1040,8 @@ def bench_paged(args, dev, kv, lib, info, cfg=None, cpu=False):
         atomflow_amd.check(lib.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, stream.handle))
     bm.attach_pool(pool.ptr, scales.ptr if scales else None)
     desc = bm.pool()
+    if cfg == 4:  # the forks map the prefix blocks: keep KV rows cached
+        desc.flags = atomflow_amd.AF_KV_POOL_SHARED_BLOCKS
     max_pos = max_len + 1
     d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
     d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)
@@ -1692,6 +1697,8 @@ def bench_compare(args):
             atomflow_amd.check(lib0.af_rt_fill_randn_f16(pool.ptr, nbytes // 2, 7, 1.0, stream.handle))
         bm.attach_pool(pool.ptr, scales.ptr if scales else None)
         desc = bm.pool()
+        if cfg == 4:  # the forks map the prefix blocks: keep KV rows cached
+            desc.flags = atomflow_amd.AF_KV_POOL_SHARED_BLOCKS
         max_pos = max_len + 1
         d_cos = dev.DeviceBuffer(max_pos * HD // 2 * 4)
         d_sin = dev.DeviceBuffer(max_pos * HD // 2 * 4)

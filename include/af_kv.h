@@ -201,9 +201,17 @@ typedef struct af_kv_pool {
     int32_t n_layers;
     int32_t n_kv_heads;
     int32_t head_dim;
-    int32_t reserved;
+    int32_t flags;       /* AF_KV_POOL_* bits; 0 for none */
     int64_t total_blocks;
 } af_kv_pool;
+
+/* af_kv_pool.flags: the block tables of one launch may map the same block for
+ * several sequences (forked sequences, prefix caching). Decode attention then
+ * reads KV rows with the ordinary cache policy, so the sequences after the first
+ * find shared rows in L2; without it, rows are read with non-temporal loads
+ * (each row once per launch), which streams faster. Either way the results are
+ * the same bits. Other bits are rejected (AF_ERR_INVALID_ARG). */
+#define AF_KV_POOL_SHARED_BLOCKS 1
 
 size_t af_kv_pool_bytes(const af_kv_pool* pool);
 

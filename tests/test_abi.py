@@ -113,6 +113,12 @@ def test_shared_prefix_argument_checks_without_gpu():
     assert call(p64, fake, 200, 0) == atomflow_amd.AF_ERR_UNSUPPORTED
     empty = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 128, 0)
     assert call(empty, fake, 200, 0) == atomflow_amd.AF_ERR_INVALID_ARG
+    # pool flags: AF_KV_POOL_SHARED_BLOCKS is the only defined bit
+    odd = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 128, 1000, flags=2)
+    assert call(odd, fake, 200, 0) == atomflow_amd.AF_ERR_INVALID_ARG
+    shared = kv.make_pool(fake, atomflow_amd.AF_KV_FP16, 16, 2, 8, 128, 1000,
+                          flags=atomflow_amd.AF_KV_POOL_SHARED_BLOCKS)
+    assert lib.af_kv_pool_bytes(ctypes.byref(shared)) == lib.af_kv_pool_bytes(ctypes.byref(pool))
 
 
 def test_missing_library_fails_loudly(monkeypatch):

@@ -32,6 +32,16 @@ def _compile(tmp_path, arch="gfx950", src="decode_attention"):
     return r, out
 
 
+@pytest.fixture(scope="module")
+def decode_asm(tmp_path_factory):
+    """decode_attention.hip's gfx950 assembly, compiled once for the tests below."""
+    if not os.path.exists(HIPCC) and shutil.which("hipcc") is None:
+        pytest.skip("hipcc not available")
+    r, out = _compile(tmp_path_factory.mktemp("decode_asm"))
+    assert r.returncode == 0, r.stderr[-2000:]
+    return open(out).read()
+
+
 def _functions(asm, kernel="decode_attn_kernel", end=r"\.Lfunc_end"):
     """(name, instructions) of every function whose name contains `kernel`, read
     to its end (early exits end in s_endpgm blocks of their own)."""
@@ -74,14 +84,14 @@ def _arrival_atomics(ins):
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None,
                     reason="hipcc not available")
-def test_combine_publication_order(tmp_path):
-    r, out = _compile(tmp_path)
-    assert r.returncode == 0, r.stderr[-2000:]
-    asm = open(out).read()
+def test_combine_publication_order(decode_asm):
+    asm = decode_asm
     grid = comb = persistent = 0
     for name, ins in _functions(asm, "decode_attn_kernel"):
         atomics = _arrival_atomics(ins)
-        if name.endswith("Lb1EEEvNS0_8AttnArgsE") and "decode_attn_kernelI" in name:
+        m = re.search(r"decode_attn_kernelILi\d+ELi\d+E((?:Lb[01]E)+)E", name)
+        # bool arguments: FP8, PAGED, FUSED, PAIR, COMB, CACHED
+        if m and re.findall(r"Lb([01])E", m.group(1))[4] == "1":
             # dedicated-combiner form: no arrival counter; each split publishes
             # with its ready flag, an agent-scope store behind the same wait and
             # barrier, and the combiner polls the flags and loads the records
@@ -131,9 +141,10 @@ def test_combine_publication_order(tmp_path):
         loads = [i for i, l in enumerate(ins) if l.startswith("global_load") and " sc1" in l and i > a]
         assert len(loads) >= 3, (name, len(loads))  # (m, l) and the first batch of records
         persistent += 1
-    # 62 grid-form kernels (contiguous / paged, fp16 / FP8, fused, pairs, 3wg),
-    # 8 dedicated-combiner kernels, 30 persistent kernels
-    assert grid >= 60 and comb == 8 and persistent == 30, (grid, comb, persistent)
+    # 100 grid-form kernels (contiguous / paged, fp16 / FP8, fused, pairs, 3wg;
+    # paged ones with both KV load policies), 8 dedicated-combiner kernels, 60
+    # persistent kernels (both policies)
+    assert grid >= 100 and comb == 8 and persistent == 60, (grid, comb, persistent)
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None,
@@ -173,3 +184,22 @@ def test_prefill_key_piece_publication_order(tmp_path):
         assert loads and min(loads) > a, (name, min(loads) if loads else None, a)
         checked += 1
     assert checked == 3, checked  # contiguous, paged fp16, paged FP8
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None,
+                    reason="hipcc not available")
+def test_kv_rows_load_policy(decode_asm):
+    """Decode kernels read KV rows with non-temporal 16-byte loads (`global_load_dwordx4 ...
+    nt`), except the CACHED instantiations (pools with AF_KV_POOL_SHARED_BLOCKS), which use no
+    non-temporal load at all."""
+    asm = decode_asm
+    seen = {False: 0, True: 0}
+    for kernel in ("decode_attn_kernel", "decode_attn_persistent"):
+        for name, ins in _functions(asm, kernel):
+            m = re.search(kernel + r"(?:_3wg)?ILi\d+ELi\d+E((?:Lb[01]E)+)E", name)
+            assert m, name
+            cached = re.findall(r"Lb([01])E", m.group(1))[-1] == "1"  # the last: CACHED
+            nt = [l for l in ins if l.startswith("global_load_dwordx4") and l.endswith(" nt")]
+            assert (not nt) if cached else len(nt) >= 4, (name, len(nt))
+            seen[cached] += 1
+    assert seen[False] >= 98 and seen[True] >= 70, seen

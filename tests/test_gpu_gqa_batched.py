@@ -181,3 +181,58 @@ def test_batched_gqa_fused_equals_unfused(gpu, nq, nkv, fp8):
     atol, rtol = (ATOL_FP8, RTOL_FP8) if fp8 else (2e-3, 1e-2)
     assert_attn_close(fused_o[b].view(np.float16), ref, atol, rtol, what=f"fused seq {b}")
     bm.close()
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_shared_blocks_policy_gives_the_same_bits(gpu, fp8):
+    """AF_KV_POOL_SHARED_BLOCKS selects the kernels that read KV rows with the ordinary cache
+    policy instead of non-temporal loads; only the load policy differs, so a batch whose odd
+    sequences map the same blocks as their even neighbours (forks) gets the same bits either
+    way, unfused and fused, and matches the oracle."""
+    from atomflow_amd import AF_KV_POOL_SHARED_BLOCKS
+    nq, nkv = 24, 8
+    B, lengths, bm, seqs, bs, host, scales, buf, desc, d_sc = _setup(nq, nkv, fp8, 1300 + 7 * fp8)
+    shared = kv.make_pool(buf, AF_KV_FP8_E4M3 if fp8 else AF_KV_FP16, bs, 2, nkv, HD,
+                          desc.total_blocks, d_sc, flags=AF_KV_POOL_SHARED_BLOCKS)
+    say(f"shared-blocks policy fp8={fp8} B={B}")
+    q_dim = nq * HD
+    max_len = max(lengths)
+    max_blocks = (max_len + bs - 1) // bs
+    tables, lens = bm.export_tables(seqs, max_blocks)
+    tables[1::2], lens[1::2] = tables[0::2][: B // 2], lens[0::2][: B // 2]  # forks
+    lengths = [int(n) for n in lens]
+    q = randn_f16((B, q_dim), 1310)
+    d_q, d_t, d_l = up(q), up(tables), up(lens)
+    ws = kv.AttentionWorkspace(B, nq, nkv, HD, 0)
+    outs = []
+    for pool in (desc, shared):
+        d_o = dev.DeviceBuffer(B * q_dim * 2)
+        kv.launch_paged_attention(d_q, q_dim, pool, 1, d_t, max_blocks, d_l, B, max_len, d_o,
+                                  q_dim, nq, ws)
+        outs.append(d_o.download(np.float16, (B, q_dim)))
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    atol, rtol = (ATOL_FP8, RTOL_FP8) if fp8 else (2e-3, 1e-2)
+    for b in (1, 9, 10, B - 1):
+        if lengths[b]:
+            ref = _ref(q[b], host, scales, 1, tables[b], lengths[b], bs, nq, nkv)
+            assert_attn_close(outs[1][b], ref, atol, rtol, what=f"seq {b} L={lengths[b]}")
+    # fused step (RoPE + append + attention) on the unshared sequences, both policies
+    plan = bm.plan_decode(seqs)
+    assert not isinstance(plan, int), plan
+    slots, positions, _ = plan
+    max_pos = int(positions.max()) + 2
+    c, s = oracle.rope_table(max_pos, HD, THETA)
+    d_c, d_s = up(c), up(s)
+    ftables, flens = bm.export_tables(seqs, (int(positions.max()) + 1 + bs - 1) // bs)
+    qkv = randn_f16((B, q_dim + 2 * nkv * HD), 1320)
+    res = []
+    for pool in (desc, shared):
+        buf.upload(host)
+        d_qkv, d_o = up(qkv), dev.DeviceBuffer(B * q_dim * 2)
+        kv.launch_paged_decode_fused(d_qkv, B, pool, 0, up(slots), up(positions), d_c, d_s,
+                                     max_pos, up(ftables), ftables.shape[1],
+                                     int(positions.max()) + 1, d_o, q_dim, nq, ws)
+        res.append((d_o.download(np.uint16), buf.download(np.uint8)))
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1], res[1][1])
+    bm.close()
