@@ -132,7 +132,7 @@ PROTOTYPES = {
     "af_rt_memcpy_d2d": (I, [P, P, SZ, P]),
     "af_rt_fill_u32": (I, [P, U32, SZ, P]),
     "af_rt_add_i32": (I, [P, I, I32, P]),
-    "af_rt_read_probe": (I, [P, SZ, I, I, I, P, P]),
+    "af_rt_read_probe": (I, [P, SZ, I, I, I, I, P, P]),
     "af_rt_fill_randn_f16": (I, [P, SZ, U64, F, P]),
     "af_rt_fill_randn_fp8": (I, [P, SZ, U64, F, P]),
     "af_rt_stream_create": (I, [ctypes.POINTER(P)]),

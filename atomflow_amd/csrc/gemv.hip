@@ -61,6 +61,15 @@ __device__ __forceinline__ float dot16(const uint4 w, const uint4 xa, const uint
 // `hook` runs once, right after the first pass's loads are issued: loads the
 // caller needs only after the sums (the fused kernel's position and cos / sin)
 // then travel with the weight loads instead of after them.
+// Weight bytes are read once per launch: non-temporal 16-B loads (the
+// streaming cache policy; the activation, read by every workgroup, keeps the
+// default one).
+__device__ __forceinline__ uint4 load_nt16(const uint8_t* p) {
+    typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 struct NoHook {
     __device__ void operator()() const {}
 };
@@ -87,7 +96,7 @@ __device__ __forceinline__ void row_partials(const uint8_t* __restrict__ w,
             xb[c] = *reinterpret_cast<const uint4*>(x + kk + 8);
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
-                wv[c][r] = *reinterpret_cast<const uint4*>(w + size_t(rows[r]) * k + kk);
+                wv[c][r] = load_nt16(w + size_t(rows[r]) * k + kk);
                 sc[c][r] = scales[size_t(rows[r]) * groups + kk / group_size];
             }
         }

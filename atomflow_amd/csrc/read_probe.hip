@@ -23,6 +23,19 @@ constexpr uint32_t kNever = 0x9E3779B9u;
 
 __device__ __forceinline__ uint32_t fold(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
 
+// One 16-B load, non-temporal (`global_load_dwordx4 ... nt`) when NT.
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const void* p) {
+    if constexpr (NT) {
+        typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+        const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *static_cast<const uint4*>(p);
+    }
+}
+
+template <bool NT>
 __global__ __launch_bounds__(kProbeThreads) void read_contiguous(const uint4* __restrict__ p,
                                                                  size_t n16, size_t chunk,
                                                                  uint32_t* sink) {
@@ -32,14 +45,14 @@ __global__ __launch_bounds__(kProbeThreads) void read_contiguous(const uint4* __
     for (size_t i = b + threadIdx.x; i < e; i += size_t(kProbeThreads) * kProbeDepth) {
         uint4 a[kProbeDepth];
 #pragma unroll
-        for (int k = 0; k < kProbeDepth; ++k) a[k] = p[min(i + size_t(k) * kProbeThreads, e - 1)];
+        for (int k = 0; k < kProbeDepth; ++k) a[k] = load16<NT>(p + min(i + size_t(k) * kProbeThreads, e - 1));
 #pragma unroll
         for (int k = 0; k < kProbeDepth; ++k) x ^= fold(a[k]);
     }
     if (x == kNever) sink[0] = x;
 }
 
-template <int SEG>
+template <int SEG, bool NT>
 __global__ __launch_bounds__(kProbeThreads) void read_head_rows(const uint8_t* __restrict__ k_slab,
                                                                 const uint8_t* __restrict__ v_slab,
                                                                 int rows, int row_bytes,
@@ -64,8 +77,8 @@ __global__ __launch_bounds__(kProbeThreads) void read_head_rows(const uint8_t* _
             const uint8_t* vr = v_slab + size_t(t) * row_bytes + off;
 #pragma unroll
             for (int p = 0; p < kPieces; ++p) {
-                a[k][p] = *reinterpret_cast<const uint4*>(kr + 128 * p);
-                a[k][kPieces + p] = *reinterpret_cast<const uint4*>(vr + 128 * p);
+                a[k][p] = load16<NT>(kr + 128 * p);
+                a[k][kPieces + p] = load16<NT>(vr + 128 * p);
             }
         }
 #pragma unroll
@@ -81,8 +94,9 @@ __global__ __launch_bounds__(kProbeThreads) void read_head_rows(const uint8_t* _
 
 using namespace af;
 
-extern "C" int af_rt_read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
-                                int row_bytes, uint32_t* d_sink, af_stream_t stream) {
+template <bool NT>
+static int read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
+                      int row_bytes, uint32_t* d_sink, af_stream_t stream) {
     if (!src || !d_sink || workgroups <= 0 || bytes == 0) return AF_ERR_INVALID_ARG;
     if (reinterpret_cast<uintptr_t>(src) & 15u) return AF_ERR_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -90,7 +104,7 @@ extern "C" int af_rt_read_probe(const void* src, size_t bytes, int workgroups, i
         if (bytes % 16) return AF_ERR_INVALID_ARG;
         const size_t n16 = bytes / 16;
         const size_t chunk = (n16 + workgroups - 1) / size_t(workgroups);
-        hipLaunchKernelGGL(read_contiguous, dim3(workgroups), dim3(kProbeThreads), 0, s,
+        hipLaunchKernelGGL(read_contiguous<NT>, dim3(workgroups), dim3(kProbeThreads), 0, s,
                            static_cast<const uint4*>(src), n16, chunk, d_sink);
         AF_TRY_LAUNCH();
         return AF_OK;
@@ -107,11 +121,19 @@ extern "C" int af_rt_read_probe(const void* src, size_t bytes, int workgroups, i
     const uint8_t* k = static_cast<const uint8_t*>(src);
     const uint8_t* v = k + slab;
     if (segment_bytes == 256)
-        hipLaunchKernelGGL(read_head_rows<256>, dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
+        hipLaunchKernelGGL((read_head_rows<256, NT>), dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
                            rows, row_bytes, n_seg, splits, d_sink);
     else
-        hipLaunchKernelGGL(read_head_rows<128>, dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
+        hipLaunchKernelGGL((read_head_rows<128, NT>), dim3(workgroups), dim3(kProbeThreads), 0, s, k, v,
                            rows, row_bytes, n_seg, splits, d_sink);
     AF_TRY_LAUNCH();
     return AF_OK;
+}
+
+extern "C" int af_rt_read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
+                                int row_bytes, int nontemporal, uint32_t* d_sink,
+                                af_stream_t stream) {
+    return nontemporal
+               ? read_probe<true>(src, bytes, workgroups, segment_bytes, row_bytes, d_sink, stream)
+               : read_probe<false>(src, bytes, workgroups, segment_bytes, row_bytes, d_sink, stream);
 }

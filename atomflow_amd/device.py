@@ -24,10 +24,11 @@ def add_i32(ptr, n, delta, stream=None):
     check(lib().af_rt_add_i32(ptr, n, delta, _s(stream)), "af_rt_add_i32")
 
 
-def read_probe(ptr, nbytes, workgroups, sink_ptr, segment_bytes=0, row_bytes=0, stream=None):
+def read_probe(ptr, nbytes, workgroups, sink_ptr, segment_bytes=0, row_bytes=0, stream=None,
+               nontemporal=False):
     """One streaming-read launch over nbytes at ptr (af_rt_read_probe)."""
-    check(lib().af_rt_read_probe(ptr, nbytes, workgroups, segment_bytes, row_bytes, sink_ptr,
-                                 _s(stream)), "af_rt_read_probe")
+    check(lib().af_rt_read_probe(ptr, nbytes, workgroups, segment_bytes, row_bytes,
+                                 int(nontemporal), sink_ptr, _s(stream)), "af_rt_read_probe")
 
 
 def device_info():

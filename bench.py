@@ -1274,8 +1274,9 @@ def bench_read_probe(args, dev):
     """Streaming-read ceilings (af_rt_read_probe): for each workload's bytes per
     launch, the median time of a launch that only reads them, over a sweep of
     workgroup counts, for contiguous chunks and for the decode kernel's head-row
-    access pattern. Times are per launch from graphs of `layers` launches, each
-    on its own region."""
+    access pattern, each with the default and the non-temporal load policy (`_nt`
+    keys; the decode kernels' KV rows use the latter). Times are per launch from
+    graphs of `layers` launches, each on its own region."""
     stream = dev.Stream()
     sink = dev.DeviceBuffer(256)
     t = Timer(dev, stream, args.warmup)
@@ -1285,26 +1286,30 @@ def bench_read_probe(args, dev):
         buf = dev.DeviceBuffer(nbytes * layers)
         buf.fill_u32(0x3C003C00, stream)
         n_seg = row_bytes // seg if seg else 0
-        entry = {"bytes_per_launch": nbytes, "regions": layers, "contiguous_us": {},
-                 "head_rows_us": {}, "head_row_bytes": row_bytes, "segment_bytes": seg}
-        kinds = [("contiguous_us", (256, 512, 1024, 2048, 4096, 8192))]
+        entry = {"bytes_per_launch": nbytes, "regions": layers, "head_row_bytes": row_bytes,
+                 "segment_bytes": seg}
+        kinds = [("contiguous", (256, 512, 1024, 2048, 4096, 8192))]
         if n_seg:
-            kinds.append(("head_rows_us", tuple(n_seg * sp for sp in (24, 32, 64, 128, 256, 512))))
-        for kind, grid in kinds:
+            kinds.append(("head_rows", tuple(n_seg * sp for sp in (24, 32, 64, 128, 256, 512))))
+        kinds = [(k + ("_nt_us" if nt else "_us"), grid, nt) for k, grid in kinds for nt in (0, 1)]
+        for kind, _, _ in kinds:
+            entry[kind] = {}
+        for kind, grid, nt in kinds:
             for g in grid:
-                def launches(g=g, kind=kind):
+                def launches(g=g, kind=kind, nt=nt):
                     for l in range(layers):
-                        if kind == "contiguous_us":
-                            dev.read_probe(buf.ptr + l * nbytes, nbytes, g, sink.ptr, stream=stream)
+                        if kind.startswith("contiguous"):
+                            dev.read_probe(buf.ptr + l * nbytes, nbytes, g, sink.ptr, stream=stream,
+                                           nontemporal=nt)
                         else:
                             dev.read_probe(buf.ptr + l * nbytes, nbytes, g, sink.ptr, seg,
-                                           row_bytes, stream=stream)
+                                           row_bytes, stream=stream, nontemporal=nt)
                 graph = dev.Graph.capture(stream, launches)
                 us = t.graph_ms(graph, args.steps) * 1e3 / layers
                 graph.destroy()
                 entry[kind][str(g)] = round(us, 3)
-        for kind in ("contiguous_us", "head_rows_us"):
-            if not entry[kind]:
+        for kind in ("contiguous_us", "contiguous_nt_us", "head_rows_us", "head_rows_nt_us"):
+            if not entry.get(kind):
                 continue
             g, us = min(entry[kind].items(), key=lambda kv_: kv_[1])
             gbs = nbytes / (us * 1e-6) / 1e9

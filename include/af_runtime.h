@@ -54,9 +54,11 @@ int af_rt_fill_randn_fp8(uint8_t* dst, size_t n, uint64_t seed, float inv_scale,
  * segment_bytes 256 (fp16) or 128 (FP8): the decode-attention kernel's access
  * pattern for head_dim 128 without its arithmetic. src holds two equal slabs
  * (K then V) of rows of row_bytes; workgroups = splits x (row_bytes /
- * segment_bytes), each reading one head segment of one split's rows. */
+ * segment_bytes), each reading one head segment of one split's rows.
+ * nontemporal != 0: the loads use the non-temporal (streaming) cache policy, as
+ * the decode kernels' KV row loads do. */
 int af_rt_read_probe(const void* src, size_t bytes, int workgroups, int segment_bytes,
-                     int row_bytes, uint32_t* d_sink, af_stream_t stream);
+                     int row_bytes, int nontemporal, uint32_t* d_sink, af_stream_t stream);
 
 int af_rt_stream_create(af_stream_t* stream);
 int af_rt_stream_destroy(af_stream_t stream);
