@@ -595,22 +595,22 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
         const float* crow = a.cos_t + size_t(pos) * half;
         const float* srow = a.sin_t + size_t(pos) * half;
         const int nq = nkv * GROUP;
+        // Every thread loads, items past the end and other splits' K items at a
+        // clamped, in-bounds index (the rotation below skips them): a load
+        // under a branch would need its value moved at the join, and the
+        // compiler then waits for it before the ring prologue is issued.
 #pragma unroll
         for (int r = 0; r < RIT; ++r) {
-            const int it = tid + r * kThreads;
+            const int it = min(tid + r * kThreads, kRopeItems - 1);
             const int hh = hw * KVH + it / kHeadItems;  // the item's KV head
             const int gh = (it % kHeadItems) / half, d = it % half;
-            rx[r] = ry[r] = 0;
-            rc[r] = rs[r] = 0.f;
-            if (it < kRopeItems && (gh < GROUP || owner)) {
-                const uint16_t* src = qkv + size_t(gh < GROUP ? hh * GROUP + gh : nq + hh) * HD;
-                rx[r] = src[d];
-                ry[r] = src[d + half];
-                rc[r] = crow[d];
-                rs[r] = srow[d];
-            }
+            const uint16_t* src = qkv + size_t(gh < GROUP ? hh * GROUP + gh : nq + hh) * HD;
+            rx[r] = src[d];
+            ry[r] = src[d + half];
+            rc[r] = crow[d];
+            rs[r] = srow[d];
         }
-        if (owner && tid < KVH * HD) vnew = qkv[size_t(nq + nkv + hw * KVH) * HD + tid];
+        vnew = qkv[size_t(nq + nkv + hw * KVH) * HD + tid % (KVH * HD)];  // used by the owner
     } else {
         const uint16_t* qb = a.q + size_t(b) * a.q_stride + size_t(h) * GROUP * HD;
 #pragma unroll
