@@ -558,8 +558,9 @@ __device__ __forceinline__ void decode_attn_seg(const AttnArgs& a, const Seg& sg
     // several sequences of a launch: forks, prefix caching) keep the default
     // policy, so that the sequences after the first find shared rows in L2
     // (64 forks of a 2048-row prefix: 68 us per launch, 85 us streaming).
-    // STREAM = false: the default policy whatever CACHED is (the last round's
-    // refills, whose re-reads of the split's last step then hit L2).
+    // `stream` is kStream or kDefault; kDefault takes the default policy in
+    // every kernel (the paged last round's refills, whose re-reads of the
+    // split's last step then hit L2).
     auto load_row = [&](Row& r, int step, auto stream) {
         const int64_t off = row_offset(lane_t0 + step * STEP);
         if constexpr (!CACHED && decltype(stream)::value) {
