@@ -15,7 +15,7 @@ import pytest
 
 import atomflow_amd
 import oracle
-from atomflow_amd import AF_KV_FP8_E4M3, AF_KV_FP16
+from atomflow_amd import AF_KV_FP8_E4M3, AF_KV_FP16, AF_KV_POOL_SHARED_BLOCKS
 from atomflow_amd import device as dev
 from atomflow_amd import kv
 from inputs import (ATOL_FP8, HD, KV_DIM, NKV, NQ, Q_DIM, QKV, RTOL_FP8, THETA,
@@ -249,6 +249,16 @@ def test_shared_prefix_configs3_shape(gpu):
     for i in range(0, B, 9):
         ref = P.reference(q[i], 0, tables[i], int(lens[i]))
         assert_attn_close(got[i], ref, what=f"seq {i} L={lens[i]}")
+    # the forks map the prefix blocks: with AF_KV_POOL_SHARED_BLOCKS both paths take the
+    # kernels with the default load policy, and give the same bits as above
+    shared = kv.make_pool(P.buf, AF_KV_FP16, 16, 1, NKV, HD, P.desc.total_blocks,
+                          flags=AF_KV_POOL_SHARED_BLOCKS)
+    kv.launch_paged_attention_shared_prefix(d_q, Q_DIM, shared, 0, d_root, 2048, d_t, max_blocks,
+                                            d_l, B, max_len, a, Q_DIM, NQ, ws)
+    kv.launch_paged_attention(d_q, Q_DIM, shared, 0, d_t, max_blocks, d_l, B, max_len, b, Q_DIM,
+                              NQ, ws)
+    assert np.array_equal(a.download(np.uint16), got.view(np.uint16).ravel())
+    assert np.array_equal(b.download(np.uint16), plain.view(np.uint16).ravel())
 
 
 @pytest.mark.parametrize("fp8,splits", [(False, 0), (False, 1), (False, 3), (True, 0)])
